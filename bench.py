@@ -1,0 +1,230 @@
+#!/usr/bin/env python3
+"""KHQ decode-attention benchmark (config 3: 32K context, 16 layers, batch 1).
+
+One step = one decode token through the 16 full-attention layers: per layer
+one two-region KHQ attention step (32,640 compressed tokens + 128 raw ring
+tokens, H_q 24 / H_kv 4, D 256) with uniform-random packed codes resident in
+HBM (a separate 28.7 MB payload per layer, 460 MB in total, so the 256 MB
+last-level cache cannot hold the working set).  Prints one JSON line.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu]
+
+value = microseconds per layer-step (lower is better), timed with HIP events
+over exactly K steps.  roofline = the compressed-region kernel alone, timed
+with HIP events on its launch stream, against 8 TB/s.  cpu_baseline = the
+CPU oracle (C restatement of the reference kernels, OpenMP) on one layer-step
+of the same workload on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "bonsai-mojo-1bit-optimization-t4-cuda_amd"))
+
+H_Q, H_KV, D = 24, 4, 256
+ROW_BYTES = 220
+HBM_PEAK_GBS = 8000.0
+RING = 256
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=16)
+    ap.add_argument("--ctx", type=int, default=32768)
+    ap.add_argument("--win", type=int, default=128)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--sweep", action="store_true",
+                    help="also time the reference entry points at splits 1/8/32/64")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py: this build runs on one GPU only; --gpus must be 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from khq import ops, synth
+    from khq.centroids import synthetic_layer
+
+    dev = "cuda"
+    c_len = args.ctx - args.win
+    win_len = args.win
+    scale = 1.0 / 16.0
+    layers = []
+    for l in range(args.layers):
+        lc = synthetic_layer(l, seed=1234)
+        pay = ops.Payload(c_len * H_KV, dev)
+        rows = synth.random_rows(c_len * H_KV, seed=1000 + l, device=dev)
+        for k, v in rows.items():
+            getattr(pay, k).copy_(v)
+        del rows
+        g = torch.Generator(device=dev)
+        g.manual_seed(5000 + l)
+        ring_k = torch.randn((RING, H_KV, D), generator=g, device=dev).half()
+        ring_v = torch.randn((RING, H_KV, D), generator=g, device=dev).half()
+        q = synth.q_gate(H_Q, seed=7000 + l, device=dev)
+        out = torch.empty((H_Q, D), device=dev, dtype=torch.float16)
+        layers.append(dict(lc=lc, cents=ops.Centroids(lc, dev), pay=pay, ring_k=ring_k,
+                           ring_v=ring_v, q=q, out=out))
+    torch.cuda.synchronize()
+    win_start = c_len % RING
+    stream = torch.cuda.current_stream()
+
+    def step():
+        for L in layers:
+            ops.attn_step(L["q"], L["pay"], L["cents"], L["ring_k"], L["ring_v"], L["out"],
+                          H_q=H_Q, H_kv=H_KV, c_len=c_len, win_start=win_start, win_len=win_len,
+                          ring_cap=RING, scale=scale)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_total = e0.elapsed_time(e1)
+    ms_per_step = ms_total / args.steps
+    us_layer_step = ms_per_step * 1000.0 / args.layers
+
+    # dominant kernel alone: compressed-region partials, HIP events on its stream
+    n_launch = args.steps * args.layers
+    for L in layers:
+        ops.attn_partials(L["q"], L["pay"], L["cents"], H_q=H_Q, H_kv=H_KV, c_len=c_len,
+                          scale=scale)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        for L in layers:
+            ops.attn_partials(L["q"], L["pay"], L["cents"], H_q=H_Q, H_kv=H_KV, c_len=c_len,
+                              scale=scale)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    kern_us = e0.elapsed_time(e1) * 1000.0 / n_launch
+    c_bytes = c_len * H_KV * ROW_BYTES
+    step_bytes = c_bytes + win_len * H_KV * D * 2 * 2
+    kern_gbs = c_bytes / (kern_us * 1e-6) / 1e9
+    step_gbs = step_bytes / (us_layer_step * 1e-6) / 1e9
+
+    result = {
+        "metric": "KHQ decode attn us/layer-step @32K ctx + achieved HBM GB/s (% of peak)",
+        "value": round(us_layer_step, 3),
+        "unit": "us/layer-step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded uniform-random packed codes, N(0,1) fp16 ring)",
+        "config": {
+            "workload": f"C3: {args.layers} layers x ({c_len} compressed + {win_len} raw) tokens, "
+                        f"batch 1, H_q {H_Q} / H_kv {H_KV}, D {D}, fused two-region step",
+            "ctx": args.ctx, "layers": args.layers, "c_len": c_len, "win_len": win_len,
+            "parallelism": "1 GPU",
+        },
+        "hbm_gbps": round(step_gbs, 1),
+        "hbm_pct_peak": round(100.0 * step_gbs / HBM_PEAK_GBS, 2),
+        "bytes_per_layer_step": step_bytes,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "attn_part_kernel<6> (compressed region)",
+            "achieved": round(kern_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_kernel_us": round(kern_us, 3),
+            "bytes_per_launch": c_bytes,
+        },
+    }
+
+    if args.sweep:
+        sweep = {}
+        ac = torch.empty((H_Q, D + 2), device=dev)
+        aw = torch.empty((H_Q, D + 2), device=dev)
+        ap_ = torch.empty((H_Q, 64, D + 2), device=dev)
+        for sp in (1, 8, 32, 64):
+            def ref_step():
+                for L in layers:
+                    ops.attn(L["q"], L["pay"], L["cents"], ac, c_len=c_len, H_q=H_Q, H_kv=H_KV,
+                             scale=scale, num_splits=sp, out_partial=ap_ if sp > 1 else None)
+                    ops.window_attn(L["q"], L["ring_k"], L["ring_v"], aw, win_start=win_start,
+                                    win_len=win_len, ring_cap=RING, H_q=H_Q, H_kv=H_KV,
+                                    scale=scale)
+                    ops.merge_gate(ac, aw, L["q"], L["out"], H_q=H_Q, has_w=True)
+            ref_step()
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(args.steps):
+                ref_step()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            sweep[f"splits_{sp}"] = round(e0.elapsed_time(e1) * 1000.0 / n_launch, 3)
+        result["reference_entry_us_per_layer_step"] = sweep
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(layers[0], c_len, win_len, win_start, scale,
+                                              args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline(L, c_len, win_len, win_start, scale, budget_s):
+    """Times the CPU oracle on one layer-step of the same workload (layer 0)."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    from khq.layer import split_count
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    oracle.set_num_threads(threads)
+    pay = L["pay"]
+    rows = {k: getattr(pay, k).cpu().numpy() for k in
+            ("kmask", "kpay", "knorm", "krn", "vpay", "vnorm", "vrn", "vsm")}
+    rows["kmask"] = rows["kmask"].view(np.uint32)
+    h = L["lc"].fp16()
+    q = L["q"].cpu().numpy()
+    rk, rv = L["ring_k"].cpu().numpy(), L["ring_v"].cpu().numpy()
+    n_sp = split_count(c_len, 16)  # BONSAI_KHQ_SPLITS default
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        _, ac, _ = oracle.attn(q, rows["kpay"], rows["vpay"], rows["vsm"], rows["kmask"],
+                               rows["knorm"], rows["krn"], rows["vnorm"], rows["vrn"],
+                               h["cents_k"], h["cents_v"], h["vq"], h["rotor_k"], h["rotor_v"],
+                               h["d_k"], h["d_v"], num_queries=H_Q, num_heads=H_Q, L_q=1,
+                               c_len=c_len, n_rep=H_Q // H_KV, scale=scale,
+                               alpha_k=L["lc"].alpha_k, alpha_v=L["lc"].alpha_v,
+                               rope_base=1e7, start_pos=0, num_splits=n_sp)
+        _, aw = oracle.window_attn(q, rk, rv, win_start=win_start, win_len=win_len,
+                                   ring_cap=RING, H_q=H_Q, H_kv=H_KV, scale=scale)
+        oracle.merge_gate(ac, aw, q, H_q=H_Q, has_w=True)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 50:
+            break
+    return {"value": round(el / reps * 1e6, 1), "unit": "us/layer-step", "cores": threads,
+            "kind": "port",
+            "sample": f"{reps} layer-step(s) of layer 0 at the same shape "
+                      f"({c_len} compressed + {win_len} raw, splits {n_sp}), OpenMP over "
+                      f"(query head x split)"}
+
+
+if __name__ == "__main__":
+    main()

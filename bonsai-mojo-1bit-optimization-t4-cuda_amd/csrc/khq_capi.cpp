@@ -1,0 +1,344 @@
+// khq_capi.cpp -- extern "C" boundary of libkhq_hip.so (declared in
+// include/khq.h).  Argument checks and return codes follow the reference
+// launchers of ref:src/csrc/qmv_sm75_kernel.cu:4277-4429; the work split into
+// kernels is this library's own.
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+#include <mutex>
+
+#include "khq.h"
+#include "khq_internal.h"
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_ws_mu;
+void* g_ws[kMaxDevices] = {nullptr};
+size_t g_ws_bytes[kMaxDevices] = {0};
+
+int rc_of(hipError_t e) { return e == hipSuccess ? 0 : static_cast<int>(e); }
+
+// Device workspace for split partials, grown on demand (never shrunk).
+hipError_t workspace(size_t bytes, float** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    if (g_ws_bytes[dev] < bytes) {
+        size_t want = std::max(bytes, (size_t)4 << 20);
+        if (g_ws[dev]) {
+            e = hipDeviceSynchronize();
+            if (e != hipSuccess) return e;
+            e = hipFree(g_ws[dev]);
+            if (e != hipSuccess) return e;
+            g_ws[dev] = nullptr;
+            g_ws_bytes[dev] = 0;
+        }
+        e = hipMalloc(&g_ws[dev], want);
+        if (e != hipSuccess) return e;
+        g_ws_bytes[dev] = want;
+    }
+    *out = static_cast<float*>(g_ws[dev]);
+    return hipSuccess;
+}
+
+int window_parts(int win_len) { return std::max(1, std::min(64, (win_len + 15) / 16)); }
+
+khq::AttnArgs attn_args(const void* q, const void* k_payload, const void* v_payload,
+                        const void* v_shared_meta, const void* k_mask, const void* k_norms,
+                        const void* k_r_norms, const void* v_norms, const void* v_r_norms,
+                        const void* centroids_k, const void* centroids_v,
+                        const void* vq_centroids, const void* k_rotor, const void* v_rotor,
+                        const void* d_vec_k, const void* d_vec_v) {
+    khq::AttnArgs a{};
+    a.q = static_cast<const __half*>(q);
+    a.kpay = static_cast<const uint8_t*>(k_payload);
+    a.vpay = static_cast<const uint8_t*>(v_payload);
+    a.vsm = static_cast<const uint8_t*>(v_shared_meta);
+    a.kmask = static_cast<const uint32_t*>(k_mask);
+    a.knorm = static_cast<const __half*>(k_norms);
+    a.krn = static_cast<const __half*>(k_r_norms);
+    a.vnorm = static_cast<const __half*>(v_norms);
+    a.vrn = static_cast<const __half*>(v_r_norms);
+    a.cents_k = static_cast<const __half*>(centroids_k);
+    a.cents_v = static_cast<const __half*>(centroids_v);
+    a.vq = static_cast<const __half*>(vq_centroids);
+    a.rotor_k = static_cast<const __half*>(k_rotor);
+    a.rotor_v = static_cast<const __half*>(v_rotor);
+    a.dk = static_cast<const __half*>(d_vec_k);
+    a.dv = static_cast<const __half*>(d_vec_v);
+    return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* khq_version(void) { return "khq-mi355x 0.1 (gfx950)"; }
+
+int khq_attn_parts(int c_len) {
+    if (c_len <= 0) return 0;
+    return std::max(1, std::min(256, (c_len + 31) / 32));
+}
+
+int khq_workspace_reserve(size_t bytes) {
+    float* p = nullptr;
+    return rc_of(workspace(bytes, &p));
+}
+
+int launch_khq_compress_fp16(const void* x, const void* d_vec, const void* rotor,
+                             const void* centroids, const void* vq_centroids, void* out_mask,
+                             void* out_norms, void* out_r_norms, void* out_payload,
+                             void* out_shared_meta, int n, int d, float threshold_scale,
+                             float alpha, int is_v, hipStream_t stream) {
+    if (n <= 0 || d != 256) return -100;
+    return rc_of(khq::launch_compress(
+        static_cast<const __half*>(x), static_cast<const __half*>(d_vec),
+        static_cast<const __half*>(rotor), static_cast<const __half*>(centroids),
+        static_cast<const __half*>(vq_centroids), static_cast<uint32_t*>(out_mask),
+        static_cast<__half*>(out_norms), static_cast<__half*>(out_r_norms),
+        static_cast<uint8_t*>(out_payload), static_cast<uint8_t*>(out_shared_meta), n,
+        threshold_scale, alpha, is_v ? 1 : 0, stream));
+}
+
+int launch_khq_attn_fp16(const void* q, const void* k_payload, const void* v_payload,
+                         const void* v_shared_meta, const void* k_mask, const void* k_norms,
+                         const void* k_r_norms, const void* v_norms, const void* v_r_norms,
+                         const void* centroids_k, const void* centroids_v,
+                         const void* vq_centroids, const void* k_rotor, const void* v_rotor,
+                         const void* d_vec_k, const void* d_vec_v, void* out_attn,
+                         void* out_partial, int num_queries, int num_heads, int L_q, int c_len,
+                         int stride_s, int n_rep, float scale, float alpha_k, float alpha_v,
+                         float rope_base, int start_pos, int num_splits, hipStream_t stream) {
+    (void)stride_s;
+    if (num_queries <= 0 || c_len <= 0) return -100;
+    if (num_splits < 1) num_splits = 1;
+    if (num_splits > 1 && out_partial == nullptr) return -101;
+    // Shapes this library's kernels are built for.
+    if (n_rep < 1 || n_rep > 8 || num_heads % n_rep != 0 || L_q < 1 ||
+        num_queries != num_heads * L_q)
+        return -100;
+    const int h_kv = num_heads / n_rep;
+    const int np = khq_attn_parts(L_q > 1 ? std::min(c_len, L_q) : c_len);
+    float* ws = nullptr;
+    hipError_t e = workspace((size_t)num_queries * np * 258 * sizeof(float), &ws);
+    if (e != hipSuccess) return rc_of(e);
+    khq::AttnArgs a = attn_args(q, k_payload, v_payload, v_shared_meta, k_mask, k_norms,
+                                k_r_norms, v_norms, v_r_norms, centroids_k, centroids_v,
+                                vq_centroids, k_rotor, v_rotor, d_vec_k, d_vec_v);
+    a.part = ws;
+    a.c_len = c_len;
+    a.h_kv = h_kv;
+    a.L_q = L_q;
+    a.start_pos = start_pos;
+    a.n_parts = np;
+    a.part_stride = np;
+    a.part_offset = 0;
+    a.sc = scale;
+    a.a_k = alpha_k;
+    a.a_v = alpha_v;
+    a.rope_base = rope_base;
+    e = khq::launch_attn_parts(a, n_rep, dim3(np, h_kv, L_q), stream);
+    if (e != hipSuccess) return rc_of(e);
+    return rc_of(khq::launch_lse_reduce(ws, static_cast<float*>(out_attn), num_queries, np,
+                                        stream));
+}
+
+int launch_khq_window_attn_fp16(const void* q, const void* ring_k, const void* ring_v,
+                                void* out_attn, int win_start, int win_len, int ring_cap, int H_q,
+                                int H_kv, int d, float scale, hipStream_t stream) {
+    if (H_q <= 0 || win_len <= 0) return -100;
+    if (d != 256 || H_kv <= 0 || H_q % H_kv != 0 || H_q / H_kv > 8 || ring_cap <= 0 ||
+        win_len > ring_cap || win_start < 0)
+        return -100;
+    const int np = window_parts(win_len);
+    float* ws = nullptr;
+    hipError_t e = workspace((size_t)H_q * np * 258 * sizeof(float), &ws);
+    if (e != hipSuccess) return rc_of(e);
+    khq::WinArgs w{};
+    w.q = static_cast<const __half*>(q);
+    w.ring_k = static_cast<const __half*>(ring_k);
+    w.ring_v = static_cast<const __half*>(ring_v);
+    w.part = ws;
+    w.win_start = win_start;
+    w.win_len = win_len;
+    w.ring_cap = ring_cap;
+    w.h_kv = H_kv;
+    w.n_parts = np;
+    w.part_stride = np;
+    w.part_offset = 0;
+    w.sc = scale;
+    e = khq::launch_window_parts(w, H_q / H_kv, dim3(np, H_kv), stream);
+    if (e != hipSuccess) return rc_of(e);
+    return rc_of(khq::launch_lse_reduce(ws, static_cast<float*>(out_attn), H_q, np, stream));
+}
+
+int launch_khq_gather_q_fp16(const void* q_gate, void* q_out, int H_q, int d,
+                             hipStream_t stream) {
+    if (H_q <= 0 || d <= 0) return -100;
+    return rc_of(khq::launch_gather_q(static_cast<const __half*>(q_gate),
+                                      static_cast<__half*>(q_out), H_q, d, stream));
+}
+
+int launch_khq_merge_gate_fp16(const void* attn_c, const void* attn_w, const void* q_gate,
+                               void* out, int H_q, int d, int has_w, hipStream_t stream) {
+    if (H_q <= 0 || d <= 0) return -100;
+    return rc_of(khq::launch_merge_gate(static_cast<const float*>(attn_c),
+                                        static_cast<const float*>(attn_w),
+                                        static_cast<const __half*>(q_gate),
+                                        static_cast<__half*>(out), H_q, d, has_w ? 1 : 0,
+                                        stream));
+}
+
+int launch_khq_ring_write_fp16(void* ring_k, void* ring_v, void* ring_u, const void* k_roped,
+                               const void* v, const void* k_unroped, int slot, int kv,
+                               hipStream_t stream) {
+    if (kv <= 0 || slot < 0) return -100;
+    if ((ring_k == nullptr) != (k_roped == nullptr) || (ring_v == nullptr) != (v == nullptr) ||
+        (ring_u == nullptr) != (k_unroped == nullptr))
+        return -100;
+    if (ring_k == nullptr && ring_v == nullptr && ring_u == nullptr) return -100;
+    const size_t off = (size_t)slot * kv;
+    __half* rk = ring_k ? static_cast<__half*>(ring_k) + off : nullptr;
+    __half* rv = ring_v ? static_cast<__half*>(ring_v) + off : nullptr;
+    __half* ru = ring_u ? static_cast<__half*>(ring_u) + off : nullptr;
+    return rc_of(khq::launch_ring_write(rk, rv, ru,
+                                        static_cast<const __half*>(k_roped),
+                                        static_cast<const __half*>(v),
+                                        static_cast<const __half*>(k_unroped), kv, stream));
+}
+
+int launch_khq_partial_rope_fp16(void* vec, int num_heads, int head_dim, int rotary_dim,
+                                 int pos, float theta_base, int stride, hipStream_t stream) {
+    if (num_heads <= 0 || head_dim <= 0 || rotary_dim <= 0 || rotary_dim > head_dim ||
+        (rotary_dim & 1))
+        return -100;
+    return rc_of(khq::launch_partial_rope(static_cast<__half*>(vec), num_heads, head_dim,
+                                          rotary_dim, pos, theta_base, stride, stream));
+}
+
+int launch_khq_gqa_attn_fp16(const void* q_gate, const void* k_cache, const void* v_cache,
+                             void* out, int seq_len, int H_q, int H_kv, int head_dim,
+                             float scale, hipStream_t stream) {
+    // The reference launcher refuses head_dim != 256 (tests/test_gqa_attention_gpu.mojo:183-208).
+    if (head_dim != 256 || seq_len <= 0 || H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 ||
+        H_q / H_kv > 8)
+        return -100;
+    const int np = std::max(1, std::min(256, (seq_len + 15) / 16));
+    float* ws = nullptr;
+    hipError_t e = workspace((size_t)H_q * np * 258 * sizeof(float), &ws);
+    if (e != hipSuccess) return rc_of(e);
+    khq::WinArgs w{};
+    w.q = static_cast<const __half*>(q_gate);
+    w.ring_k = static_cast<const __half*>(k_cache);
+    w.ring_v = static_cast<const __half*>(v_cache);
+    w.part = ws;
+    w.win_start = 0;
+    w.win_len = seq_len;
+    w.ring_cap = seq_len;
+    w.h_kv = H_kv;
+    w.n_parts = np;
+    w.part_stride = np;
+    w.part_offset = 0;
+    w.sc = scale;
+    e = khq::launch_window_parts(w, H_q / H_kv, dim3(np, H_kv), stream);
+    if (e != hipSuccess) return rc_of(e);
+    return rc_of(khq::launch_combine_gate(ws, static_cast<const __half*>(q_gate),
+                                          static_cast<__half*>(out), H_q, np, 1e-9f, stream));
+}
+
+int khq_attn_partials_fp16(const void* q_gate, const void* k_payload, const void* v_payload,
+                           const void* v_shared_meta, const void* k_mask, const void* k_norms,
+                           const void* k_r_norms, const void* v_norms, const void* v_r_norms,
+                           const void* centroids_k, const void* centroids_v,
+                           const void* vq_centroids, const void* k_rotor, const void* v_rotor,
+                           const void* d_vec_k, const void* d_vec_v, int H_q, int H_kv,
+                           int c_len, float scale, float alpha_k, float alpha_v,
+                           float rope_base, hipStream_t stream) {
+    if (c_len <= 0 || H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || H_q / H_kv > 8) return -100;
+    const int npc = khq_attn_parts(c_len);
+    float* ws = nullptr;
+    hipError_t e = workspace((size_t)H_q * npc * 258 * sizeof(float), &ws);
+    if (e != hipSuccess) return rc_of(e);
+    khq::AttnArgs a = attn_args(q_gate, k_payload, v_payload, v_shared_meta, k_mask, k_norms,
+                                k_r_norms, v_norms, v_r_norms, centroids_k, centroids_v,
+                                vq_centroids, k_rotor, v_rotor, d_vec_k, d_vec_v);
+    a.part = ws;
+    a.c_len = c_len;
+    a.h_kv = H_kv;
+    a.L_q = 1;
+    a.start_pos = 0;
+    a.n_parts = npc;
+    a.part_stride = npc;
+    a.part_offset = 0;
+    a.sc = scale;
+    a.a_k = alpha_k;
+    a.a_v = alpha_v;
+    a.rope_base = rope_base;
+    return rc_of(khq::launch_attn_parts(a, H_q / H_kv, dim3(npc, H_kv, 1), stream));
+}
+
+int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_payload,
+                       const void* v_shared_meta, const void* k_mask, const void* k_norms,
+                       const void* k_r_norms, const void* v_norms, const void* v_r_norms,
+                       const void* centroids_k, const void* centroids_v,
+                       const void* vq_centroids, const void* k_rotor, const void* v_rotor,
+                       const void* d_vec_k, const void* d_vec_v, const void* ring_k,
+                       const void* ring_v, void* out, int H_q, int H_kv, int c_len,
+                       int win_start, int win_len, int ring_cap, float scale, float alpha_k,
+                       float alpha_v, float rope_base, hipStream_t stream) {
+    if (c_len < 0 || win_len < 0 || (c_len == 0 && win_len == 0)) return -100;
+    if (H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || H_q / H_kv > 8) return -100;
+    if (win_len > 0 && (ring_cap <= 0 || win_len > ring_cap || win_start < 0)) return -100;
+    const int n_rep = H_q / H_kv;
+    const int npc = khq_attn_parts(c_len);
+    const int npw = win_len > 0 ? window_parts(win_len) : 0;
+    const int np = npc + npw;
+    float* ws = nullptr;
+    hipError_t e = workspace((size_t)H_q * np * 258 * sizeof(float), &ws);
+    if (e != hipSuccess) return rc_of(e);
+    if (npc > 0) {
+        khq::AttnArgs a = attn_args(q_gate, k_payload, v_payload, v_shared_meta, k_mask,
+                                    k_norms, k_r_norms, v_norms, v_r_norms, centroids_k,
+                                    centroids_v, vq_centroids, k_rotor, v_rotor, d_vec_k,
+                                    d_vec_v);
+        a.part = ws;
+        a.c_len = c_len;
+        a.h_kv = H_kv;
+        a.L_q = 1;
+        a.start_pos = 0;
+        a.n_parts = npc;
+        a.part_stride = np;
+        a.part_offset = 0;
+        a.sc = scale;
+        a.a_k = alpha_k;
+        a.a_v = alpha_v;
+        a.rope_base = rope_base;
+        e = khq::launch_attn_parts(a, n_rep, dim3(npc, H_kv, 1), stream);
+        if (e != hipSuccess) return rc_of(e);
+    }
+    if (npw > 0) {
+        khq::WinArgs w{};
+        w.q = static_cast<const __half*>(q_gate);
+        w.ring_k = static_cast<const __half*>(ring_k);
+        w.ring_v = static_cast<const __half*>(ring_v);
+        w.part = ws;
+        w.win_start = win_start;
+        w.win_len = win_len;
+        w.ring_cap = ring_cap;
+        w.h_kv = H_kv;
+        w.n_parts = npw;
+        w.part_stride = np;
+        w.part_offset = npc;
+        w.sc = scale;
+        e = khq::launch_window_parts(w, n_rep, dim3(npw, H_kv), stream);
+        if (e != hipSuccess) return rc_of(e);
+    }
+    return rc_of(khq::launch_combine_gate(ws, static_cast<const __half*>(q_gate),
+                                          static_cast<__half*>(out), H_q, np, 1e-8f, stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,64 @@
+// khq_internal.h -- kernel argument blocks and launch helpers shared by the
+// kernels (khq_kernels.hip) and the C ABI layer (khq_capi.cpp).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace khq {
+
+// Compressed-region work: token range [0, c_len) of KV head blockIdx.y cut
+// into n_parts parts; the partial triple of query qid, part i lands at
+// part[(qid * part_stride + part_offset + i) * 258].
+struct AttnArgs {
+    const __half* q;  // q_gate [H_q][512]
+    const uint8_t* kpay;
+    const uint8_t* vpay;
+    const uint8_t* vsm;
+    const uint32_t* kmask;
+    const __half* knorm;
+    const __half* krn;
+    const __half* vnorm;
+    const __half* vrn;
+    const __half* cents_k;
+    const __half* cents_v;
+    const __half* vq;
+    const __half* rotor_k;
+    const __half* rotor_v;
+    const __half* dk;
+    const __half* dv;
+    float* part;
+    int c_len, h_kv, L_q, start_pos, n_parts, part_stride, part_offset;
+    float sc, a_k, a_v, rope_base;
+};
+
+// fp16 ring-window work, same partial layout (query = head).
+struct WinArgs {
+    const __half* q;
+    const __half* ring_k;
+    const __half* ring_v;
+    float* part;
+    int win_start, win_len, ring_cap, h_kv, n_parts, part_stride, part_offset;
+    float sc;
+};
+
+hipError_t launch_compress(const __half* x, const __half* d_vec, const __half* rotor,
+                           const __half* cents, const __half* vq, uint32_t* out_mask,
+                           __half* out_norms, __half* out_rn, uint8_t* out_pay,
+                           uint8_t* out_sm, int n, float ts, float alpha, int is_v,
+                           hipStream_t st);
+hipError_t launch_attn_parts(const AttnArgs& a, int n_rep, dim3 grid, hipStream_t st);
+hipError_t launch_window_parts(const WinArgs& a, int n_rep, dim3 grid, hipStream_t st);
+hipError_t launch_lse_reduce(const float* part, float* out, int n_q, int n_parts,
+                             hipStream_t st);
+hipError_t launch_combine_gate(const float* part, const __half* q_gate, __half* out, int H_q,
+                               int n_parts, float eps, hipStream_t st);
+hipError_t launch_merge_gate(const float* ac, const float* aw, const __half* qg, __half* out,
+                             int H_q, int D, int has_w, hipStream_t st);
+hipError_t launch_gather_q(const __half* qg, __half* qo, int H_q, int D, hipStream_t st);
+hipError_t launch_ring_write(__half* rk, __half* rv, __half* ru, const __half* k,
+                             const __half* v, const __half* ku, int kv, hipStream_t st);
+hipError_t launch_partial_rope(__half* vec, int num_heads, int head_dim, int rotary_dim, int pos,
+                               float theta, int stride, hipStream_t st);
+
+}  // namespace khq

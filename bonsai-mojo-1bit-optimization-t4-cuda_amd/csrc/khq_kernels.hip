@@ -1,0 +1,807 @@
+// khq_kernels.hip -- KHQ compressed-KV decode attention for MI355X (gfx950).
+//
+// Kernels are written for 64-lane wavefronts.  The common lane mapping is
+// "lane p owns patch p": dims 4p..4p+3 of a 256-wide head, so one wavefront
+// covers one head row and the 4x4 per-patch rotors never leave a lane.
+// The 256-point Walsh-Hadamard transform is then two in-lane butterfly
+// stages followed by six cross-lane stages (lane xor 1..32).
+//
+// Compiled with -ffp-contract=off: every fused multiply-add is an explicit
+// fmaf(), so the compress kernel reproduces the CPU restatement's operation
+// sequence bit for bit.
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "khq_internal.h"
+
+namespace khq {
+
+__device__ __forceinline__ float h2f(__half h) { return __half2float(h); }
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+    const unsigned lane = threadIdx.x & 63u;
+    return lane == 0 ? 0ull : (~0ull >> (64u - lane));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+
+// Butterfly across lanes: lower lane (bit m clear) keeps a+b, upper keeps a-b
+// where a is the lower lane's value.  Same operands and order as the
+// in-place FWHT of the reference (a + b, a - b).
+__device__ __forceinline__ float xbfly(float x, int m, bool lower) {
+    float p = __shfl_xor(x, m, 64);
+    return lower ? (x + p) : (p - x);
+}
+
+// FWHT-256 on a wavefront holding 4 consecutive dims per lane.
+__device__ __forceinline__ void fwht256(float (&v)[4]) {
+    const int lane = threadIdx.x & 63;
+    float a = v[0], b = v[1];
+    v[0] = a + b; v[1] = a - b;
+    a = v[2]; b = v[3];
+    v[2] = a + b; v[3] = a - b;
+    a = v[0]; b = v[2];
+    v[0] = a + b; v[2] = a - b;
+    a = v[1]; b = v[3];
+    v[1] = a + b; v[3] = a - b;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const bool lower = (lane & m) == 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[c] = xbfly(v[c], m, lower);
+    }
+}
+
+// ---------------------------------------------------------------- compress
+// One wavefront per row, four rows per 256-thread block.  The reference
+// (ref:src/csrc/qmv_sm75_kernel.cu:1256-1467) runs one thread per row; the
+// three order-sensitive sums (sum of squares, sum_normals/sum_cbase, the V
+// energies) are kept sequential here by staging the terms in LDS and letting
+// every lane fold them in index order.
+__global__ __launch_bounds__(256) void compress_kernel(
+    const __half* __restrict__ x, const __half* __restrict__ d_vec,
+    const __half* __restrict__ rotor, const __half* __restrict__ cents,
+    const __half* __restrict__ vq, uint32_t* __restrict__ out_mask,
+    __half* __restrict__ out_norms, __half* __restrict__ out_rn,
+    uint8_t* __restrict__ out_pay, uint8_t* __restrict__ out_sm, int n, float ts,
+    float alpha, int is_v) {
+    __shared__ float s_a[4][256];
+    __shared__ float s_b[4][256];
+    __shared__ uint32_t s_w[4][32];
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + wave;
+    const bool live = row < n;
+    const float f_s = 0.0625f;
+
+    float xv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (live) {
+        const __half* xr = x + (size_t)row * 256 + lane * 4;
+#pragma unroll
+        for (int c = 0; c < 4; c++) xv[c] = h2f(xr[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) s_a[wave][lane * 4 + c] = xv[c];
+    if (lane < 32) s_w[wave][lane] = 0u;
+    __syncthreads();
+    float sum_sq = 0.0f;
+    for (int i = 0; i < 256; i += 4) {
+        float4 t = *reinterpret_cast<const float4*>(&s_a[wave][i]);
+        sum_sq = fmaf(t.x, t.x, sum_sq);
+        sum_sq = fmaf(t.y, t.y, sum_sq);
+        sum_sq = fmaf(t.z, t.z, sum_sq);
+        sum_sq = fmaf(t.w, t.w, sum_sq);
+    }
+    const float norm = sqrtf(sum_sq + 1e-8f);
+    if (live && lane == 0) out_norms[row] = __float2half(norm);
+
+    float r[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) r[c] = (xv[c] * h2f(d_vec[lane * 4 + c])) / (norm + 1e-8f);
+    fwht256(r);
+
+    float proj[4];
+    {
+        const __half* R = rotor + lane * 16;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float acc = r[0] * h2f(R[0 * 4 + c]);
+            acc = fmaf(r[1], h2f(R[1 * 4 + c]), acc);
+            acc = fmaf(r[2], h2f(R[2 * 4 + c]), acc);
+            acc = fmaf(r[3], h2f(R[3 * 4 + c]), acc);
+            proj[c] = acc * f_s;
+        }
+    }
+    __syncthreads();  // s_a reused below
+
+    if (!is_v) {
+        // ---- K branch, ref .cu:1314-1351 and :1429-1466
+        bool cand[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) cand[c] = fabsf(proj[c]) > 1.60f * f_s;
+        const uint64_t lt = lanemask_lt();
+        unsigned base = 0, total = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint64_t b = __ballot(cand[c]);
+            base += (unsigned)__popcll(b & lt);
+            total += (unsigned)__popcll(b);
+        }
+        const unsigned n_out = total < 50u ? total : 50u;
+        unsigned code[4], ord[4];
+        unsigned run = base;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            ord[c] = run;
+            float sa = 0.0f, sb = 0.0f;
+            if (cand[c]) {
+                code[c] = (run < 50u) ? 3u : (proj[c] > 0.0f ? 2u : 1u);
+                run++;
+            } else {
+                code[c] = proj[c] > 0.47f * f_s ? 2u : (proj[c] < -0.47f * f_s ? 1u : 0u);
+                if (code[c] != 0u) {
+                    sa = fabsf(proj[c]);
+                    sb = h2f(cents[2 * 256 + lane * 4 + c]);
+                }
+            }
+            s_a[wave][lane * 4 + c] = sa;
+            s_b[wave][lane * 4 + c] = sb;
+        }
+        unsigned byte = code[0] | (code[1] << 2) | (code[2] << 4) | (code[3] << 6);
+        atomicOr(&s_w[wave][16 + (lane >> 2)], byte << (8 * (lane & 3)));
+        __syncthreads();
+        float sum_normals = 0.0f, sum_cbase = 0.0f;
+        for (int i = 0; i < 256; i += 4) {
+            float4 ta = *reinterpret_cast<const float4*>(&s_a[wave][i]);
+            float4 tb = *reinterpret_cast<const float4*>(&s_b[wave][i]);
+            sum_normals += ta.x; sum_normals += ta.y; sum_normals += ta.z; sum_normals += ta.w;
+            sum_cbase += tb.x; sum_cbase += tb.y; sum_cbase += tb.z; sum_cbase += tb.w;
+        }
+        float mult = (sum_cbase > 1e-5f) ? (sum_normals / sum_cbase) : 1.0f;
+        if (mult < 0.1f || mult > 10.0f || isnan(mult)) mult = 1.0f;
+        float res[4] = {0.f, 0.f, 0.f, 0.f};
+        float my_max = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            if (code[c] == 3u) {
+                const float cb = h2f(cents[2 * 256 + lane * 4 + c]);
+                res[c] = fmaxf(0.0f, fmaf(-cb, mult, fabsf(proj[c] * ts)));
+                my_max = fmaxf(my_max, res[c]);
+            }
+        }
+        const float max_res = wave_max(my_max);
+        const float rs = (n_out > 0u) ? (fmaxf(max_res, 1e-4f) / 15.0f) : 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            if (code[c] == 3u) {
+                const unsigned j = ord[c];
+                if (rs > 0.0f) {
+                    const float r4 = roundf(res[c] / rs);
+                    const unsigned rv = (unsigned)(uint8_t)fmaxf(0.0f, fminf(15.0f, r4));
+                    const unsigned by = 4u + j / 2u;
+                    atomicOr(&s_w[wave][by >> 2], rv << (8u * (by & 3u) + 4u * (j & 1u)));
+                }
+                if (proj[c] > 0.0f) {
+                    const unsigned by = 29u + j / 8u;
+                    atomicOr(&s_w[wave][by >> 2], 1u << (8u * (by & 3u) + (j & 7u)));
+                }
+            }
+        }
+        if (lane == 0) {
+            atomicOr(&s_w[wave][0], (unsigned)(mult * 1000.0f));
+            atomicOr(&s_w[wave][9], 0x02u);
+        }
+        __syncthreads();
+        if (live) {
+            if (lane < 16) out_mask[(size_t)row * 16 + lane] = s_w[wave][16 + lane];
+            if (lane < 10)
+                reinterpret_cast<uint32_t*>(out_pay + (size_t)row * 40)[lane] = s_w[wave][lane];
+            if (lane == 0) {
+                out_rn[row] = __float2half(rs);
+                *reinterpret_cast<uint32_t*>(out_sm + (size_t)row * 4) = 0u;
+            }
+        }
+        return;
+    }
+
+    // ---- V branch, ref .cu:1353-1428: lane p owns patch p
+    const float v0 = proj[0], v1 = proj[1], v2 = proj[2], v3 = proj[3];
+    const __half* cb = vq + (size_t)lane * 768;
+    float best_d = 1e20f;
+    unsigned best = 0;
+    for (unsigned i = 0; i < 256; i++) {
+        const float d0 = fmaf(-h2f(cb[i * 3 + 0]), alpha, v0);
+        const float d1 = fmaf(-h2f(cb[i * 3 + 1]), alpha, v1);
+        const float d2 = fmaf(-h2f(cb[i * 3 + 2]), alpha, v2);
+        const float dist = fmaf(d2, d2, fmaf(d1, d1, d0 * d0));
+        if (dist < best_d) { best_d = dist; best = i; }
+    }
+    const float c0 = h2f(cb[best * 3 + 0]) * alpha;
+    const float c1 = h2f(cb[best * 3 + 1]) * alpha;
+    const float c2 = h2f(cb[best * 3 + 2]) * alpha;
+    const float te = fmaf(v2, v2, fmaf(v1, v1, v0 * v0));
+    const float ve = fmaf(c2, c2, fmaf(c1, c1, c0 * c0));
+    const float cv0 = h2f(cents[0 * 256 + lane * 4 + 3]);
+    const float cv1 = h2f(cents[1 * 256 + lane * 4 + 3]);
+    const float dd0 = fabsf(fmaf(-cv0, alpha, v3));
+    const float dd1 = fabsf(fmaf(-cv1, alpha, v3));
+    unsigned bs = 0;
+    float best_s = 1e20f;
+    if (dd0 < best_s) { best_s = dd0; bs = 0; }
+    if (dd1 < best_s) { best_s = dd1; bs = 1; }
+    const float resid = fmaf(-(bs ? cv1 : cv0), alpha, v3);
+    const float max_res = wave_max(fabsf(resid));
+    const float res_scale = fmaxf(max_res, 1e-4f);
+    const float scaled = fmaf(resid / res_scale, 7.0f, 8.0f);
+    const unsigned dump = (unsigned)fmaxf(0.0f, fminf(15.0f, roundf(scaled)));
+    const unsigned pv = (best & 0x7Fu) | ((bs & 1u) << 7) | ((dump & 0xFu) << 8);
+    const uint64_t hi = __ballot(((best >> 7) & 1u) != 0u);
+    s_a[wave][lane] = te;
+    s_b[wave][lane] = ve;
+    __shared__ uint32_t s_pv[4][64];
+    s_pv[wave][lane] = pv;
+    __syncthreads();
+    if (!live) return;
+    uint32_t* op = reinterpret_cast<uint32_t*>(out_pay + (size_t)row * 104);
+    if (lane < 8) {
+        const uint32_t* p = &s_pv[wave][lane * 8];
+        op[lane * 3 + 0] = p[0] | (p[1] << 12) | ((p[2] & 0xFFu) << 24);
+        op[lane * 3 + 1] = (p[2] >> 8) | (p[3] << 4) | (p[4] << 16) | ((p[5] & 0xFu) << 28);
+        op[lane * 3 + 2] = (p[5] >> 4) | (p[6] << 8) | (p[7] << 20);
+    } else if (lane == 8) {
+        op[24] = (uint32_t)(hi & 0xFFFFFFFFull);
+        op[25] = (uint32_t)(hi >> 32);
+    } else if (lane == 9) {
+        float st = 0.0f, sv = 0.0f;
+        for (int p = 0; p < 64; p++) { st += s_a[wave][p]; sv += s_b[wave][p]; }
+        out_rn[row] = __float2half(sqrtf(st / (sv + 1e-8f)));
+        *reinterpret_cast<float*>(out_sm + (size_t)row * 4) = max_res;
+    }
+}
+
+// ------------------------------------------------- compressed-region parts
+// One 256-thread block per (token part, KV head, query position).  Each of
+// the four wavefronts walks every fourth token of the part; per token the
+// packed K row is decoded ONCE and shared by the n_rep query heads of the
+// KV group (the reference decodes it once per query head).  V is
+// accumulated in the rotated domain and the inverse rotor + FWHT + 1/(16 d_v)
+// are applied once per part after the four wavefronts are merged.
+template <int NREP>
+__global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs a) {
+    __shared__ float s_acc[4][NREP][256];
+    __shared__ float s_ml[4][NREP][2];
+    const int wave = threadIdx.x >> 6;
+    const int p = threadIdx.x & 63;  // patch
+    const int part = blockIdx.x;
+    const int hkv = blockIdx.y;
+    const int l_idx = blockIdx.z;
+    const int s_limit = (a.L_q > 1) ? min(a.c_len, l_idx + 1) : a.c_len;
+    const int per = (s_limit + a.n_parts - 1) / a.n_parts;
+    const int lo = min(part * per, s_limit);
+    const int hi = min(lo + per, s_limit);
+
+    // per-lane constants
+    float q[NREP][4];
+#pragma unroll
+    for (int i = 0; i < NREP; i++) {
+        const int h = hkv * NREP + i;
+        const __half* qp = a.q + (size_t)h * 512 + p * 4;
+#pragma unroll
+        for (int c = 0; c < 4; c++) q[i][c] = h2f(qp[c]);
+    }
+    float rk[16];
+#pragma unroll
+    for (int t = 0; t < 16; t++) rk[t] = h2f(a.rotor_k[p * 16 + t]);
+    float cbk[4], dks[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        cbk[c] = h2f(a.cents_k[512 + p * 4 + c]);
+        dks[c] = (1.0f / 256.0f) / (h2f(a.dk[p * 4 + c]) + 1e-8f);
+    }
+    const float cv0 = h2f(a.cents_v[p * 4 + 3]) * a.a_v;
+    const float cv1 = h2f(a.cents_v[256 + p * 4 + 3]) * a.a_v;
+    const __half* vcb = a.vq + (size_t)p * 768;
+
+    // RoPE on dims 0..63 (lanes 0..15); pair (i, i+32) = lanes p, p^8
+    const bool rope_lane = p < 16;
+    float freq[4], cc[4], ss[4], stc[4], sts[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int m = (p * 4 + c) & 31;
+        freq[c] = powf(a.rope_base, -2.0f * (float)m / 64.0f);
+        stc[c] = cosf(4.0f * freq[c]);
+        sts[c] = sinf(4.0f * freq[c]);
+        cc[c] = 1.0f;
+        ss[c] = 0.0f;
+    }
+
+    float acc[NREP][4];
+    float mx[NREP], sm[NREP];
+#pragma unroll
+    for (int i = 0; i < NREP; i++) {
+        mx[i] = -1e20f;
+        sm[i] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[i][c] = 0.0f;
+    }
+
+    const uint64_t lt = lanemask_lt();
+    int since_anchor = 1 << 30;
+    for (int s = lo + wave; s < hi; s += 4) {
+        if (since_anchor >= 64) {  // exact angle every 256 tokens
+            if (rope_lane) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const float th = (float)(a.start_pos + s) * freq[c];
+                    cc[c] = cosf(th);
+                    ss[c] = sinf(th);
+                }
+            }
+            since_anchor = 0;
+        }
+        const size_t g = (size_t)s * a.h_kv + hkv;
+        // ---- K decode
+        const uint8_t* kb = a.kpay + g * 40;
+        const unsigned mword = *reinterpret_cast<const uint32_t*>(kb);
+        float mult = (float)mword / 1000.0f;
+        if (mult < 0.1f || mult > 10.0f || isnan(mult)) mult = 1.0f;
+        const float nk = h2f(a.knorm[g]);
+        const float rs = h2f(a.krn[g]);
+        const unsigned mb = reinterpret_cast<const uint8_t*>(a.kmask + g * 16)[p];
+        unsigned code[4];
+        unsigned base = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            code[c] = (mb >> (2 * c)) & 3u;
+            base += (unsigned)__popcll(__ballot(code[c] == 3u) & lt);
+        }
+        float kv[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float cbase = cbk[c] * mult;
+            float v = 0.0f;
+            if (code[c] == 3u) {
+                const unsigned j = base;
+                float sign = -1.0f, r4 = 0.0f;
+                if (j < 50u) {
+                    sign = ((kb[29 + j / 8] >> (j % 8)) & 1u) ? 1.0f : -1.0f;
+                    r4 = (float)((kb[4 + j / 2] >> ((j % 2) * 4)) & 0xFu);
+                }
+                v = sign * fmaf(r4, rs, cbase);
+                base++;
+            } else if (code[c] == 2u) {
+                v = cbase;
+            } else if (code[c] == 1u) {
+                v = -cbase;
+            }
+            kv[c] = v * a.a_k * nk;
+        }
+        float k[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float t = kv[0] * rk[c * 4 + 0];
+            t = fmaf(kv[1], rk[c * 4 + 1], t);
+            t = fmaf(kv[2], rk[c * 4 + 2], t);
+            t = fmaf(kv[3], rk[c * 4 + 3], t);
+            k[c] = t;
+        }
+        fwht256(k);
+#pragma unroll
+        for (int c = 0; c < 4; c++) k[c] *= dks[c];
+        {
+            float xo[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) xo[c] = __shfl_xor(k[c], 8, 64);
+            if (rope_lane) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    if (p < 8) k[c] = fmaf(k[c], cc[c], -(xo[c] * ss[c]));
+                    else k[c] = fmaf(xo[c], ss[c], k[c] * cc[c]);
+                    const float nc = fmaf(cc[c], stc[c], -(ss[c] * sts[c]));
+                    const float ns = fmaf(ss[c], stc[c], cc[c] * sts[c]);
+                    cc[c] = nc;
+                    ss[c] = ns;
+                }
+            }
+        }
+        since_anchor++;
+        // ---- scores for the n_rep heads of the group
+        float sc[NREP];
+#pragma unroll
+        for (int i = 0; i < NREP; i++) {
+            float t = q[i][0] * k[0];
+            t = fmaf(q[i][1], k[1], t);
+            t = fmaf(q[i][2], k[2], t);
+            t = fmaf(q[i][3], k[3], t);
+            sc[i] = wave_sum(t) * a.sc;
+        }
+        // ---- V decode (rotated domain)
+        const uint8_t* vb = a.vpay + g * 104;
+        const uint32_t* vw = reinterpret_cast<const uint32_t*>(vb);
+        const unsigned grp = (unsigned)p >> 3, sub = (unsigned)p & 7u;
+        const uint64_t w0 = vw[grp * 3 + 0], w1 = vw[grp * 3 + 1], w2 = vw[grp * 3 + 2];
+        const uint64_t low64 = (w1 << 32) | w0;
+        const uint64_t high64 = (w2 << 32) | w1;
+        const unsigned pvl = (sub < 4) ? (unsigned)((low64 >> (sub * 12)) & 0xFFFu)
+                                       : (unsigned)((high64 >> ((sub - 4) * 12 + 16)) & 0xFFFu);
+        const unsigned hw = vw[24 + (p >> 5)];
+        const unsigned vcode = (pvl & 0x7Fu) | (((hw >> (p & 31)) & 1u) << 7);
+        const unsigned d3c = (pvl >> 7) & 1u;
+        const unsigned d3d = (pvl >> 8) & 0xFu;
+        const float nv = h2f(a.vnorm[g]);
+        const float ec = h2f(a.vrn[g]);
+        const float smv = *reinterpret_cast<const float*>(a.vsm + g * 4);
+        const float pre_v = (a.a_v * nv) * ec;
+        const float pre_r = smv * nv;
+        float vv[4];
+        vv[0] = h2f(vcb[vcode * 3 + 0]) * pre_v;
+        vv[1] = h2f(vcb[vcode * 3 + 1]) * pre_v;
+        vv[2] = h2f(vcb[vcode * 3 + 2]) * pre_v;
+        vv[3] = fmaf(((float)d3d - 8.0f) / 7.0f, pre_r, (d3c ? cv1 : cv0) * nv);
+        // ---- online softmax + accumulate
+#pragma unroll
+        for (int i = 0; i < NREP; i++) {
+            float e;
+            if (sc[i] > mx[i]) {
+                const float fac = expf(mx[i] - sc[i]);
+                sm[i] = fmaf(sm[i], fac, 1.0f);
+#pragma unroll
+                for (int c = 0; c < 4; c++) acc[i][c] *= fac;
+                mx[i] = sc[i];
+                e = 1.0f;
+            } else {
+                e = expf(sc[i] - mx[i]);
+                sm[i] += e;
+            }
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[i][c] = fmaf(e, vv[c], acc[i][c]);
+        }
+    }
+
+    // ---- merge the four wavefronts
+#pragma unroll
+    for (int i = 0; i < NREP; i++) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) s_acc[wave][i][p * 4 + c] = acc[i][c];
+        if (p == 0) {
+            s_ml[wave][i][0] = mx[i];
+            s_ml[wave][i][1] = sm[i];
+        }
+    }
+    __syncthreads();
+    for (int i = wave; i < NREP; i += 4) {
+        float M = -1e20f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, s_ml[w][i][0]);
+        float den = 0.0f;
+        float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float f = expf(s_ml[w][i][0] - M);
+            den = fmaf(s_ml[w][i][1], f, den);
+#pragma unroll
+            for (int c = 0; c < 4; c++) o[c] = fmaf(s_acc[w][i][p * 4 + c], f, o[c]);
+        }
+        // inverse V rotor + FWHT + (1/16)/d_v, ref .cu:1776-1826
+        const __half* R = a.rotor_v + p * 16;
+        float t[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float u = o[0] * h2f(R[c * 4 + 0]);
+            u = fmaf(o[1], h2f(R[c * 4 + 1]), u);
+            u = fmaf(o[2], h2f(R[c * 4 + 2]), u);
+            u = fmaf(o[3], h2f(R[c * 4 + 3]), u);
+            t[c] = u;
+        }
+        fwht256(t);
+        const int h = hkv * NREP + i;
+        const int qid = h * a.L_q + l_idx;
+        float* out = a.part + ((size_t)qid * a.part_stride + a.part_offset + part) * 258;
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            out[p * 4 + c] = (t[c] * (1.0f / 16.0f)) / (h2f(a.dv[p * 4 + c]) + 1e-8f);
+        if (p == 0) {
+            out[256] = M;
+            out[257] = den;
+        }
+    }
+}
+
+// --------------------------------------------------------- fp16 window parts
+// One 256-thread block per (window part, KV head); each wavefront walks every
+// fourth slot of the part, lane p holding dims 4p..4p+3 of K and V, and the
+// n_rep heads of the group share each K/V row.
+template <int NREP>
+__global__ __launch_bounds__(256) void window_part_kernel(WinArgs a) {
+    __shared__ float s_acc[4][NREP][256];
+    __shared__ float s_ml[4][NREP][2];
+    const int wave = threadIdx.x >> 6;
+    const int p = threadIdx.x & 63;
+    const int part = blockIdx.x;
+    const int hkv = blockIdx.y;
+    const int per = (a.win_len + a.n_parts - 1) / a.n_parts;
+    const int lo = min(part * per, a.win_len);
+    const int hi = min(lo + per, a.win_len);
+    float q[NREP][4];
+#pragma unroll
+    for (int i = 0; i < NREP; i++) {
+        const __half* qp = a.q + (size_t)(hkv * NREP + i) * 512 + p * 4;
+#pragma unroll
+        for (int c = 0; c < 4; c++) q[i][c] = h2f(qp[c]);
+    }
+    float acc[NREP][4], mx[NREP], sm[NREP];
+#pragma unroll
+    for (int i = 0; i < NREP; i++) {
+        mx[i] = -1e20f;
+        sm[i] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[i][c] = 0.0f;
+    }
+    for (int s = lo + wave; s < hi; s += 4) {
+        const int slot = (a.win_start + s) % a.ring_cap;
+        const size_t off = ((size_t)slot * a.h_kv + hkv) * 256 + p * 4;
+        const uint2 kraw = *reinterpret_cast<const uint2*>(a.ring_k + off);
+        const uint2 vraw = *reinterpret_cast<const uint2*>(a.ring_v + off);
+        const __half* kh = reinterpret_cast<const __half*>(&kraw);
+        const __half* vh = reinterpret_cast<const __half*>(&vraw);
+        float k[4], v[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) { k[c] = h2f(kh[c]); v[c] = h2f(vh[c]); }
+#pragma unroll
+        for (int i = 0; i < NREP; i++) {
+            float t = q[i][0] * k[0];
+            t = fmaf(q[i][1], k[1], t);
+            t = fmaf(q[i][2], k[2], t);
+            t = fmaf(q[i][3], k[3], t);
+            const float sv = wave_sum(t) * a.sc;
+            float e;
+            if (sv > mx[i]) {
+                const float fac = expf(mx[i] - sv);
+                sm[i] = fmaf(sm[i], fac, 1.0f);
+#pragma unroll
+                for (int c = 0; c < 4; c++) acc[i][c] *= fac;
+                mx[i] = sv;
+                e = 1.0f;
+            } else {
+                e = expf(sv - mx[i]);
+                sm[i] += e;
+            }
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[i][c] = fmaf(e, v[c], acc[i][c]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NREP; i++) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) s_acc[wave][i][p * 4 + c] = acc[i][c];
+        if (p == 0) {
+            s_ml[wave][i][0] = mx[i];
+            s_ml[wave][i][1] = sm[i];
+        }
+    }
+    __syncthreads();
+    for (int i = wave; i < NREP; i += 4) {
+        float M = -1e20f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, s_ml[w][i][0]);
+        float den = 0.0f, o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float f = expf(s_ml[w][i][0] - M);
+            den = fmaf(s_ml[w][i][1], f, den);
+#pragma unroll
+            for (int c = 0; c < 4; c++) o[c] = fmaf(s_acc[w][i][p * 4 + c], f, o[c]);
+        }
+        const int h = hkv * NREP + i;
+        float* out = a.part + ((size_t)h * a.part_stride + a.part_offset + part) * 258;
+#pragma unroll
+        for (int c = 0; c < 4; c++) out[p * 4 + c] = o[c];
+        if (p == 0) {
+            out[256] = M;
+            out[257] = den;
+        }
+    }
+}
+
+// ------------------------------------------------------ logsumexp combines
+// Unnormalised merge of n_parts partial triples per query, the reduce of
+// ref .cu:1836-1877.  Each thread owns one dim; the max / denominator pass is
+// done redundantly by every thread (parts are few hundred at most).
+__global__ __launch_bounds__(256) void lse_reduce_kernel(const float* __restrict__ part,
+                                                        float* __restrict__ out,
+                                                        int n_parts) {
+    const int qid = blockIdx.x;
+    const int d = threadIdx.x;
+    const float* base = part + (size_t)qid * n_parts * 258;
+    float M = -1e20f;
+    for (int s = 0; s < n_parts; s++) M = fmaxf(M, base[(size_t)s * 258 + 256]);
+    float den = 0.0f, num = 0.0f;
+    for (int s = 0; s < n_parts; s++) {
+        const float* p = base + (size_t)s * 258;
+        const float f = expf(p[256] - M);
+        den = fmaf(p[257], f, den);
+        num = fmaf(p[d], f, num);
+    }
+    float* o = out + (size_t)qid * 258;
+    o[d] = num;
+    if (d == 0) {
+        o[256] = M;
+        o[257] = den;
+    }
+}
+
+// Final merge of all parts of one head + normalise + sigmoid gate -> f16.
+__global__ __launch_bounds__(256) void combine_gate_kernel(const float* __restrict__ part,
+                                                          const __half* __restrict__ q_gate,
+                                                          __half* __restrict__ out,
+                                                          int n_parts, float eps) {
+    const int h = blockIdx.x;
+    const int d = threadIdx.x;
+    const float* base = part + (size_t)h * n_parts * 258;
+    float M = -1e20f;
+    for (int s = 0; s < n_parts; s++) M = fmaxf(M, base[(size_t)s * 258 + 256]);
+    float den = 0.0f, num = 0.0f;
+    for (int s = 0; s < n_parts; s++) {
+        const float* p = base + (size_t)s * 258;
+        const float f = expf(p[256] - M);
+        den = fmaf(p[257], f, den);
+        num = fmaf(p[d], f, num);
+    }
+    float val = num / (den + eps);
+    const float g = h2f(q_gate[(size_t)h * 512 + 256 + d]);
+    val = val * (1.0f / (1.0f + expf(-g)));
+    out[(size_t)h * 256 + d] = __float2half(val);
+}
+
+// ref .cu:1983-2010
+__global__ void merge_gate_kernel(const float* __restrict__ attn_c,
+                                  const float* __restrict__ attn_w,
+                                  const __half* __restrict__ q_gate, __half* __restrict__ out,
+                                  int H_q, int D, int has_w) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= H_q * D) return;
+    const int h = i / D, d = i % D;
+    const float* cc = attn_c + (size_t)h * (D + 2);
+    float num = cc[d], den = cc[D + 1];
+    if (has_w) {
+        const float* cw = attn_w + (size_t)h * (D + 2);
+        const float mc = cc[D], mw = cw[D];
+        const float M = fmaxf(mc, mw);
+        const float wc = expf(mc - M), ww = expf(mw - M);
+        num = fmaf(num, wc, cw[d] * ww);
+        den = fmaf(den, wc, cw[D + 1] * ww);
+    }
+    float val = num / (den + 1e-8f);
+    const float g = h2f(q_gate[(size_t)h * 2 * D + D + d]);
+    val = val * (1.0f / (1.0f + expf(-g)));
+    out[i] = __float2half(val);
+}
+
+__global__ void gather_q_kernel(const __half* __restrict__ q_gate, __half* __restrict__ q_out,
+                                int H_q, int D) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= H_q * D) return;
+    q_out[i] = q_gate[(size_t)(i / D) * 2 * D + (i % D)];
+}
+
+__global__ void ring_write_kernel(__half* __restrict__ rk, __half* __restrict__ rv,
+                                  __half* __restrict__ ru, const __half* __restrict__ k,
+                                  const __half* __restrict__ v, const __half* __restrict__ ku,
+                                  int kv) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= kv) return;
+    if (rk) rk[i] = k[i];
+    if (rv) rv[i] = v[i];
+    if (ru) ru[i] = ku[i];
+}
+
+// ref elementwise_sm75.mojo:1023-1061 (freq = exp(log(theta) * -2i/rot))
+__global__ void partial_rope_kernel(__half* __restrict__ vec, int head_dim, int rotary_dim,
+                                    int pos, float theta, int stride) {
+    const int h = blockIdx.x;
+    const int t = threadIdx.x;
+    const int half_rot = rotary_dim / 2;
+    const int es = stride > 0 ? stride : head_dim;
+    for (int i = t; i < half_rot; i += blockDim.x) {
+        const float ex = -(float)(2 * i) / (float)rotary_dim;
+        const float fr = expf(logf(theta) * ex);
+        const float mt = (float)pos * fr;
+        const float c = cosf(mt), s = sinf(mt);
+        __half* row = vec + (size_t)h * es;
+        const float x0 = h2f(row[i]);
+        const float x1 = h2f(row[i + half_rot]);
+        row[i] = __float2half(fmaf(x0, c, -(x1 * s)));
+        row[i + half_rot] = __float2half(fmaf(x0, s, x1 * c));
+    }
+}
+
+// ------------------------------------------------------------ dispatchers
+hipError_t launch_attn_parts(const AttnArgs& a, int n_rep, dim3 grid, hipStream_t st) {
+    switch (n_rep) {
+#define KHQ_CASE(N) \
+    case N: hipLaunchKernelGGL(attn_part_kernel<N>, grid, dim3(256), 0, st, a); break;
+        KHQ_CASE(1) KHQ_CASE(2) KHQ_CASE(3) KHQ_CASE(4)
+        KHQ_CASE(5) KHQ_CASE(6) KHQ_CASE(7) KHQ_CASE(8)
+#undef KHQ_CASE
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_window_parts(const WinArgs& a, int n_rep, dim3 grid, hipStream_t st) {
+    switch (n_rep) {
+#define KHQ_CASE(N) \
+    case N: hipLaunchKernelGGL(window_part_kernel<N>, grid, dim3(256), 0, st, a); break;
+        KHQ_CASE(1) KHQ_CASE(2) KHQ_CASE(3) KHQ_CASE(4)
+        KHQ_CASE(5) KHQ_CASE(6) KHQ_CASE(7) KHQ_CASE(8)
+#undef KHQ_CASE
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_compress(const __half* x, const __half* d_vec, const __half* rotor,
+                           const __half* cents, const __half* vq, uint32_t* out_mask,
+                           __half* out_norms, __half* out_rn, uint8_t* out_pay,
+                           uint8_t* out_sm, int n, float ts, float alpha, int is_v,
+                           hipStream_t st) {
+    const int blocks = (n + 3) / 4;
+    hipLaunchKernelGGL(compress_kernel, dim3(blocks), dim3(256), 0, st, x, d_vec, rotor, cents,
+                       vq, out_mask, out_norms, out_rn, out_pay, out_sm, n, ts, alpha, is_v);
+    return hipGetLastError();
+}
+
+hipError_t launch_lse_reduce(const float* part, float* out, int n_q, int n_parts,
+                             hipStream_t st) {
+    hipLaunchKernelGGL(lse_reduce_kernel, dim3(n_q), dim3(256), 0, st, part, out, n_parts);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine_gate(const float* part, const __half* q_gate, __half* out, int H_q,
+                               int n_parts, float eps, hipStream_t st) {
+    hipLaunchKernelGGL(combine_gate_kernel, dim3(H_q), dim3(256), 0, st, part, q_gate, out,
+                       n_parts, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_merge_gate(const float* ac, const float* aw, const __half* qg, __half* out,
+                             int H_q, int D, int has_w, hipStream_t st) {
+    const int total = H_q * D;
+    hipLaunchKernelGGL(merge_gate_kernel, dim3((total + 255) / 256), dim3(256), 0, st, ac, aw,
+                       qg, out, H_q, D, has_w);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_q(const __half* qg, __half* qo, int H_q, int D, hipStream_t st) {
+    const int total = H_q * D;
+    hipLaunchKernelGGL(gather_q_kernel, dim3((total + 255) / 256), dim3(256), 0, st, qg, qo,
+                       H_q, D);
+    return hipGetLastError();
+}
+
+hipError_t launch_ring_write(__half* rk, __half* rv, __half* ru, const __half* k,
+                             const __half* v, const __half* ku, int kv, hipStream_t st) {
+    hipLaunchKernelGGL(ring_write_kernel, dim3((kv + 255) / 256), dim3(256), 0, st, rk, rv, ru,
+                       k, v, ku, kv);
+    return hipGetLastError();
+}
+
+hipError_t launch_partial_rope(__half* vec, int num_heads, int head_dim, int rotary_dim, int pos,
+                               float theta, int stride, hipStream_t st) {
+    hipLaunchKernelGGL(partial_rope_kernel, dim3(num_heads), dim3(64), 0, st, vec, head_dim,
+                       rotary_dim, pos, theta, stride);
+    return hipGetLastError();
+}
+
+}  // namespace khq

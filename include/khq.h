@@ -1,0 +1,156 @@
+/*
+ * khq.h -- C ABI of libkhq_hip.so, the MI355X (gfx950) KHQ decode-attention
+ * library.
+ *
+ * The first five entry points are drop-ins for the extern "C" launchers of
+ * oki-abrian/bonsai-mojo-1bit-optimization-t4-cuda's libbonsai_qmv_sm75.so:
+ * same names, same argument order and meaning, same return codes
+ * (0 = ok, -100 = bad shape, -101 = split-K without a partial buffer,
+ * otherwise a positive hipError_t), with hipStream_t in place of
+ * cudaStream_t.  All pointers are device pointers owned by the caller.
+ * Launches are asynchronous on `stream` (NULL = the null stream).
+ *
+ * Layouts (row r = token * H_kv + kv_head, 220 B per row in total):
+ *   k_mask  u32[r][16]   2-bit codes, dim i at word i/16 bits 2*(i%16)
+ *   k_pay   u8 [r][40]   c_base_mult*1000 (u32), 50 residual nibbles,
+ *                        50 sign bits, 0x02 marker
+ *   k_norm, k_rn  f16[r] norm, residual scale
+ *   v_pay   u8 [r][104]  64 x 12-bit patch fields + 2 words of VQ bit 7
+ *   v_norm, v_rn  f16[r] norm, energy correction
+ *   v_sm    u8 [r][4]    f32 max |dim-3 residual|
+ *   q_gate  f16[H_q][2*256]  q at 0..255, gate at 256..511 (per head)
+ *   ring_k/ring_v f16[ring_cap][H_kv][256]
+ *   out_attn f32[queries][258]  unnormalised (acc[256], max, sum_exp)
+ */
+#ifndef KHQ_H
+#define KHQ_H
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Replaces launch_khq_compress_fp16, ref:src/csrc/qmv_sm75_kernel.cu:4279-4310.
+ * Compresses n rows of x (f16 [n][256]).  is_v=0: K branch (writes mask,
+ * norms, residual scale, 40-B payload, shared meta = 0).  is_v=1: V branch
+ * (writes norms, energy, 104-B payload, shared meta = max residual; the mask
+ * is not touched).  Codes are bit-exact with the CPU restatement. */
+int launch_khq_compress_fp16(const void* x, const void* d_vec, const void* rotor,
+                             const void* centroids, const void* vq_centroids,
+                             void* out_mask, void* out_norms, void* out_r_norms,
+                             void* out_payload, void* out_shared_meta, int n, int d,
+                             float threshold_scale, float alpha, int is_v,
+                             hipStream_t stream);
+
+/* Replaces launch_khq_attn_fp16, ref:.cu:4314-4375.  Attention of
+ * num_queries = num_heads * L_q queries over compressed tokens [0, c_len),
+ * RoPE on dims 0..63 at absolute position start_pos + s.  Writes the
+ * unnormalised triple to out_attn.  num_splits keeps the reference's
+ * contract (-101 when > 1 and out_partial is NULL); the token partition used
+ * internally is the library's own and out_partial is not written, so its
+ * contents are unspecified after the call.  stride_s is unused, as in the
+ * reference. */
+int launch_khq_attn_fp16(const void* q, const void* k_payload, const void* v_payload,
+                         const void* v_shared_meta, const void* k_mask,
+                         const void* k_norms, const void* k_r_norms, const void* v_norms,
+                         const void* v_r_norms, const void* centroids_k,
+                         const void* centroids_v, const void* vq_centroids,
+                         const void* k_rotor, const void* v_rotor, const void* d_vec_k,
+                         const void* d_vec_v, void* out_attn, void* out_partial,
+                         int num_queries, int num_heads, int L_q, int c_len,
+                         int stride_s, int n_rep, float scale, float alpha_k,
+                         float alpha_v, float rope_base, int start_pos,
+                         int num_splits, hipStream_t stream);
+
+/* Replaces launch_khq_window_attn_fp16, ref:.cu:4378-4396.  fp16 attention of
+ * H_q heads over ring slots (win_start + s) % ring_cap, s < win_len (K already
+ * roped).  Unnormalised triple into out_attn f32[H_q][258].  Beyond the
+ * reference it returns -100 for d != 256, H_q % H_kv != 0, H_q/H_kv > 8 or
+ * win_len > ring_cap instead of reading stale slots. */
+int launch_khq_window_attn_fp16(const void* q, const void* ring_k, const void* ring_v,
+                                void* out_attn, int win_start, int win_len, int ring_cap,
+                                int H_q, int H_kv, int d, float scale, hipStream_t stream);
+
+/* Replaces launch_khq_gather_q_fp16, ref:.cu:4399-4411. */
+int launch_khq_gather_q_fp16(const void* q_gate, void* q_out, int H_q, int d,
+                             hipStream_t stream);
+
+/* Replaces launch_khq_merge_gate_fp16, ref:.cu:4414-4429.  Logsumexp merge of
+ * the compressed and window triples (has_w = 0: attn_c only), divide by
+ * (den + 1e-8), times sigmoid(gate), f16 out [H_q][d]. */
+int launch_khq_merge_gate_fp16(const void* attn_c, const void* attn_w, const void* q_gate,
+                               void* out, int H_q, int d, int has_w, hipStream_t stream);
+
+/* ---- helpers the reference implements as Mojo GPU kernels ---- */
+
+/* Replaces khq_ring_dual_sm75_gpu + copy_vec_sm75_gpu
+ * (ref:src/kernels/elementwise_sm75.mojo:277-312, called from
+ * ref:src/khq/runtime.mojo:432-451,486-488): one launch copies one token's
+ * roped K, V and unroped K into ring slot `slot` of ring_k, ring_v, ring_u.
+ * Any of the three (destination, source) pairs may be (NULL, NULL), not all.
+ * kv = H_kv * 256 halves per tensor. */
+int launch_khq_ring_write_fp16(void* ring_k, void* ring_v, void* ring_u,
+                               const void* k_roped, const void* v, const void* k_unroped,
+                               int slot, int kv, hipStream_t stream);
+
+/* Replaces partial_rope_sm75_gpu (ref:elementwise_sm75.mojo:1023-1061):
+ * half-split RoPE on dims 0..rotary_dim-1 of each head, in place, heads
+ * `stride` halves apart (0 = head_dim). */
+int launch_khq_partial_rope_fp16(void* vec, int num_heads, int head_dim, int rotary_dim,
+                                 int pos, float theta_base, int stride, hipStream_t stream);
+
+/* Replaces gqa_attention_sm75_gpu (ref:elementwise_sm75.mojo:1091-1231), the
+ * uncompressed fp16 baseline: GQA softmax attention of q_gate over
+ * k_cache/v_cache f16 [seq][H_kv][256] (positions 0..seq_len-1), softmax
+ * denominator Z + 1e-9, times sigmoid(gate), f16 out [H_q][256]. */
+int launch_khq_gqa_attn_fp16(const void* q_gate, const void* k_cache, const void* v_cache,
+                             void* out, int seq_len, int H_q, int H_kv, int head_dim,
+                             float scale, hipStream_t stream);
+
+/* ---- fused layer step (no reference counterpart: the reference issues
+ * launch_khq_attn_fp16 + launch_khq_window_attn_fp16 +
+ * launch_khq_merge_gate_fp16 from ref:src/khq/runtime.mojo:554-613) ----
+ * Both regions in one pass: compressed tokens [0, c_len) (c_len may be 0) and
+ * ring window slots (win_start + s) % ring_cap, s < win_len (win_len may be
+ * 0), merged by logsumexp, divided by (den + 1e-8), gated, f16 out [H_q][256].
+ * Returns -100 if both regions are empty. */
+int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_payload,
+                       const void* v_shared_meta, const void* k_mask, const void* k_norms,
+                       const void* k_r_norms, const void* v_norms, const void* v_r_norms,
+                       const void* centroids_k, const void* centroids_v,
+                       const void* vq_centroids, const void* k_rotor, const void* v_rotor,
+                       const void* d_vec_k, const void* d_vec_v, const void* ring_k,
+                       const void* ring_v, void* out, int H_q, int H_kv, int c_len,
+                       int win_start, int win_len, int ring_cap, float scale,
+                       float alpha_k, float alpha_v, float rope_base, hipStream_t stream);
+
+/* Profiling entry (no reference counterpart): launches only the
+ * compressed-region kernel of khq_attn_step_fp16 (partials into the library
+ * workspace, nothing merged), so its duration can be timed on its own. */
+int khq_attn_partials_fp16(const void* q_gate, const void* k_payload, const void* v_payload,
+                           const void* v_shared_meta, const void* k_mask, const void* k_norms,
+                           const void* k_r_norms, const void* v_norms, const void* v_r_norms,
+                           const void* centroids_k, const void* centroids_v,
+                           const void* vq_centroids, const void* k_rotor, const void* v_rotor,
+                           const void* d_vec_k, const void* d_vec_v, int H_q, int H_kv,
+                           int c_len, float scale, float alpha_k, float alpha_v,
+                           float rope_base, hipStream_t stream);
+
+/* Number of compressed-region token parts the library uses for c_len
+ * (exposed for tests and the benchmark). */
+int khq_attn_parts(int c_len);
+
+/* Grows the library's device workspace (split partials) to at least `bytes`
+ * on the current device.  Every launcher grows it on demand; call this first
+ * when the launches will be captured into a HIP graph. */
+int khq_workspace_reserve(size_t bytes);
+
+/* Library version string. */
+const char* khq_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KHQ_H */

@@ -1,0 +1,290 @@
+"""GPU parity: libkhq_hip.so (through its C ABI) against the C oracle.
+
+Bars: packed codes / masks / norms bit-exact; attention outputs within
+max-abs 2e-3 and rel 1e-3 of the oracle's fp32 result (normalised acc, and the
+logsumexp of each triple within 1e-3).
+"""
+import numpy as np
+import pytest
+import torch
+
+import npref
+import oracle
+from khq import ops, synth
+from khq.centroids import synthetic_layer
+from khqdata import (D, H_KV, H_Q, N_REP, SCALE, THETA, layer_consts, oracle_attn,
+                     oracle_window, random_rows_np, two_region_state)
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-3
+
+
+def t(a, device="cuda"):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def close(got, want, atol=ATOL, rtol=RTOL):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    err = np.abs(got - want)
+    assert err.max() <= atol, f"max abs err {err.max():.3e}"
+    rel = err.max() / max(np.abs(want).max(), 1e-30)
+    assert rel <= rtol, f"rel err {rel:.3e}"
+
+
+def check_triple(got, want):
+    g, gl = npref.triple_to_out(got)
+    w, wl = npref.triple_to_out(want)
+    close(g, w)
+    assert np.abs(gl - wl).max() <= 1e-3
+
+
+def payload_from_rows(rows, n_rows, device="cuda"):
+    pay = ops.Payload(n_rows, device)
+    pay.kmask.copy_(t(rows["kmask"].view(np.int32)))
+    for k in ("kpay", "knorm", "krn", "vpay", "vnorm", "vrn", "vsm"):
+        getattr(pay, k).copy_(t(rows[k]))
+    return pay
+
+
+def cents_dev(lc, device="cuda"):
+    return ops.Centroids(lc, device)
+
+
+# ------------------------------------------------------------------ compress
+@pytest.mark.parametrize("n", [1, 5, 512, 1001])
+def test_compress_bitexact(device, n):
+    lc, h = layer_consts()
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal((n, D)).astype(np.float16)
+    x[0] = 0  # zero row edge case
+    if n > 4:  # rows with many outliers (cap 50 hit)
+        x[1:3] *= np.float16(0)
+        x[1, ::3] = 40.0
+        x[2, :] = np.float16(1e-3)
+        x[2, 7] = 30000.0
+    cents = cents_dev(lc, device)
+    pay = ops.Payload(n, device)
+    xt = t(x)
+    ops.compress(xt, cents, pay, 0, is_v=False)
+    ops.compress(xt, cents, pay, 0, is_v=True)
+    torch.cuda.synchronize()
+    rc, kmask, knorm, krn, kpay, ksm = oracle.compress(x, h["d_k"], h["rotor_k"], h["cents_k"],
+                                                       h["cents_k"], ts=lc.ts_k, alpha=lc.alpha_k,
+                                                       is_v=False)
+    rc, _, vnorm, vrn, vpay, vsm = oracle.compress(x, h["d_v"], h["rotor_v"], h["cents_v"],
+                                                   h["vq"], ts=lc.ts_v, alpha=lc.alpha_v,
+                                                   is_v=True)
+    g = lambda a: a.cpu().numpy()
+    assert np.array_equal(g(pay.kmask).view(np.uint32), kmask)
+    assert np.array_equal(g(pay.kpay), kpay)
+    assert np.array_equal(g(pay.knorm).view(np.uint16), knorm.view(np.uint16))
+    assert np.array_equal(g(pay.krn).view(np.uint16), krn.view(np.uint16))
+    assert np.array_equal(g(pay.vpay), vpay)
+    assert np.array_equal(g(pay.vnorm).view(np.uint16), vnorm.view(np.uint16))
+    assert np.array_equal(g(pay.vrn).view(np.uint16), vrn.view(np.uint16))
+    assert np.array_equal(g(pay.vsm), vsm)  # V writes max residual after K wrote 0
+
+
+def test_compress_bitexact_scaled_codebook(device):
+    # alpha_v = 1/16 puts the codebook at the projection scale: real VQ decisions
+    lc, h = layer_consts(alpha_v=1.0 / 16.0, ts_k=1.3)
+    rng = np.random.default_rng(99)
+    x = rng.standard_normal((256, D)).astype(np.float16)
+    cents = cents_dev(lc, device)
+    pay = ops.Payload(256, device)
+    ops.compress(t(x), cents, pay, 0, is_v=False)
+    ops.compress(t(x), cents, pay, 0, is_v=True)
+    rc, kmask, _, krn, kpay, _ = oracle.compress(x, h["d_k"], h["rotor_k"], h["cents_k"],
+                                                 h["cents_k"], ts=1.3, alpha=1.0, is_v=False)
+    rc, _, _, vrn, vpay, vsm = oracle.compress(x, h["d_v"], h["rotor_v"], h["cents_v"], h["vq"],
+                                               ts=1.95, alpha=1.0 / 16.0, is_v=True)
+    assert np.array_equal(pay.kmask.cpu().numpy().view(np.uint32), kmask)
+    assert np.array_equal(pay.kpay.cpu().numpy(), kpay)
+    assert np.array_equal(pay.vpay.cpu().numpy(), vpay)
+    assert np.array_equal(pay.vsm.cpu().numpy(), vsm)
+    assert np.array_equal(pay.vrn.cpu().numpy().view(np.uint16), vrn.view(np.uint16))
+
+
+def test_compress_error_codes(device):
+    lib = __import__("khq._lib", fromlist=["lib"])
+    rc = lib.call("launch_khq_compress_fp16", *([None] * 10), 0, 256, 1.0, 1.0, 0, None,
+                  check=False)
+    assert rc == -100
+    rc = lib.call("launch_khq_compress_fp16", *([None] * 10), 4, 128, 1.0, 1.0, 0, None,
+                  check=False)
+    assert rc == -100
+
+
+# ----------------------------------------------------------------- attention
+def _gpu_state(st, device="cuda"):
+    n_rows = st["rows"]["kmask"].shape[0]
+    return payload_from_rows(st["rows"], n_rows, device), cents_dev(st["lc"], device)
+
+
+@pytest.mark.parametrize("splits", [1, 8])
+def test_attn_c2(device, splits):
+    st = two_region_state(seed=21)
+    pay, cents = _gpu_state(st)
+    out = torch.zeros((H_Q, D + 2), device=device)
+    part = torch.zeros((H_Q, splits, D + 2), device=device)
+    ops.attn(t(st["q_gate"]), pay, cents, out, c_len=st["c_len"], H_q=H_Q, H_kv=H_KV,
+             scale=SCALE, num_splits=splits, out_partial=part if splits > 1 else None)
+    torch.cuda.synchronize()
+    rc, want, _ = oracle_attn(st, num_splits=splits)
+    check_triple(out.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("c_len", [1, 7, 255, 256, 257, 1000])
+def test_attn_random_rows(device, c_len):
+    lc, h = layer_consts()
+    rows = random_rows_np(c_len * H_KV, seed=c_len)
+    q = np.random.default_rng(c_len).standard_normal((H_Q, 2 * D)).astype(np.float16)
+    st = dict(rows=rows, h=h, lc=lc, q_gate=q, c_len=c_len)
+    pay = payload_from_rows(rows, c_len * H_KV, device)
+    out = torch.zeros((H_Q, D + 2), device=device)
+    ops.attn(t(q), pay, cents_dev(lc, device), out, c_len=c_len, H_q=H_Q, H_kv=H_KV,
+             scale=SCALE)
+    torch.cuda.synchronize()
+    check_triple(out.cpu().numpy(), oracle_attn(st)[1])
+
+
+def test_attn_lq_start_pos(device):
+    st = two_region_state(seed=22)
+    pay, cents = _gpu_state(st)
+    out = torch.zeros((H_Q * 3, D + 2), device=device)
+    ops.attn(t(st["q_gate"]), pay, cents, out, c_len=300, H_q=H_Q, H_kv=H_KV, scale=SCALE,
+             L_q=3, start_pos=11)
+    torch.cuda.synchronize()
+    rc, want, _ = oracle_attn(st, c_len=300, L_q=3, start_pos=11)
+    check_triple(out.cpu().numpy(), want)
+
+
+def test_attn_error_codes(device):
+    st = two_region_state(seed=23)
+    pay, cents = _gpu_state(st)
+    out = torch.zeros((H_Q, D + 2), device=device)
+    q = t(st["q_gate"])
+    assert ops.attn(q, pay, cents, out, c_len=0, H_q=H_Q, H_kv=H_KV, scale=SCALE,
+                    check=False) == -100
+    assert ops.attn(q, pay, cents, out, c_len=10, H_q=H_Q, H_kv=H_KV, scale=SCALE, num_splits=4,
+                    out_partial=None, check=False) == -101
+
+
+def test_window_and_merge(device):
+    st = two_region_state(seed=24)
+    pay, cents = _gpu_state(st)
+    q = t(st["q_gate"])
+    ac = torch.zeros((H_Q, D + 2), device=device)
+    aw = torch.zeros((H_Q, D + 2), device=device)
+    out = torch.zeros((H_Q, D), device=device, dtype=torch.float16)
+    ops.attn(q, pay, cents, ac, c_len=st["c_len"], H_q=H_Q, H_kv=H_KV, scale=SCALE)
+    ops.window_attn(q, t(st["ring_k"]), t(st["ring_v"]), aw, win_start=st["win_start"],
+                    win_len=st["win_len"], ring_cap=256, H_q=H_Q, H_kv=H_KV, scale=SCALE)
+    ops.merge_gate(ac, aw, q, out, H_q=H_Q, has_w=True)
+    torch.cuda.synchronize()
+    rc, wc, _ = oracle_attn(st)
+    rc, ww = oracle_window(st)
+    check_triple(aw.cpu().numpy(), ww)
+    rc, want = oracle.merge_gate(wc, ww, st["q_gate"], H_q=H_Q, has_w=True)
+    close(out.cpu().numpy(), want)
+    # merge kernel alone on the oracle's triples (isolates the merge)
+    out2 = torch.zeros_like(out)
+    ops.merge_gate(t(wc), t(ww), q, out2, H_q=H_Q, has_w=True)
+    torch.cuda.synchronize()
+    close(out2.cpu().numpy(), want, atol=1e-3)
+    # fused two-region step
+    out3 = torch.zeros_like(out)
+    ops.attn_step(q, pay, cents, t(st["ring_k"]), t(st["ring_v"]), out3, H_q=H_Q, H_kv=H_KV,
+                  c_len=st["c_len"], win_start=st["win_start"], win_len=st["win_len"],
+                  ring_cap=256, scale=SCALE)
+    torch.cuda.synchronize()
+    close(out3.cpu().numpy(), want)
+
+
+def test_window_wrap_and_guards(device):
+    st = two_region_state(seed=25, n_tokens=600, boundary=384)
+    st["win_start"], st["win_len"] = 384 % 256, 216
+    q = t(st["q_gate"])
+    aw = torch.zeros((H_Q, D + 2), device=device)
+    ops.window_attn(q, t(st["ring_k"]), t(st["ring_v"]), aw, win_start=128, win_len=216,
+                    ring_cap=256, H_q=H_Q, H_kv=H_KV, scale=SCALE)
+    torch.cuda.synchronize()
+    check_triple(aw.cpu().numpy(), oracle_window(st)[1])
+    rk, rv = t(st["ring_k"]), t(st["ring_v"])
+    assert ops.window_attn(q, rk, rv, aw, win_start=0, win_len=0, ring_cap=256, H_q=H_Q,
+                           H_kv=H_KV, scale=SCALE, check=False) == -100
+    assert ops.window_attn(q, rk, rv, aw, win_start=0, win_len=257, ring_cap=256, H_q=H_Q,
+                           H_kv=H_KV, scale=SCALE, check=False) == -100
+
+
+def test_gather_q_bitexact(device):
+    q = np.random.default_rng(1).standard_normal((H_Q, 2 * D)).astype(np.float16)
+    out = torch.zeros((H_Q, D), device=device, dtype=torch.float16)
+    ops.gather_q(t(q), out, H_q=H_Q)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), q[:, :D])
+
+
+def test_c3_full_size(device):
+    """Config 3 at its real shape: 32,640 compressed + 128 raw, vs the oracle."""
+    lc, h = layer_consts(layer_id=0)
+    c_len, win = 32640, 128
+    rows = random_rows_np(c_len * H_KV, seed=3)
+    q = np.random.default_rng(4).standard_normal((H_Q, 2 * D)).astype(np.float16)
+    st = dict(rows=rows, h=h, lc=lc, q_gate=q, c_len=c_len)
+    pay = payload_from_rows(rows, c_len * H_KV, device)
+    cents = cents_dev(lc, device)
+    out = torch.zeros((H_Q, D + 2), device=device)
+    ops.attn(t(q), pay, cents, out, c_len=c_len, H_q=H_Q, H_kv=H_KV, scale=SCALE)
+    torch.cuda.synchronize()
+    rc, want, _ = oracle_attn(st, num_splits=32)
+    check_triple(out.cpu().numpy(), want)
+    # splits do not change the library's result (its partition is its own)
+    out8 = torch.zeros_like(out)
+    part = torch.zeros((H_Q, 64, D + 2), device=device)
+    ops.attn(t(q), pay, cents, out8, c_len=c_len, H_q=H_Q, H_kv=H_KV, scale=SCALE,
+             num_splits=64, out_partial=part)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out8)
+    # determinism: same inputs, identical bits
+    out_b = torch.zeros_like(out)
+    ops.attn(t(q), pay, cents, out_b, c_len=c_len, H_q=H_Q, H_kv=H_KV, scale=SCALE)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_b)
+
+
+def test_gqa_baseline_reference_cases(device):
+    from test_oracle_pins import _modular_inputs, gqa_fp64
+
+    for H_q, H_kv, seq, max_seq in [(24, 4, 8, 16), (4, 2, 16, 16), (4, 2, 1, 16), (24, 4, 512, 512)]:
+        qg, k, v = _modular_inputs(H_q, H_kv, 256, max_seq)
+        qg16, k16, v16 = (a.astype(np.float16) for a in (qg, k, v))
+        out = torch.zeros((H_q, D), device=device, dtype=torch.float16)
+        ops.gqa_attn(t(qg16.reshape(H_q, 512)), t(k16.reshape(max_seq, H_kv, D)),
+                     t(v16.reshape(max_seq, H_kv, D)), out, seq_len=seq, H_q=H_q, H_kv=H_kv,
+                     scale=1.0 / 16.0)
+        torch.cuda.synchronize()
+        want = gqa_fp64(qg16.astype(np.float64), k16.astype(np.float64),
+                        v16.astype(np.float64), seq, H_q, H_kv, 256, 1.0 / 16.0)
+        got = out.cpu().numpy().astype(np.float64).ravel()
+        assert np.abs(got - want).max() / np.abs(want).max() <= 2e-3
+    # the guard of ref tests/test_gqa_attention_gpu.mojo:183-208: head_dim != 256 refused
+    assert ops.gqa_attn(t(qg16.reshape(H_q, 512)), t(k16.reshape(max_seq, H_kv, D)),
+                        t(v16.reshape(max_seq, H_kv, D)), out, seq_len=4, H_q=4, H_kv=2,
+                        head_dim=128, scale=0.1, check=False) == -100
+
+
+def test_partial_rope_matches_oracle(device):
+    H = 24
+    j = np.arange(H * 512)
+    x = (((j * 7919 + 1013) % 2000).astype(np.float32) * 0.002 - 2.0).astype(np.float16)
+    for pos in (0, 511, 8191):
+        xt = t(x.reshape(H, 512).copy())
+        ops.partial_rope(xt, num_heads=H, pos=pos, stride=512)
+        torch.cuda.synchronize()
+        want = oracle.partial_rope_fp16(x.reshape(H, 512), num_heads=H, head_dim=256,
+                                        rotary_dim=64, pos=pos, theta=1e7, stride=512)
+        got = xt.cpu().numpy()
+        assert np.abs(got.astype(np.float32) - want.astype(np.float32)).max() <= 2e-3
+        assert np.array_equal(got[:, 64:], want[:, 64:])
