@@ -45,7 +45,39 @@ hipError_t workspace(size_t bytes, float** out) {
     return hipSuccess;
 }
 
-int window_parts(int win_len) { return std::max(1, std::min(64, (win_len + 15) / 16)); }
+// 0 = automatic (matrix-core kernel for the 24/4/256 shape), 1 = portable
+// lane-per-patch kernel for every shape.
+int g_kernel_choice = 0;
+
+bool use_mfma(int n_rep, int h_kv, int L_q) {
+    return g_kernel_choice == 0 && n_rep == 6 && h_kv == 4 && L_q == 1;
+}
+
+// Launches the compressed-region partials of query heads into part
+// (stride part_stride, first index part_offset); returns the part count used.
+hipError_t launch_compressed(khq::AttnArgs a, int n_rep, int L_q, int* parts_used,
+                             hipStream_t stream) {
+    if (use_mfma(n_rep, a.h_kv, L_q)) {
+        int n_chunks = 0;
+        const int per = khq::attn_mfma_tiles_per_chunk(a.c_len, &n_chunks);
+        *parts_used = n_chunks;
+        return khq::launch_attn_mfma(a, per, n_chunks, stream);
+    }
+    *parts_used = a.n_parts;
+    return khq::launch_attn_parts(a, n_rep, dim3(a.n_parts, a.h_kv, L_q), stream);
+}
+
+int compressed_parts(int c_len, int n_rep, int h_kv, int L_q) {
+    if (c_len <= 0) return 0;
+    if (use_mfma(n_rep, h_kv, L_q)) {
+        int n_chunks = 0;
+        khq::attn_mfma_tiles_per_chunk(c_len, &n_chunks);
+        return n_chunks;
+    }
+    return std::max(1, std::min(256, (c_len + 31) / 32));
+}
+
+int window_parts(int win_len) { return std::max(1, std::min(64, (win_len + 3) / 4)); }
 
 khq::AttnArgs attn_args(const void* q, const void* k_payload, const void* v_payload,
                         const void* v_shared_meta, const void* k_mask, const void* k_norms,
@@ -79,9 +111,12 @@ extern "C" {
 
 const char* khq_version(void) { return "khq-mi355x 0.1 (gfx950)"; }
 
-int khq_attn_parts(int c_len) {
-    if (c_len <= 0) return 0;
-    return std::max(1, std::min(256, (c_len + 31) / 32));
+int khq_attn_parts(int c_len) { return compressed_parts(c_len, 6, 4, 1); }
+
+int khq_select_kernel(int which) {
+    if (which < 0 || which > 1) return -100;
+    g_kernel_choice = which;
+    return 0;
 }
 
 int khq_workspace_reserve(size_t bytes) {
@@ -122,7 +157,7 @@ int launch_khq_attn_fp16(const void* q, const void* k_payload, const void* v_pay
         num_queries != num_heads * L_q)
         return -100;
     const int h_kv = num_heads / n_rep;
-    const int np = khq_attn_parts(L_q > 1 ? std::min(c_len, L_q) : c_len);
+    const int np = compressed_parts(L_q > 1 ? std::min(c_len, L_q) : c_len, n_rep, h_kv, L_q);
     float* ws = nullptr;
     hipError_t e = workspace((size_t)num_queries * np * 258 * sizeof(float), &ws);
     if (e != hipSuccess) return rc_of(e);
@@ -141,7 +176,8 @@ int launch_khq_attn_fp16(const void* q, const void* k_payload, const void* v_pay
     a.a_k = alpha_k;
     a.a_v = alpha_v;
     a.rope_base = rope_base;
-    e = khq::launch_attn_parts(a, n_rep, dim3(np, h_kv, L_q), stream);
+    int used = 0;
+    e = launch_compressed(a, n_rep, L_q, &used, stream);
     if (e != hipSuccess) return rc_of(e);
     return rc_of(khq::launch_lse_reduce(ws, static_cast<float*>(out_attn), num_queries, np,
                                         stream));
@@ -259,7 +295,7 @@ int khq_attn_partials_fp16(const void* q_gate, const void* k_payload, const void
                            int c_len, float scale, float alpha_k, float alpha_v,
                            float rope_base, hipStream_t stream) {
     if (c_len <= 0 || H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || H_q / H_kv > 8) return -100;
-    const int npc = khq_attn_parts(c_len);
+    const int npc = compressed_parts(c_len, H_q / H_kv, H_kv, 1);
     float* ws = nullptr;
     hipError_t e = workspace((size_t)H_q * npc * 258 * sizeof(float), &ws);
     if (e != hipSuccess) return rc_of(e);
@@ -278,7 +314,8 @@ int khq_attn_partials_fp16(const void* q_gate, const void* k_payload, const void
     a.a_k = alpha_k;
     a.a_v = alpha_v;
     a.rope_base = rope_base;
-    return rc_of(khq::launch_attn_parts(a, H_q / H_kv, dim3(npc, H_kv, 1), stream));
+    int used = 0;
+    return rc_of(launch_compressed(a, H_q / H_kv, 1, &used, stream));
 }
 
 int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_payload,
@@ -294,7 +331,7 @@ int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_
     if (H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || H_q / H_kv > 8) return -100;
     if (win_len > 0 && (ring_cap <= 0 || win_len > ring_cap || win_start < 0)) return -100;
     const int n_rep = H_q / H_kv;
-    const int npc = khq_attn_parts(c_len);
+    const int npc = compressed_parts(c_len, n_rep, H_kv, 1);
     const int npw = win_len > 0 ? window_parts(win_len) : 0;
     const int np = npc + npw;
     float* ws = nullptr;
@@ -317,7 +354,8 @@ int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_
         a.a_k = alpha_k;
         a.a_v = alpha_v;
         a.rope_base = rope_base;
-        e = khq::launch_attn_parts(a, n_rep, dim3(npc, H_kv, 1), stream);
+        int used = 0;
+        e = launch_compressed(a, n_rep, 1, &used, stream);
         if (e != hipSuccess) return rc_of(e);
     }
     if (npw > 0) {

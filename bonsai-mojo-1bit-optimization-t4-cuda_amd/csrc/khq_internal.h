@@ -61,4 +61,11 @@ hipError_t launch_ring_write(__half* rk, __half* rv, __half* ru, const __half* k
 hipError_t launch_partial_rope(__half* vec, int num_heads, int head_dim, int rotary_dim, int pos,
                                float theta, int stride, hipStream_t st);
 
+// MFMA compressed-region kernel (H_kv = 4, n_rep = 6, L_q = 1): one block per
+// chunk of tiles_per_chunk 16-token tiles; partial index = part_offset + chunk.
+size_t attn_mfma_smem_bytes();
+int attn_mfma_tiles_per_chunk(int c_len, int* n_chunks);
+hipError_t launch_attn_mfma(const AttnArgs& a, int tiles_per_chunk, int n_chunks,
+                            hipStream_t st);
+
 }  // namespace khq

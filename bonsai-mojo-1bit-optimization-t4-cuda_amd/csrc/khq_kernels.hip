@@ -615,27 +615,70 @@ __global__ __launch_bounds__(256) void window_part_kernel(WinArgs a) {
 }
 
 // ------------------------------------------------------ logsumexp combines
-// Unnormalised merge of n_parts partial triples per query, the reduce of
-// ref .cu:1836-1877.  Each thread owns one dim; the max / denominator pass is
-// done redundantly by every thread (parts are few hundred at most).
+// Unnormalised merge of n_parts partial triples per query (the reduce of
+// ref .cu:1836-1877).  Block (query, 64-dim slice): the 256 threads first
+// find the maximum and the per-part weights exp(m_s - M) cooperatively
+// (weights kept in LDS), then 4 groups of 64 threads sum disjoint part
+// ranges for the 64 dims and the groups are added in LDS.
+constexpr int kMaxParts = 4096;
+
+__device__ __forceinline__ void lse_weights(const float* base, int n_parts, float* s_w,
+                                            float* s_red, float& M, float& den) {
+    const int t = threadIdx.x;
+    float m = -1e20f;
+    for (int s = t; s < n_parts; s += 256) m = fmaxf(m, base[(size_t)s * 258 + 256]);
+    m = wave_max(m);
+    if ((t & 63) == 0) s_red[t >> 6] = m;
+    __syncthreads();
+    M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    __syncthreads();
+    float dsum = 0.0f;
+    for (int s = t; s < n_parts; s += 256) {
+        const float wgt = expf(base[(size_t)s * 258 + 256] - M);
+        s_w[s] = wgt;
+        dsum = fmaf(base[(size_t)s * 258 + 257], wgt, dsum);
+    }
+    dsum = wave_sum(dsum);
+    if ((t & 63) == 0) s_red[4 + (t >> 6)] = dsum;
+    __syncthreads();
+    den = (s_red[4] + s_red[5]) + (s_red[6] + s_red[7]);
+}
+
+__device__ __forceinline__ float lse_num(const float* base, int n_parts, const float* s_w,
+                                         float* s_acc, int d0) {
+    const int t = threadIdx.x;
+    const int d = d0 + (t & 63);
+    const int grp = t >> 6;
+    // 8 independent chains so the loads of consecutive parts overlap
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int s = grp;
+    for (; s + 28 < n_parts; s += 32) {
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            acc[u] = fmaf(base[(size_t)(s + 4 * u) * 258 + d], s_w[s + 4 * u], acc[u]);
+    }
+    for (; s < n_parts; s += 4) acc[0] = fmaf(base[(size_t)s * 258 + d], s_w[s], acc[0]);
+    const float num = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+    s_acc[t] = num;
+    __syncthreads();
+    return (s_acc[t & 63] + s_acc[64 + (t & 63)]) + (s_acc[128 + (t & 63)] + s_acc[192 + (t & 63)]);
+}
+
 __global__ __launch_bounds__(256) void lse_reduce_kernel(const float* __restrict__ part,
                                                         float* __restrict__ out,
                                                         int n_parts) {
+    __shared__ float s_w[kMaxParts];
+    __shared__ float s_red[8];
+    __shared__ float s_acc[256];
     const int qid = blockIdx.x;
-    const int d = threadIdx.x;
+    const int d0 = blockIdx.y * 64;
     const float* base = part + (size_t)qid * n_parts * 258;
-    float M = -1e20f;
-    for (int s = 0; s < n_parts; s++) M = fmaxf(M, base[(size_t)s * 258 + 256]);
-    float den = 0.0f, num = 0.0f;
-    for (int s = 0; s < n_parts; s++) {
-        const float* p = base + (size_t)s * 258;
-        const float f = expf(p[256] - M);
-        den = fmaf(p[257], f, den);
-        num = fmaf(p[d], f, num);
-    }
+    float M, den;
+    lse_weights(base, n_parts, s_w, s_red, M, den);
+    const float num = lse_num(base, n_parts, s_w, s_acc, d0);
     float* o = out + (size_t)qid * 258;
-    o[d] = num;
-    if (d == 0) {
+    if (threadIdx.x < 64) o[d0 + threadIdx.x] = num;
+    if (blockIdx.y == 0 && threadIdx.x == 0) {
         o[256] = M;
         o[257] = den;
     }
@@ -646,22 +689,22 @@ __global__ __launch_bounds__(256) void combine_gate_kernel(const float* __restri
                                                           const __half* __restrict__ q_gate,
                                                           __half* __restrict__ out,
                                                           int n_parts, float eps) {
+    __shared__ float s_w[kMaxParts];
+    __shared__ float s_red[8];
+    __shared__ float s_acc[256];
     const int h = blockIdx.x;
-    const int d = threadIdx.x;
+    const int d0 = blockIdx.y * 64;
     const float* base = part + (size_t)h * n_parts * 258;
-    float M = -1e20f;
-    for (int s = 0; s < n_parts; s++) M = fmaxf(M, base[(size_t)s * 258 + 256]);
-    float den = 0.0f, num = 0.0f;
-    for (int s = 0; s < n_parts; s++) {
-        const float* p = base + (size_t)s * 258;
-        const float f = expf(p[256] - M);
-        den = fmaf(p[257], f, den);
-        num = fmaf(p[d], f, num);
+    float M, den;
+    lse_weights(base, n_parts, s_w, s_red, M, den);
+    const float num = lse_num(base, n_parts, s_w, s_acc, d0);
+    if (threadIdx.x < 64) {
+        const int d = d0 + threadIdx.x;
+        float val = num / (den + eps);
+        const float g = h2f(q_gate[(size_t)h * 512 + 256 + d]);
+        val = val * (1.0f / (1.0f + expf(-g)));
+        out[(size_t)h * 256 + d] = __float2half(val);
     }
-    float val = num / (den + eps);
-    const float g = h2f(q_gate[(size_t)h * 512 + 256 + d]);
-    val = val * (1.0f / (1.0f + expf(-g)));
-    out[(size_t)h * 256 + d] = __float2half(val);
 }
 
 // ref .cu:1983-2010
@@ -764,13 +807,15 @@ hipError_t launch_compress(const __half* x, const __half* d_vec, const __half* r
 
 hipError_t launch_lse_reduce(const float* part, float* out, int n_q, int n_parts,
                              hipStream_t st) {
-    hipLaunchKernelGGL(lse_reduce_kernel, dim3(n_q), dim3(256), 0, st, part, out, n_parts);
+    if (n_parts > kMaxParts) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(lse_reduce_kernel, dim3(n_q, 4), dim3(256), 0, st, part, out, n_parts);
     return hipGetLastError();
 }
 
 hipError_t launch_combine_gate(const float* part, const __half* q_gate, __half* out, int H_q,
                                int n_parts, float eps, hipStream_t st) {
-    hipLaunchKernelGGL(combine_gate_kernel, dim3(H_q), dim3(256), 0, st, part, q_gate, out,
+    if (n_parts > kMaxParts) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(combine_gate_kernel, dim3(H_q, 4), dim3(256), 0, st, part, q_gate, out,
                        n_parts, eps);
     return hipGetLastError();
 }

@@ -33,6 +33,7 @@ SIGNATURES = {
     "khq_attn_step_fp16": [P] * 19 + [I, I, I, I, I, I, F, F, F, F, P],
     "khq_attn_partials_fp16": [P] * 16 + [I, I, I, F, F, F, F, P],
     "khq_attn_parts": [I],
+    "khq_select_kernel": [I],
     "khq_workspace_reserve": [ctypes.c_size_t],
 }
 

@@ -141,6 +141,12 @@ int khq_attn_partials_fp16(const void* q_gate, const void* k_payload, const void
  * (exposed for tests and the benchmark). */
 int khq_attn_parts(int c_len);
 
+/* Kernel choice for the compressed region (no reference counterpart; a
+ * test and benchmark knob): 0 = automatic (matrix-core kernel for H_kv 4 /
+ * n_rep 6 / L_q 1, portable kernel otherwise), 1 = portable kernel always.
+ * Process-wide; returns -100 for other values. */
+int khq_select_kernel(int which);
+
 /* Grows the library's device workspace (split partials) to at least `bytes`
  * on the current device.  Every launcher grows it on demand; call this first
  * when the launches will be captured into a HIP graph. */

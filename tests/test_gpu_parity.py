@@ -20,6 +20,16 @@ pytestmark = pytest.mark.gpu
 ATOL, RTOL = 2e-3, 1e-3
 
 
+@pytest.fixture(params=[0, 1], ids=["auto", "portable"])
+def kernel(request, device):
+    """Runs a test with the automatic (matrix-core) and the portable kernel."""
+    from khq import _lib
+
+    _lib.call("khq_select_kernel", request.param)
+    yield request.param
+    _lib.call("khq_select_kernel", 0)
+
+
 def t(a, device="cuda"):
     return torch.from_numpy(np.ascontiguousarray(a)).to(device)
 
@@ -123,7 +133,7 @@ def _gpu_state(st, device="cuda"):
 
 
 @pytest.mark.parametrize("splits", [1, 8])
-def test_attn_c2(device, splits):
+def test_attn_c2(device, kernel, splits):
     st = two_region_state(seed=21)
     pay, cents = _gpu_state(st)
     out = torch.zeros((H_Q, D + 2), device=device)
@@ -136,7 +146,7 @@ def test_attn_c2(device, splits):
 
 
 @pytest.mark.parametrize("c_len", [1, 7, 255, 256, 257, 1000])
-def test_attn_random_rows(device, c_len):
+def test_attn_random_rows(device, kernel, c_len):
     lc, h = layer_consts()
     rows = random_rows_np(c_len * H_KV, seed=c_len)
     q = np.random.default_rng(c_len).standard_normal((H_Q, 2 * D)).astype(np.float16)
@@ -171,7 +181,7 @@ def test_attn_error_codes(device):
                     out_partial=None, check=False) == -101
 
 
-def test_window_and_merge(device):
+def test_window_and_merge(device, kernel):
     st = two_region_state(seed=24)
     pay, cents = _gpu_state(st)
     q = t(st["q_gate"])
@@ -226,7 +236,7 @@ def test_gather_q_bitexact(device):
     assert np.array_equal(out.cpu().numpy(), q[:, :D])
 
 
-def test_c3_full_size(device):
+def test_c3_full_size(device, kernel):
     """Config 3 at its real shape: 32,640 compressed + 128 raw, vs the oracle."""
     lc, h = layer_consts(layer_id=0)
     c_len, win = 32640, 128
