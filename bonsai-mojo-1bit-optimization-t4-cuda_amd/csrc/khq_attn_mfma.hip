@@ -36,6 +36,18 @@
 namespace khq {
 namespace mf {
 
+#ifdef KHQ_PHASE_TIMING
+__device__ unsigned long long phase_cycles[16];
+#define PHASE(k)                                                              \
+    do {                                                                      \
+        const unsigned long long now_ = __builtin_amdgcn_s_memtime();         \
+        if (blockIdx.x == 0 && threadIdx.x == 0) phase_cycles[k] += now_ - ph_t; \
+        ph_t = now_;                                                          \
+    } while (0)
+#else
+#define PHASE(k) do { } while (0)
+#endif
+
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -44,22 +56,32 @@ constexpr int TT = 16;           // tokens per tile
 constexpr int ROWS = TT * 4;     // payload rows per tile (4 KV heads)
 constexpr float RESCALE_GAP = 8.0f;
 
+// Padded strides (in 32-bit words) keep the 16 tokens of a tile, and the 64
+// codebook patches, in different LDS banks.
+constexpr int MASK_TS = 68;    // 4 rows x 16 words + 4
+constexpr int KPAY_TS = 44;    // 4 rows x 10 words + 4
+constexpr int VPAY_TS = 108;   // 4 rows x 26 words + 4
+constexpr int CB_PS = 770;     // halves per codebook patch (768 + 2)
+constexpr int O_TS = 264;      // halves per token of the outlier buffer
+constexpr int VT_CS = 20;      // halves per V-tile column (16 tokens + 4)
+constexpr int VT_COLS = 160;   // V-tile columns per half (32 patches x 5)
+
 struct __align__(16) Smem {
-    _Float16 cb[64 * 256 * 3];           // V codebook (98304 B)
-    uint32_t mask[ROWS * 16];            // staged tile
-    uint32_t kpay[ROWS * 10];
-    uint32_t vpay[ROWS * 26];
+    _Float16 cb[64 * CB_PS];             // V codebook (98560 B)
+    uint32_t mask[TT * MASK_TS];         // staged tile
+    uint32_t kpay[TT * KPAY_TS];
+    uint32_t vpay[TT * VPAY_TS];
     _Float16 knorm[ROWS], krn[ROWS], vnorm[ROWS], vrn[ROWS];
     float vsm[ROWS];
     uint2 sgn[256];                      // mask byte -> 4 fp16 signs {0,-1,+1,0}
     _Float16 cbk[256];                   // cents_k[2]
-    float cbkf[256];
     union W {                            // per wavefront scratch
-        _Float16 o[TT * 256];            // outlier values, [token][K position]
-        _Float16 vt[320 * TT];           // expanded V tile, [column][token]
+        _Float16 o[TT * O_TS];           // outlier values, [token][dim]
+        _Float16 vt[VT_COLS * VT_CS];    // expanded V tile, [column][token]
         float f[6 * 256];                // query transforms / epilogue
     } w[4];
     float pb[4][3][6][TT];               // softmax weights x 3 scalings
+    float rope[4][3][8];                 // per lane group: freq, cos(16 f), sin(16 f)
 };
 
 __device__ __forceinline__ f4 mfma32(h8 a, h8 b, f4 c) {
@@ -77,6 +99,28 @@ __device__ __forceinline__ void wave_sync() {
 
 __device__ __forceinline__ float xsh(float v, int m) { return __shfl_xor(v, m, 64); }
 
+// Cross-lane moves inside a 16-lane row (DPP, no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// max / sum over the 16 lanes of a row: xor 1, xor 2 (quad_perm), then
+// row_half_mirror and row_mirror fold the quads and the half rows.
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x141>(v));
+    v = fmaxf(v, dpp<0x140>(v));
+    return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x141>(v);
+    v += dpp<0x140>(v);
+    return v;
+}
+
 // K position (contraction index of the pass/fold MFMAs) -> natural dim.
 // kappa = q*16 + b*4 + k  <->  dim = 64 b + 4 q + k  (patch p = 16 b + q).
 __device__ __forceinline__ int kdim(int kappa) {
@@ -84,6 +128,30 @@ __device__ __forceinline__ int kdim(int kappa) {
 }
 __device__ __forceinline__ int kpos(int dim) {
     return (((dim >> 2) & 15) << 4) | ((dim >> 6) << 2) | (dim & 3);
+}
+
+// cos / sin of an fp32 angle (radians): exact reduction to [-1/2, 1/2]
+// revolutions in fp64, then the hardware sine/cosine (revolution input).
+__device__ __forceinline__ void sincos_rev(float th, float& c, float& s) {
+    double r = (double)th * 0.15915494309189535;  // 1 / (2 pi)
+    r -= rint(r);
+    const float rf = (float)r;
+    c = __builtin_amdgcn_cosf(rf);
+    s = __builtin_amdgcn_sinf(rf);
+}
+
+__device__ __forceinline__ float fexp(float x) { return __expf(x); }
+
+// hi + lo fp16 split of two floats (hi truncated, lo carries the rest).
+__device__ __forceinline__ void split2(float x, float y, _Float16& xh, _Float16& yh,
+                                       _Float16& xl, _Float16& yl) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 hi = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x, y));
+    const h2 lo = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x - (float)hi[0], y - (float)hi[1]));
+    xh = hi[0];
+    yh = hi[1];
+    xl = lo[0];
+    yl = lo[1];
 }
 
 __device__ __forceinline__ void split(float x, _Float16& hi, _Float16& lo) {
@@ -115,6 +183,9 @@ __device__ __forceinline__ void fwht256(float (&v)[4], int lane) {
 __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles_per_chunk) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem& S = *reinterpret_cast<Smem*>(smem_raw);
+#ifdef KHQ_PHASE_TIMING
+    unsigned long long ph_t = __builtin_amdgcn_s_memtime();
+#endif
     const int tid = threadIdx.x;
     const int w = tid >> 6;          // KV head
     const int lane = tid & 63;
@@ -128,16 +199,24 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
 
     // ------------------------------------------------ per-block tables
     {
-        // 96 KB codebook: 24 uint4 per thread, all loads issued before the stores
+        // 96 KB codebook: 24 uint4 per thread, all loads issued before the stores;
+        // patch p lands at word p * CB_PS / 2 (96 uint4 per patch)
         const uint4* src = reinterpret_cast<const uint4*>(a.vq);
-        uint4* dst = reinterpret_cast<uint4*>(S.cb);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(S.cb);
 #pragma unroll
         for (int b = 0; b < 3; b++) {
             uint4 tmp[8];
 #pragma unroll
             for (int i = 0; i < 8; i++) tmp[i] = src[tid + 256 * (8 * b + i)];
 #pragma unroll
-            for (int i = 0; i < 8; i++) dst[tid + 256 * (8 * b + i)] = tmp[i];
+            for (int i = 0; i < 8; i++) {
+                const int c = tid + 256 * (8 * b + i);
+                uint32_t* d = dst + (c / 96) * (CB_PS / 2) + (c % 96) * 4;
+                d[0] = tmp[i].x;
+                d[1] = tmp[i].y;
+                d[2] = tmp[i].z;
+                d[3] = tmp[i].w;
+            }
         }
         const _Float16 one = (_Float16)1.0f, mone = (_Float16)-1.0f, zero = (_Float16)0.0f;
         {
@@ -152,34 +231,78 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
         }
         const _Float16 cbv = reinterpret_cast<const _Float16*>(a.cents_k)[512 + tid];
         S.cbk[tid] = cbv;
-        S.cbkf[tid] = (float)cbv;
     }
 
     // ------------------------------------------------ per-wave query side
-    // q_h for the 6 heads of KV head w; t_h = R^T H (q[64:] * dks) (pass part)
+    // q_h for the 6 heads of KV head w; t_h = R^T H (q[64:] * dks) (pass part).
+    // H_256 = H_16 (x) H_16 (dim = 16 hi + lo): rows then columns in LDS.
     const __half* qbase = a.q + (size_t)(w * 6) * 512;
     float* tq = S.w[w].f;  // [6][256]
-    float dks[4];
-    float rk[16];
+    {
+        float dks[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) dks[c] = (1.0f / 256.0f) / (__half2float(a.dk[lane * 4 + c]) + 1e-8f);
+        for (int c = 0; c < 4; c++)
+            dks[c] = (1.0f / 256.0f) / (__half2float(a.dk[lane * 4 + c]) + 1e-8f);
 #pragma unroll
-    for (int t = 0; t < 16; t++) rk[t] = __half2float(a.rotor_k[lane * 16 + t]);
-    for (int h = 0; h < 6; h++) {
-        float v[4];
+        for (int h = 0; h < 6; h++) {
+            const uint2 qr = *reinterpret_cast<const uint2*>(qbase + h * 512 + lane * 4);
+            const __half* qh = reinterpret_cast<const __half*>(&qr);
+            f4 v;
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int dim = lane * 4 + c;
-            v[c] = dim >= 64 ? __half2float(qbase[h * 512 + dim]) * dks[c] : 0.0f;
+            for (int c = 0; c < 4; c++) v[c] = lane >= 16 ? __half2float(qh[c]) * dks[c] : 0.0f;
+            *reinterpret_cast<f4*>(&tq[h * 256 + lane * 4]) = v;
         }
-        fwht256(v, lane);
+        wave_sync();
+        // 96 transforms of 16 points (6 heads x 16), first along lo then along hi
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            float t = v[0] * rk[0 * 4 + k];
-            t = fmaf(v[1], rk[1 * 4 + k], t);
-            t = fmaf(v[2], rk[2 * 4 + k], t);
-            t = fmaf(v[3], rk[3 * 4 + k], t);
-            tq[h * 256 + lane * 4 + k] = t;
+        for (int pass = 0; pass < 2; pass++) {
+            for (int item = lane; item < 96; item += 64) {
+                const int h = item >> 4, r = item & 15;
+                const int base = h * 256 + (pass == 0 ? r * 16 : r);
+                const int step = pass == 0 ? 1 : 16;
+                float v[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++) v[i] = tq[base + i * step];
+#pragma unroll
+                for (int m = 1; m < 16; m <<= 1)
+#pragma unroll
+                    for (int i = 0; i < 16; i++)
+                        if ((i & m) == 0) {
+                            const float x = v[i], y = v[i + m];
+                            v[i] = x + y;
+                            v[i + m] = x - y;
+                        }
+#pragma unroll
+                for (int i = 0; i < 16; i++) tq[base + i * step] = v[i];
+            }
+            wave_sync();
+        }
+        // per patch: t[4p + k] = sum_c u[4p + c] R_p[c][k]
+        float rk[16];
+        {
+            const uint4* rp = reinterpret_cast<const uint4*>(a.rotor_k + lane * 16);
+            const uint4 r0 = rp[0], r1 = rp[1];
+            const __half* rh0 = reinterpret_cast<const __half*>(&r0);
+            const __half* rh1 = reinterpret_cast<const __half*>(&r1);
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                rk[t] = __half2float(rh0[t]);
+                rk[8 + t] = __half2float(rh1[t]);
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < 6; h++) {
+            const f4 u = *reinterpret_cast<const f4*>(&tq[h * 256 + lane * 4]);
+            f4 t;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float x = u[0] * rk[0 * 4 + k];
+                x = fmaf(u[1], rk[1 * 4 + k], x);
+                x = fmaf(u[2], rk[2 * 4 + k], x);
+                x = fmaf(u[3], rk[3 * 4 + k], x);
+                t[k] = x;
+            }
+            *reinterpret_cast<f4*>(&tq[h * 256 + lane * 4]) = t;
         }
     }
     __syncthreads();
@@ -198,40 +321,47 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
             At[st][e] = arow_lo ? lo : hi;
         }
     }
-    // fold: z_(4q+c') = sum_k R_p[c'][k] b_(4p+k) over p = q, q+16, q+32, q+48
-    h8 Aw[4][2];
-#pragma unroll
-    for (int T = 0; T < 4; T++)
-#pragma unroll
-        for (int s = 0; s < 2; s++) {
-            const int st = 2 * T + s;
-            const int q_row = 4 * T + (li >> 2), c_row = li & 3;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int kap = 32 * st + 8 * lg + e;
-                const int q_col = kap >> 4, b = (kap >> 2) & 3, k = kap & 3;
-                const int p = 16 * b + q_col;
-                Aw[T][s][e] = (q_row == q_col)
-                                  ? reinterpret_cast<const _Float16*>(a.rotor_k)[p * 16 + c_row * 4 + k]
-                                  : (_Float16)0.0f;
-            }
-        }
-    // H_64 with 1/(256 d): row j = 16T' + li, K position (kap, lg, e) ->
-    // m = 16 (2 (kap & 1) + e / 4) + 4 lg + (e & 3); kap >= 2 is the lo half.
-    h8 Ah[4][2];
-#pragma unroll
-    for (int Tp = 0; Tp < 4; Tp++) {
-        const int j = 16 * Tp + li;
-        const float dj = (1.0f / 256.0f) / (__half2float(a.dk[j]) + 1e-8f);
-#pragma unroll
-        for (int kk = 0; kk < 2; kk++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int m = 16 * (2 * kk + (e >> 2)) + 4 * lg + (e & 3);
-                const float sgn = (__popc(j & m) & 1) ? -1.0f : 1.0f;
-                Ah[Tp][kk][e] = (_Float16)(sgn * dj);
-            }
+    // fold: z_(4q+c') = sum_k R_p[c'][k] b_(4p+k) over p = q, q+16, q+32, q+48.
+    // In M-tile T only K-step 2T + s_fold carries this lane's row (q_row = q_col
+    // needs li/4 = 2 s + lg/2); Aw[T] holds those 8 rotor entries.
+    {   // stage rotor_k (2 KB) in the V staging area, free until the first commit
+        const uint4* src = reinterpret_cast<const uint4*>(a.rotor_k);
+        if (tid < 128) reinterpret_cast<uint4*>(S.vpay)[tid] = src[tid];
+        __syncthreads();
     }
+    const _Float16* rk_lds = reinterpret_cast<const _Float16*>(S.vpay);
+    const int s_fold = ((li >> 2) - (lg >> 1)) >> 1;
+    const bool fold_ok = (((li >> 2) - (lg >> 1)) & 1) == 0 && s_fold >= 0 && s_fold < 2;
+    h8 Aw[4];
+#pragma unroll
+    for (int T = 0; T < 4; T++) {
+        const int c_row = li & 3;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int b = 2 * (lg & 1) + (e >> 2), k = e & 3;
+            const int p = 16 * b + 4 * T + (li >> 2);
+            Aw[T][e] = fold_ok ? rk_lds[p * 16 + c_row * 4 + k] : (_Float16)0.0f;
+        }
+    }
+    const h8 hzero = {0, 0, 0, 0, 0, 0, 0, 0};
+    // H_64 = H_4 (x) H_16 (j = 16 T' + li, m = 16 T + 4 lg + c'):
+    // A[T'][kk] = H_4[T'][2 kk + e/4] * H_16[li][4 lg + (e & 3)] / 256; the
+    // sign of 1/d_j is applied to the output rows instead.  Ag[0] = [g, g],
+    // Ag[1] = [g, -g], with -Ag for the negated patterns.
+    h8 Ag[2];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float g = ((__popc(li & (4 * lg + (e & 3))) & 1) ? -1.0f : 1.0f) / 256.0f;
+        Ag[0][e] = (_Float16)g;
+        Ag[1][e] = (_Float16)((e >> 2) ? -g : g);
+    }
+    // output-row signs of 1/d for this lane's rows j = 16 T' + 4 lg + c'
+    float dsg[4][4];
+#pragma unroll
+    for (int Tp = 0; Tp < 4; Tp++)
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            dsg[Tp][c] = (__half2float(a.dk[16 * Tp + 4 * lg + c]) < 0.0f) ? -1.0f : 1.0f;
     // q_rot (roped dims 0..63), K positions matching the rope'd key layout
     h8 Aq[2];
 #pragma unroll
@@ -246,24 +376,24 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
 
     // RoPE constants: this lane's key dims are 16T' + 4 lg + c' (T' = 0..3),
     // frequency index m = dim & 31 for T' in {0, 1}.
-    float fr[8], dc[8], ds[8];
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
+    float dc[8], ds[8];
+    if (w == 0 && li < 8) {  // lanes (u = li, lg) of wave 0 fill the group table
+        const int u = li;
         const int m = 16 * (u >> 2) + 4 * lg + (u & 3);
-        fr[u] = powf(a.rope_base, -2.0f * (float)m / 64.0f);
-        dc[u] = cosf((float)li * fr[u]);
-        ds[u] = sinf((float)li * fr[u]);
+        const float f = powf(a.rope_base, -2.0f * (float)m / 64.0f);
+        S.rope[lg][0][u] = f;
+        S.rope[lg][1][u] = cosf(16.0f * f);
+        S.rope[lg][2][u] = sinf(16.0f * f);
     }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 8; u++) sincos_rev((float)li * S.rope[lg][0][u], dc[u], ds[u]);
 
     // V side per-lane constants (expansion lane = patch `lane`)
     const float av = a.a_v;
-    const _Float16 c3v0 = reinterpret_cast<const _Float16*>(a.cents_v)[lane * 4 + 3];
-    const _Float16 c3v1 = reinterpret_cast<const _Float16*>(a.cents_v)[256 + lane * 4 + 3];
-    const int vgrp = lane >> 3, vsub = lane & 7;
-    const int vbit = 12 * vsub;                 // bit offset of the field in the group
-    const int vw0 = vgrp * 3 + (vbit >> 5);     // first word holding the field
-    const int vsh = vbit & 31;
-    const int vhw = 24 + (lane >> 5), vhb = lane & 31;
+    const _Float16* cvh = reinterpret_cast<const _Float16*>(a.cents_v);
+    const _Float16 c3v0a = cvh[(lane & 31) * 4 + 3], c3v1a = cvh[256 + (lane & 31) * 4 + 3];
+    const _Float16 c3v0b = cvh[(32 + (lane & 31)) * 4 + 3], c3v1b = cvh[256 + (32 + (lane & 31)) * 4 + 3];
 
     // ------------------------------------------------ accumulators
     f4 pv[20];
@@ -320,10 +450,13 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
     } while (0)
 #define KHQ_COMMIT() \
     do { \
-        reinterpret_cast<uint4*>(S.mask)[tid] = pre[0]; \
-        if (tid < 160) reinterpret_cast<uint4*>(S.kpay)[tid] = pre[1]; \
-        reinterpret_cast<uint4*>(S.vpay)[tid] = pre[2]; \
-        if (tid + 256 < 416) reinterpret_cast<uint4*>(S.vpay)[tid + 256] = pre[3]; \
+        *reinterpret_cast<uint4*>(&S.mask[(tid >> 4) * MASK_TS + (tid & 15) * 4]) = pre[0]; \
+        if (tid < 160) \
+            *reinterpret_cast<uint4*>(&S.kpay[(tid / 10) * KPAY_TS + (tid % 10) * 4]) = pre[1]; \
+        *reinterpret_cast<uint4*>(&S.vpay[(tid / 26) * VPAY_TS + (tid % 26) * 4]) = pre[2]; \
+        if (tid + 256 < 416) \
+            *reinterpret_cast<uint4*>(&S.vpay[((tid + 256) / 26) * VPAY_TS + ((tid + 256) % 26) * 4]) = \
+                pre[3]; \
         if (tid < 64) { \
             const int arr = tid >> 4, part = tid & 15; \
             _Float16* base = arr == 0 ? S.knorm : arr == 1 ? S.krn : arr == 2 ? S.vnorm : S.vrn; \
@@ -338,17 +471,16 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
     if (n_tiles > 0) KHQ_COMMIT();
     __syncthreads();
 
-    // RoPE base angle for the first tile, advanced by 16 tokens per tile and
+    // RoPE base angle of the tile, advanced by 16 tokens per tile and
     // re-anchored exactly every 16 tiles.
-    float bc[8], bs[8], sc16[8], ss16[8];
+    float bc[8], bs[8];
 #pragma unroll
     for (int u = 0; u < 8; u++) {
-        sc16[u] = cosf(16.0f * fr[u]);
-        ss16[u] = sinf(16.0f * fr[u]);
         bc[u] = 1.0f;
         bs[u] = 0.0f;
     }
 
+    PHASE(0);
     _Float16* ow = S.w[w].o;
     _Float16* vt = S.w[w].vt;
     float* pbw = &S.pb[w][0][0][0];
@@ -359,23 +491,22 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
         if ((t & 15) == 0) {
 #pragma unroll
             for (int u = 0; u < 8; u++) {
-                const float th = (float)(a.start_pos + s0) * fr[u];
-                bc[u] = cosf(th);
-                bs[u] = sinf(th);
+                const float th = (float)(a.start_pos + s0) * S.rope[lg][0][u];
+                sincos_rev(th, bc[u], bs[u]);
             }
         }
 
         // ---- (a) zero outlier buffer
         {
             uint4* o4 = reinterpret_cast<uint4*>(ow);
-#pragma unroll
-            for (int i = 0; i < (TT * 256 * 2) / 16 / 64; i++) o4[lane + 64 * i] = uint4{0, 0, 0, 0};
+            for (int i = lane; i < (TT * O_TS * 2) / 16; i += 64) o4[i] = uint4{0, 0, 0, 0};
         }
         wave_sync();
 
+        PHASE(1);
         // ---- per-token scalars of this lane's token (row li*4 + w)
         const int row = li * 4 + w;
-        const uint32_t* krow = &S.kpay[row * 10];
+        const uint32_t* krow = &S.kpay[li * KPAY_TS + w * 10];
         float mult = (float)krow[0] / 1000.0f;
         if (mult < 0.1f || mult > 10.0f || isnan(mult)) mult = 1.0f;
         const float nk = (float)S.knorm[row];
@@ -384,12 +515,13 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
 
         // ---- (b) outliers: lane (token li, quarter lg) owns dims 64 lg .. 64 lg + 63
         {
-            const uint32_t* mrow = &S.mask[row * 16 + 4 * lg];
-            uint32_t c3[4];
+            const uint32_t* mrow = &S.mask[li * MASK_TS + w * 16 + 4 * lg];
+            uint32_t c3[4], c3w[4];
             int cnt = 0;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t m = mrow[i];
+                c3w[i] = m;
                 c3[i] = (m & (m >> 1)) & 0x55555555u;
                 cnt += __popc(c3[i]);
             }
@@ -411,32 +543,69 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
                 x = (x | (x >> 8)) & 0x0000FFFFu;
                 msk |= (uint64_t)x << (16 * i);
             }
+            // sign bits (bytes 29..35) and nibbles (bytes 4..28), both in outlier order;
+            // only ordinals < 50 are stored (others: sign -1, residual 0).  The
+            // sign goes back into the staged mask (code 3 -> 2 for +, 1 for -),
+            // so the b operand's sign table yields +-cb; O keeps the signed
+            // residual nib * rs / mult.
             const uint64_t signs = ((uint64_t)krow[7] | ((uint64_t)krow[8] << 32)) >> 8;
-            const unsigned char* kb = reinterpret_cast<const unsigned char*>(krow);
-            _Float16* orow = ow + li * 256;
+            const int nv0 = max(0, min(64, 50 - j));
+            uint64_t sw = (j < 64 ? (signs >> j) : 0ull) & (nv0 >= 64 ? ~0ull : ((1ull << nv0) - 1ull));
+            uint64_t nw = 0, neg = 0;
+            int left = 0;  // nibbles remaining in nw
+            const uint64_t all3 = msk;
+            _Float16* orow = ow + li * O_TS + 64 * lg;
             while (msk) {
+                if (left == 0) {
+                    // 16 nibbles from ordinal j: bit 32 + 4 j of the row (dword 1 + j / 8)
+                    const int dwi = 1 + (j >> 3), sh = 4 * (j & 7);
+                    const uint64_t lo64 = (uint64_t)krow[min(dwi, 9)] | ((uint64_t)krow[min(dwi + 1, 9)] << 32);
+                    const uint32_t d2 = krow[min(dwi + 2, 9)];
+                    nw = (lo64 >> sh) | (sh ? ((uint64_t)d2 << (64 - sh)) : 0ull);
+                    const int nvn = max(0, min(16, 50 - j));
+                    nw &= (nvn >= 16) ? ~0ull : ((1ull << (4 * nvn)) - 1ull);
+                    left = 16;
+                }
                 const int bpos = __builtin_ctzll(msk);
                 msk &= msk - 1;
-                const int dim = 64 * lg + bpos;
-                float sgn = -1.0f, nib = 0.0f;
-                if (j < 50) {
-                    sgn = ((signs >> j) & 1ull) ? 1.0f : -1.0f;
-                    nib = (float)((kb[4 + (j >> 1)] >> ((j & 1) * 4)) & 0xF);
-                }
-                orow[kpos(dim)] = (_Float16)(sgn * fmaf(nib, rr, S.cbkf[dim]));
+                const float r = (float)(uint32_t)(nw & 15ull) * rr;
+                const bool pos = (sw & 1ull) != 0ull;
+                orow[bpos] = (_Float16)(pos ? r : -r);
+                neg |= (uint64_t)(!pos) << bpos;
+                nw >>= 4;
+                sw >>= 1;
+                left--;
                 j++;
+            }
+            // spread the 16-bit halves back to the 2-bit code positions
+            uint32_t* mw = &S.mask[li * MASK_TS + w * 16 + 4 * lg];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                uint32_t ng = (uint32_t)(neg >> (16 * i)) & 0xFFFFu;
+                uint32_t a3 = (uint32_t)(all3 >> (16 * i)) & 0xFFFFu;
+                ng = (ng | (ng << 8)) & 0x00FF00FFu;
+                ng = (ng | (ng << 4)) & 0x0F0F0F0Fu;
+                ng = (ng | (ng << 2)) & 0x33333333u;
+                ng = (ng | (ng << 1)) & 0x55555555u;
+                a3 = (a3 | (a3 << 8)) & 0x00FF00FFu;
+                a3 = (a3 | (a3 << 4)) & 0x0F0F0F0Fu;
+                a3 = (a3 | (a3 << 2)) & 0x33333333u;
+                a3 = (a3 | (a3 << 1)) & 0x55555555u;
+                // negative: clear bit 1 (3 -> 1); positive: clear bit 0 (3 -> 2)
+                mw[i] = c3w[i] ^ ((ng << 1) | (a3 & ~ng));
             }
         }
         wave_sync();
 
+        PHASE(2);
         // ---- (c) b operand + pass / fold MFMAs
         f4 cs = f4{0.f, 0.f, 0.f, 0.f};
         f4 zt[4];
 #pragma unroll
         for (int T = 0; T < 4; T++) zt[T] = f4{0.f, 0.f, 0.f, 0.f};
         {
-            const unsigned char* mb = reinterpret_cast<const unsigned char*>(&S.mask[row * 16]);
-            const _Float16* orow = ow + li * 256;
+            const unsigned char* mb = reinterpret_cast<const unsigned char*>(&S.mask[li * MASK_TS + w * 16]);
+            const _Float16* orow = ow + li * O_TS;
 #pragma unroll
             for (int st = 0; st < 8; st++) {
                 const int q = 2 * st + (lg >> 1);
@@ -445,43 +614,45 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
                 const uint2 sg1 = S.sgn[mb[p1]];
                 const uint2 cb0 = *reinterpret_cast<const uint2*>(&S.cbk[p0 * 4]);
                 const uint2 cb1 = *reinterpret_cast<const uint2*>(&S.cbk[p1 * 4]);
-                const h8 ov = *reinterpret_cast<const h8*>(&orow[32 * st + 8 * lg]);
+                const h4 ov0 = *reinterpret_cast<const h4*>(&orow[4 * p0]);
+                const h4 ov1 = *reinterpret_cast<const h4*>(&orow[4 * p1]);
                 h4 s0v = *reinterpret_cast<const h4*>(&sg0), s1v = *reinterpret_cast<const h4*>(&sg1);
                 h4 c0v = *reinterpret_cast<const h4*>(&cb0), c1v = *reinterpret_cast<const h4*>(&cb1);
-                h4 b0 = s0v * c0v, b1 = s1v * c1v;
-                h8 bv;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    bv[e] = b0[e] + ov[e];
-                    bv[4 + e] = b1[e] + ov[4 + e];
-                }
+                const h4 b0 = s0v * c0v + ov0, b1 = s1v * c1v + ov1;
+                const h8 bv = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
                 cs = mfma32(At[st], bv, cs);
-                zt[st >> 1] = mfma32(Aw[st >> 1][st & 1], bv, zt[st >> 1]);
+                zt[st >> 1] = mfma32((st & 1) == s_fold ? Aw[st >> 1] : hzero, bv, zt[st >> 1]);
             }
         }
 
+        PHASE(3);
         // ---- (d) H_64 (1/(256 d)) on z, split hi + lo
         f4 kr[4];
         {
             h8 zb[4];
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
+            for (int e = 0; e < 8; e += 2) {
                 const int T0 = e >> 2, c = e & 3;
-                _Float16 hi, lo;
-                split(zt[T0][c], hi, lo);
-                zb[0][e] = hi;
-                zb[2][e] = lo;
-                split(zt[2 + T0][c], hi, lo);
-                zb[1][e] = hi;
-                zb[3][e] = lo;
+                _Float16 a0, a1, a2, a3;
+                split2(zt[T0][c], zt[T0][c + 1], a0, a1, a2, a3);
+                zb[0][e] = a0; zb[0][e + 1] = a1; zb[2][e] = a2; zb[2][e + 1] = a3;
+                split2(zt[2 + T0][c], zt[2 + T0][c + 1], a0, a1, a2, a3);
+                zb[1][e] = a0; zb[1][e + 1] = a1; zb[3][e] = a2; zb[3][e + 1] = a3;
             }
+            // H_4 rows: T'=0 [+ + + +], 1 [+ - + -], 2 [+ + - -], 3 [+ - - +]
+            // over T = 0..3 = (kk, half): Ag[0] = [+,+], Ag[1] = [+,-].
+            const h8 A00 = Ag[0], A01 = Ag[1], A10 = -Ag[0], A11 = -Ag[1];
 #pragma unroll
             for (int Tp = 0; Tp < 4; Tp++) {
+                const h8 k0 = (Tp & 1) ? A01 : A00;               // T = 0, 1
+                const h8 k1 = (Tp == 0) ? A00 : (Tp == 1) ? A01 : (Tp == 2) ? A10 : A11;  // T = 2, 3
                 f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-                acc = mfma32(Ah[Tp][0], zb[0], acc);
-                acc = mfma32(Ah[Tp][1], zb[1], acc);
-                acc = mfma32(Ah[Tp][0], zb[2], acc);
-                acc = mfma32(Ah[Tp][1], zb[3], acc);
+                acc = mfma32(k0, zb[0], acc);
+                acc = mfma32(k1, zb[1], acc);
+                acc = mfma32(k0, zb[2], acc);
+                acc = mfma32(k1, zb[3], acc);
+#pragma unroll
+                for (int c = 0; c < 4; c++) acc[c] *= dsg[Tp][c];
                 kr[Tp] = acc;
             }
         }
@@ -503,15 +674,13 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
         {
             h8 kb[4];
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
+            for (int e = 0; e < 8; e += 2) {
                 const int T0 = e >> 2, c = e & 3;
-                _Float16 hi, lo;
-                split(kr[T0][c], hi, lo);
-                kb[0][e] = hi;
-                kb[2][e] = lo;
-                split(kr[2 + T0][c], hi, lo);
-                kb[1][e] = hi;
-                kb[3][e] = lo;
+                _Float16 a0, a1, a2, a3;
+                split2(kr[T0][c], kr[T0][c + 1], a0, a1, a2, a3);
+                kb[0][e] = a0; kb[0][e + 1] = a1; kb[2][e] = a2; kb[2][e + 1] = a3;
+                split2(kr[2 + T0][c], kr[2 + T0][c + 1], a0, a1, a2, a3);
+                kb[1][e] = a0; kb[1][e + 1] = a1; kb[3][e] = a2; kb[3][e + 1] = a3;
             }
             cs = mfma32(Aq[0], kb[0], cs);
             cs = mfma32(Aq[1], kb[1], cs);
@@ -519,6 +688,7 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
             cs = mfma32(Aq[1], kb[3], cs);
         }
 
+        PHASE(4);
         // ---- (g) scores of heads 2 lg, 2 lg + 1 for token li
         const bool tok_ok = (s0 + li) < s_hi;
         const float fsc = a.a_k * nk * mult * a.sc;
@@ -531,12 +701,7 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
         float mx[2];
 #pragma unroll
         for (int x = 0; x < 2; x++) {
-            float m = sc2[x];
-            m = fmaxf(m, xsh(m, 1));
-            m = fmaxf(m, xsh(m, 2));
-            m = fmaxf(m, xsh(m, 4));
-            m = fmaxf(m, xsh(m, 8));
-            mx[x] = m;
+            mx[x] = row16_max(sc2[x]);
         }
         const bool need = (mx[0] > Mref[0] + RESCALE_GAP) || (mx[1] > Mref[1] + RESCALE_GAP);
         if (__ballot(need) != 0ull) {
@@ -545,7 +710,7 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
             for (int x = 0; x < 2; x++) {
                 const bool up = mx[x] > Mref[x] + RESCALE_GAP;
                 const float nm = up ? mx[x] : Mref[x];
-                fac[x] = (nm == -INFINITY) ? 1.0f : expf(Mref[x] - nm);
+                fac[x] = (nm == -INFINITY) ? 1.0f : fexp(Mref[x] - nm);
                 Mref[x] = nm;
                 lsum[x] *= fac[x];
                 s3sum[x] *= fac[x];
@@ -561,10 +726,11 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
         float pr[2];
 #pragma unroll
         for (int x = 0; x < 2; x++) {
-            pr[x] = (sc2[x] == -INFINITY) ? 0.0f : expf(sc2[x] - Mref[x]);
+            pr[x] = (sc2[x] == -INFINITY) ? 0.0f : fexp(sc2[x] - Mref[x]);
             lsum[x] += pr[x];
         }
 
+        PHASE(5);
         // ---- (i) weights x V scalings -> A operands (rows = head hi/lo, K = tokens)
         {
             const float nv = (float)S.vnorm[row];
@@ -592,70 +758,84 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
             const f4 pw = arow_ok ? *reinterpret_cast<const f4*>(&pbw[(v * 6 + arow_h) * TT + 4 * lg])
                                   : f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                _Float16 hi, lo;
-                split(pw[e], hi, lo);
-                Ap[v][e] = arow_lo ? lo : hi;
+            for (int e = 0; e < 4; e += 2) {
+                _Float16 h0, h1, l0, l1;
+                split2(pw[e], pw[e + 1], h0, h1, l0, l1);
+                Ap[v][e] = arow_lo ? l0 : h0;
+                Ap[v][e + 1] = arow_lo ? l1 : h1;
             }
         }
 
-        // ---- (j) expand the V tile: lane = patch, columns 3p+k, 192+p, 256+p
-        {
+        PHASE(6);
+        // ---- (j, k) V in two halves of 32 patches: expand [160 columns][16 tokens]
+        // (column 3p'+k: codebook dim k of patch p'; 96+p': cents[d3]; 128+p': dump),
+        // then P x V on MFMA (16x16x16, K = the 16 tokens).  Expansion lane:
+        // patch 32 half + (lane & 31), tokens 8 (lane >> 5) .. + 7.
 #pragma unroll
-            for (int quad = 0; quad < 4; quad++) {
+        for (int hv = 0; hv < 2; hv++) {
+            const int pl = lane & 31;
+            const int p = 32 * hv + pl;
+            const int vgrp = p >> 3, vsub = p & 7;
+            const int vbit = 12 * vsub;
+            const int vw0 = vgrp * 3 + (vbit >> 5);
+            const int vsh = vbit & 31;
+            const int vhw = 24 + hv, vhb = pl;
+            const _Float16 c3a = hv ? c3v0b : c3v0a, c3b = hv ? c3v1b : c3v1a;
+#pragma unroll
+            for (int quad = 0; quad < 2; quad++) {
                 h4 col[5];
 #pragma unroll
                 for (int tt = 0; tt < 4; tt++) {
-                    const int tok = quad * 4 + tt;
-                    const uint32_t* vr = &S.vpay[(tok * 4 + w) * 26];
-                    const uint64_t pair = (uint64_t)vr[vw0] | ((uint64_t)vr[vw0 + 1 < 26 ? vw0 + 1 : vw0] << 32);
-                    const uint32_t fld = (uint32_t)(pair >> vsh) & 0xFFFu;
-                    const uint32_t code = (fld & 0x7Fu) | (((vr[vhw] >> vhb) & 1u) << 7);
-                    const _Float16* ce = &S.cb[(lane * 256 + code) * 3];
+                    const int tok = 8 * (lane >> 5) + 4 * quad + tt;
+                    const uint32_t* vr = &S.vpay[tok * VPAY_TS + w * 26];
+                    const uint32_t fld = __builtin_amdgcn_alignbit(vr[vw0 + 1], vr[vw0], vsh) & 0xFFFu;
+                    const uint32_t code = (fld & 0x7Fu) | (__builtin_amdgcn_ubfe(vr[vhw], vhb, 1) << 7);
+                    const _Float16* ce = &S.cb[p * CB_PS + code * 3];
                     col[0][tt] = ce[0];
                     col[1][tt] = ce[1];
                     col[2][tt] = ce[2];
-                    col[3][tt] = ((fld >> 7) & 1u) ? c3v1 : c3v0;
-                    col[4][tt] = (_Float16)(float)((fld >> 8) & 0xFu);
+                    col[3][tt] = ((fld >> 7) & 1u) ? c3b : c3a;
+                    col[4][tt] = (_Float16)(unsigned short)((fld >> 8) & 0xFu);
                 }
-                *reinterpret_cast<h4*>(&vt[(3 * lane + 0) * TT + 4 * quad]) = col[0];
-                *reinterpret_cast<h4*>(&vt[(3 * lane + 1) * TT + 4 * quad]) = col[1];
-                *reinterpret_cast<h4*>(&vt[(3 * lane + 2) * TT + 4 * quad]) = col[2];
-                *reinterpret_cast<h4*>(&vt[(192 + lane) * TT + 4 * quad]) = col[3];
-                *reinterpret_cast<h4*>(&vt[(256 + lane) * TT + 4 * quad]) = col[4];
+                const int t0 = 8 * (lane >> 5) + 4 * quad;
+                *reinterpret_cast<h4*>(&vt[(3 * pl + 0) * VT_CS + t0]) = col[0];
+                *reinterpret_cast<h4*>(&vt[(3 * pl + 1) * VT_CS + t0]) = col[1];
+                *reinterpret_cast<h4*>(&vt[(3 * pl + 2) * VT_CS + t0]) = col[2];
+                *reinterpret_cast<h4*>(&vt[(96 + pl) * VT_CS + t0]) = col[3];
+                *reinterpret_cast<h4*>(&vt[(128 + pl) * VT_CS + t0]) = col[4];
             }
-        }
-        wave_sync();
-
-        // ---- (k) P x V on MFMA (16x16x16, K = the 16 tokens)
+            wave_sync();
 #pragma unroll
-        for (int n = 0; n < 20; n++) {
-            const h4 bv = *reinterpret_cast<const h4*>(&vt[(16 * n + li) * TT + 4 * lg]);
-            pv[n] = mfma16(Ap[n < 12 ? 0 : (n < 16 ? 1 : 2)], bv, pv[n]);
+            for (int n = 0; n < 10; n++) {
+                const h4 bv = *reinterpret_cast<const h4*>(&vt[(16 * n + li) * VT_CS + 4 * lg]);
+                pv[10 * hv + n] = mfma16(Ap[n < 6 ? 0 : (n < 8 ? 1 : 2)], bv, pv[10 * hv + n]);
+            }
+            wave_sync();
         }
 
+        PHASE(7);
         // ---- (l) advance RoPE base by 16 tokens, stage the next tile
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            const float nc = fmaf(bc[u], sc16[u], -(bs[u] * ss16[u]));
-            const float ns = fmaf(bs[u], sc16[u], bc[u] * ss16[u]);
+            const float sc16 = S.rope[lg][1][u], ss16 = S.rope[lg][2][u];
+            const float nc = fmaf(bc[u], sc16, -(bs[u] * ss16));
+            const float ns = fmaf(bs[u], sc16, bc[u] * ss16);
             bc[u] = nc;
             bs[u] = ns;
         }
         __syncthreads();
         if (t + 1 < n_tiles) KHQ_COMMIT();
         __syncthreads();
+        PHASE(8);
     }
 
+    PHASE(9);
     // ------------------------------------------------ epilogue
     // sums over the 16 tokens (lanes) of each head group
 #pragma unroll
     for (int x = 0; x < 2; x++) {
-#pragma unroll
-        for (int m = 1; m < 16; m <<= 1) {
-            lsum[x] += xsh(lsum[x], m);
-            s3sum[x] += xsh(s3sum[x], m);
-        }
+        lsum[x] = row16_sum(lsum[x]);
+        s3sum[x] = row16_sum(s3sum[x]);
     }
     float* ep = S.w[w].f;  // [6][256] rotated-domain accumulators
     if (lg < 3) {
@@ -663,16 +843,20 @@ __global__ __launch_bounds__(256, 1) void attn_mfma_kernel(AttnArgs a, int tiles
         for (int x = 0; x < 2; x++) {
             const int h = 2 * lg + x;
 #pragma unroll
-            for (int n = 0; n < 12; n++) {
-                const int col = 16 * n + li;
-                ep[h * 256 + 4 * (col / 3) + col % 3] = pv[n][2 * x] + pv[n][2 * x + 1];
-            }
+            for (int hv = 0; hv < 2; hv++) {
 #pragma unroll
-            for (int n = 12; n < 16; n++) {
-                const int p = 16 * (n - 12) + li;
-                const float d3 = pv[n][2 * x] + pv[n][2 * x + 1];
-                const float du = pv[n + 4][2 * x] + pv[n + 4][2 * x + 1];
-                ep[h * 256 + 4 * p + 3] = d3 + du - 8.0f * s3sum[x];
+                for (int n = 0; n < 6; n++) {
+                    const int col = 16 * n + li;  // 3 p' + k
+                    const int p = 32 * hv + col / 3;
+                    ep[h * 256 + 4 * p + col % 3] = pv[10 * hv + n][2 * x] + pv[10 * hv + n][2 * x + 1];
+                }
+#pragma unroll
+                for (int n = 6; n < 8; n++) {
+                    const int p = 32 * hv + 16 * (n - 6) + li;
+                    const float d3 = pv[10 * hv + n][2 * x] + pv[10 * hv + n][2 * x + 1];
+                    const float du = pv[10 * hv + n + 2][2 * x] + pv[10 * hv + n + 2][2 * x + 1];
+                    ep[h * 256 + 4 * p + 3] = d3 + du - 8.0f * s3sum[x];
+                }
             }
         }
     }
@@ -752,3 +936,15 @@ hipError_t launch_attn_mfma(const AttnArgs& a, int tiles_per_chunk, int n_chunks
 }
 
 }  // namespace khq
+
+#ifdef KHQ_PHASE_TIMING
+extern "C" int khq_phase_cycles(unsigned long long* out, int reset) {
+    hipError_t e = hipMemcpyFromSymbol(out, HIP_SYMBOL(khq::mf::phase_cycles),
+                                       sizeof(unsigned long long) * 16);
+    if (e == hipSuccess && reset) {
+        unsigned long long z[16] = {0};
+        e = hipMemcpyToSymbol(HIP_SYMBOL(khq::mf::phase_cycles), z, sizeof(z));
+    }
+    return e == hipSuccess ? 0 : (int)e;
+}
+#endif
