@@ -119,6 +119,11 @@ def main():
     kern_gbs = c_bytes / (kern_us * 1e-6) / 1e9
     step_gbs = step_bytes / (us_layer_step * 1e-6) / 1e9
 
+    traffic = {}
+    tpath = os.path.join(ROOT, "profiles", "attn_mfma_c3_traffic.json")
+    if os.path.exists(tpath) and c_len == 32640:
+        with open(tpath) as f:
+            traffic = json.load(f)
     result = {
         "metric": "KHQ decode attn us/layer-step @32K ctx + achieved HBM GB/s (% of peak)",
         "value": round(us_layer_step, 3),
@@ -143,12 +148,13 @@ def main():
         "bytes_per_layer_step": step_bytes,
         "roofline": {
             "bound": "hbm",
-            "kernel": "attn_part_kernel<6> (compressed region)",
+            "kernel": "attn_mfma_kernel (compressed region)",
             "achieved": round(kern_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic.get("traffic_bytes_scaled"),
+            "traffic_128b_requests": traffic.get("traffic_bytes_128b_requests"),
             "avg_kernel_us": round(kern_us, 3),
             "bytes_per_launch": c_bytes,
         },
