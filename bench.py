@@ -30,6 +30,9 @@ H_Q, H_KV, D = 24, 4, 256
 ROW_BYTES = 220
 HBM_PEAK_GBS = 8000.0
 RING = 256
+KERNEL_NAMES = {"auto": "attn_ws_kernel (compressed region)",
+                "portable": "attn_part_kernel<6> (compressed region)",
+                "mfma-single": "attn_mfma_kernel (compressed region)"}
 
 
 def parse():
@@ -42,6 +45,8 @@ def parse():
     ap.add_argument("--win", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--kernel", choices=["auto", "portable", "mfma-single"], default="auto",
+                    help="compressed-region kernel (library default: auto)")
     ap.add_argument("--sweep", action="store_true",
                     help="also time the reference entry points at splits 1/8/32/64")
     return ap.parse_args()
@@ -54,7 +59,9 @@ def main():
         sys.exit(2)
     import torch
 
-    from khq import ops, synth
+    from khq import _lib, ops, synth
+
+    _lib.call("khq_select_kernel", ["auto", "portable", "mfma-single"].index(args.kernel))
     from khq.centroids import synthetic_layer
 
     dev = "cuda"
@@ -120,7 +127,8 @@ def main():
     step_gbs = step_bytes / (us_layer_step * 1e-6) / 1e9
 
     traffic = {}
-    tpath = os.path.join(ROOT, "profiles", "attn_mfma_c3_traffic.json")
+    tname = {"auto": "attn_ws_c3_traffic.json", "mfma-single": "attn_mfma_c3_traffic.json"}
+    tpath = os.path.join(ROOT, "profiles", tname.get(args.kernel, "none"))
     if os.path.exists(tpath) and c_len == 32640:
         with open(tpath) as f:
             traffic = json.load(f)
@@ -148,7 +156,7 @@ def main():
         "bytes_per_layer_step": step_bytes,
         "roofline": {
             "bound": "hbm",
-            "kernel": "attn_mfma_kernel (compressed region)",
+            "kernel": KERNEL_NAMES[args.kernel],
             "achieved": round(kern_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -1,0 +1,725 @@
+// khq_attn_ws.hip -- compressed-region KHQ attention on MI355X matrix cores,
+// wavefront-specialised.
+//
+// Shape: H_kv = 4 KV heads, 6 query heads per KV head, D = 256, one query
+// token.  One 512-thread block per token chunk, tiles of 16 tokens:
+//   key wavefronts   0..3 (KV head w): outliers, scores, softmax of tile t;
+//   value wavefronts 4..7 (KV head w-4): V decode and P x V of tile t - 1.
+// Each SIMD holds one key and one value wavefront, so one hides the other's
+// latency.  The two roles meet once per tile at a block barrier; the softmax
+// weights (and the rescale factors of a raised running maximum) pass through
+// a double-buffered LDS slot.
+//
+// The decoded key of row s is   k_s = a_k * norm_s * mult_s * M b_s   with
+//   b_s[i] = sgn_i * cb_i                    for codes 0..2 (sgn 0, -1, +1)
+//   b_s[i] = sgn_i * (cb_i + res_i * rs_s / mult_s)   for code 3 (outlier)
+//   M      = diag(1/(256 d)) * H_256 * blockdiag(R_p)    (fixed per layer)
+// and RoPE touches only dims 0..63.  The score splits into
+//   pass part:  t . b,  t = R^T H (q[64:] / (256 d)) (query side, fp16 hi+lo);
+//   roped part: z = W b (the four 64-blocks of R b summed, exact fp16 rotor
+//               entries), then H_64 z (z split hi + lo), RoPE in registers,
+//               and the dot with q (key split hi + lo), all on MFMA.
+// K contraction order: K-step st, lane group lg, element e <-> dim
+// 64 lg + 8 st + e, so lane (token li, lg) owns dims 64 lg .. 64 lg + 63 of
+// its token in every K-step: it walks the outliers of exactly those dims and
+// keeps their values in a lane-private LDS strip.
+// V is accumulated in the rotated domain; lane (patch 16 g + li, tokens
+// 4 lg .. 4 lg + 3) decodes straight into the B operand of 16x16x16 MFMAs:
+//   dims (p, k<3): codebook value * (w * a_v * norm * energy)
+//   dim  (p, 3):   cents[d3] * (w * a_v * norm) + dump * (w * norm * smeta / 7)
+//                  - 8 * sum(w * norm * smeta / 7)
+// with the weights split hi + lo.  The inverse V rotor + FWHT + 1/(16 d_v)
+// run once per chunk.  Softmax uses a per-head reference maximum that is only
+// raised when a tile exceeds it by more than 8 (weights stay <= e^8).
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "khq_internal.h"
+#include "khq_mfma_util.h"
+
+namespace khq {
+namespace ws {
+
+using namespace mu;
+
+constexpr int TT = 16;          // tokens per tile
+constexpr int NTHR = 512;       // 4 key + 4 value wavefronts
+constexpr int CB_PS = 768;      // halves per codebook patch (256 codes x 3)
+constexpr int O_LS = 72;        // halves per lane strip of the outlier buffer
+constexpr int KP_TS = 10;       // words per staged kpay row
+constexpr int VP_TS = 26;       // words per staged vpay row
+constexpr float RESCALE_GAP = 8.0f;
+
+struct __align__(16) Smem {
+    _Float16 cb[64 * CB_PS];     // V codebook, [patch][code][3]       98304 B
+    _Float16 o[4][64 * O_LS];    // outlier values per key lane strip   36864 B
+                                 // (setup: query transform; end: V sums)
+    uint32_t vp[4][TT * VP_TS];  // staged vpay rows per KV head         6656 B
+                                 // (setup: rotor_k)
+    uint32_t kp[4][TT * KP_TS];  // staged kpay rows per KV head         2560 B
+    uint2 sgn[256];              // mask byte -> 4 fp16 signs {0,-1,+1,0}
+    _Float16 cbk[256];           // cents_k[2]
+    float pw[2][4][6][TT];       // softmax weights, by tile parity
+    float fac[2][4][8];          // rescale factors of the same tile
+    float vsc[4][3][TT];         // per token V scalings
+    float rope[4][3][8];         // per lane group: freq, cos(16 f), sin(16 f)
+    float ml[4][6][2];           // final (max, sum) per query head
+    float s3[4][8];              // final dump-offset sums per query head
+};
+
+// ---------------------------------------------------------------- key role
+__device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int lane,
+                                         int s_lo, int s_hi, int n_tiles) {
+    const int li = lane & 15, lg = lane >> 4;
+    const __half* qbase = a.q + (size_t)(h * 6) * 512;
+
+    // ---- query side: tq_h = R^T H (q_h[64:] / (256 d)) in the strip area
+    float* tq = reinterpret_cast<float*>(S.o[h]);  // [6][256]
+    {
+        float dks[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            dks[c] = (1.0f / 256.0f) / (__half2float(a.dk[lane * 4 + c]) + 1e-8f);
+#pragma unroll
+        for (int hd = 0; hd < 6; hd++) {
+            const uint2 qr = *reinterpret_cast<const uint2*>(qbase + hd * 512 + lane * 4);
+            const __half* qh = reinterpret_cast<const __half*>(&qr);
+            f4 v;
+#pragma unroll
+            for (int c = 0; c < 4; c++) v[c] = lane >= 16 ? __half2float(qh[c]) * dks[c] : 0.0f;
+            *reinterpret_cast<f4*>(&tq[hd * 256 + lane * 4]) = v;
+        }
+        wave_sync();
+        fwht256_lds(tq, 6, lane);
+        float rk[16];
+        {
+            const uint4* rp = reinterpret_cast<const uint4*>(a.rotor_k + lane * 16);
+            const uint4 r0 = rp[0], r1 = rp[1];
+            const __half* rh0 = reinterpret_cast<const __half*>(&r0);
+            const __half* rh1 = reinterpret_cast<const __half*>(&r1);
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                rk[t] = __half2float(rh0[t]);
+                rk[8 + t] = __half2float(rh1[t]);
+            }
+        }
+        // per patch: t[4p + k] = sum_c u[4p + c] R_p[c][k]
+#pragma unroll
+        for (int hd = 0; hd < 6; hd++) {
+            const f4 u = *reinterpret_cast<const f4*>(&tq[hd * 256 + lane * 4]);
+            f4 t;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float x = u[0] * rk[0 * 4 + k];
+                x = fmaf(u[1], rk[1 * 4 + k], x);
+                x = fmaf(u[2], rk[2 * 4 + k], x);
+                x = fmaf(u[3], rk[3 * 4 + k], x);
+                t[k] = x;
+            }
+            *reinterpret_cast<f4*>(&tq[hd * 256 + lane * 4]) = t;
+        }
+        wave_sync();
+    }
+    __syncthreads();  // (1) shared tables and the staged rotor are in place
+
+    // A operands (rows: 2 hd = hi, 2 hd + 1 = lo of head hd; rows 12..15 zero)
+    const int arow_h = li >> 1;
+    const bool arow_lo = (li & 1) != 0;
+    const bool arow_ok = li < 12;
+    h8 At[8];
+#pragma unroll
+    for (int st = 0; st < 8; st++) {
+        f4 u0 = f4{0.f, 0.f, 0.f, 0.f}, u1 = u0;
+        if (arow_ok) {
+            u0 = *reinterpret_cast<const f4*>(&tq[arow_h * 256 + 64 * lg + 8 * st]);
+            u1 = *reinterpret_cast<const f4*>(&tq[arow_h * 256 + 64 * lg + 8 * st + 4]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            _Float16 hi, lo;
+            split(e < 4 ? u0[e] : u1[e - 4], hi, lo);
+            At[st][e] = arow_lo ? lo : hi;
+        }
+    }
+    // fold: z_(4q+c') = sum over blocks b of sum_k R_(16b+q)[c'][k] b_(64b+4q+k).
+    // K-step st carries q = 2 st + e/4 of block lg; M-tile T = st / 2 holds
+    // z rows of q = 4T .. 4T + 3, so the lane row li takes part in K-step st
+    // only when li / 8 == st % 2 (s_fold) and then only for e / 4 == (li / 4) % 2.
+    const _Float16* rk_lds = reinterpret_cast<const _Float16*>(S.vp);
+    const int s_fold = li >> 3;
+    h8 Aw[4];
+#pragma unroll
+    for (int T = 0; T < 4; T++) {
+        const int p = 16 * lg + 4 * T + (li >> 2);
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            Aw[T][e] = ((e >> 2) == ((li >> 2) & 1)) ? rk_lds[p * 16 + (li & 3) * 4 + (e & 3)]
+                                                     : (_Float16)0.0f;
+    }
+    const h8 hzero = {0, 0, 0, 0, 0, 0, 0, 0};
+    // H_64 = H_4 (x) H_16 (j = 16 T' + li, m = 16 T + 4 lg + c'):
+    // A[T'][kk] = H_4[T'][2 kk + e/4] * H_16[li][4 lg + (e & 3)] / 256; the
+    // sign of 1/d_j is applied to the output rows instead.
+    h8 Ag[2];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float g = ((__popc(li & (4 * lg + (e & 3))) & 1) ? -1.0f : 1.0f) / 256.0f;
+        Ag[0][e] = (_Float16)g;
+        Ag[1][e] = (_Float16)((e >> 2) ? -g : g);
+    }
+    float dsg[4][4];
+#pragma unroll
+    for (int Tp = 0; Tp < 4; Tp++)
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            dsg[Tp][c] = (__half2float(a.dk[16 * Tp + 4 * lg + c]) < 0.0f) ? -1.0f : 1.0f;
+    // q_rot (roped dims 0..63), K positions matching the rope'd key layout
+    h8 Aq[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int dim = 16 * (2 * kk + (e >> 2)) + 4 * lg + (e & 3);
+            _Float16 hi = (_Float16)0.0f, lo = (_Float16)0.0f;
+            if (arow_ok) split(__half2float(qbase[arow_h * 512 + dim]), hi, lo);
+            Aq[kk][e] = arow_lo ? lo : hi;
+        }
+    wave_sync();
+    // clear this lane's outlier strip (the query scratch is no longer needed)
+    _Float16* orow = &S.o[h][lane * O_LS];
+#pragma unroll
+    for (int i = 0; i < 8; i++) reinterpret_cast<uint4*>(orow)[i] = uint4{0, 0, 0, 0};
+
+    // ---- staging: mask words 4 lg .. 4 lg + 3 of (token li, head h) straight
+    // to registers; kpay rows through LDS; norms to registers.
+    const int kp_tok0 = lane / 5, kp_part0 = lane % 5;
+    const int kp_tok1 = (lane + 64) / 5, kp_part1 = (lane + 64) % 5;
+    uint4 m_nx = uint4{0, 0, 0, 0};
+    uint2 kp_nx0 = uint2{0, 0}, kp_nx1 = uint2{0, 0};
+    unsigned short nk_nx = 0, rs_nx = 0;
+    auto prefetch = [&](int s0) {
+        const int s = s0 + li;
+        const bool ok = s < s_hi;
+        const size_t row = (size_t)s * 4 + h;
+        m_nx = ok ? reinterpret_cast<const uint4*>(a.kmask + row * 16)[lg] : uint4{0, 0, 0, 0};
+        nk_nx = ok ? reinterpret_cast<const unsigned short*>(a.knorm)[row] : (unsigned short)0;
+        rs_nx = ok ? reinterpret_cast<const unsigned short*>(a.krn)[row] : (unsigned short)0;
+        kp_nx0 = (s0 + kp_tok0 < s_hi)
+                     ? reinterpret_cast<const uint2*>(a.kpay + ((size_t)(s0 + kp_tok0) * 4 + h) * 40)[kp_part0]
+                     : uint2{0, 0};
+        if (lane < 16)
+            kp_nx1 = (s0 + kp_tok1 < s_hi)
+                         ? reinterpret_cast<const uint2*>(a.kpay + ((size_t)(s0 + kp_tok1) * 4 + h) * 40)[kp_part1]
+                         : uint2{0, 0};
+    };
+    if (n_tiles > 0) prefetch(s_lo);
+
+    float bc[8], bs[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        bc[u] = 1.0f;
+        bs[u] = 0.0f;
+    }
+    float Mref[2] = {-INFINITY, -INFINITY};
+    float lsum[2] = {0.f, 0.f};
+    const _Float16* cbq = &S.cbk[64 * lg];
+    uint32_t* kpw = S.kp[h];
+
+    for (int it = 0; it <= n_tiles; it++) {
+        if (it < n_tiles) {
+            const int t = it;
+            const int s0 = s_lo + t * TT;
+            // ---- take the staged tile, start loading the next one
+            const uint4 mc = m_nx;
+            const float nk = __half2float(__ushort_as_half(nk_nx));
+            const float rs = __half2float(__ushort_as_half(rs_nx));
+            *reinterpret_cast<uint2*>(&kpw[kp_tok0 * KP_TS + kp_part0 * 2]) = kp_nx0;
+            if (lane < 16) *reinterpret_cast<uint2*>(&kpw[kp_tok1 * KP_TS + kp_part1 * 2]) = kp_nx1;
+            if (t + 1 < n_tiles) prefetch(s0 + TT);
+            if ((t & 15) == 0) {
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    sincos_rev((float)(a.start_pos + s0 + li) * S.rope[lg][0][u], bc[u], bs[u]);
+            }
+            wave_sync();
+
+            // ---- per-token scalars of this lane's token
+            const uint32_t* krow = &kpw[li * KP_TS];
+            float mult = (float)krow[0] / 1000.0f;
+            if (mult < 0.1f || mult > 10.0f || isnan(mult)) mult = 1.0f;
+            const float rr = rs / mult;
+
+            // ---- outliers of dims 64 lg .. 64 lg + 63: value sgn (cb + nib rr)
+            {
+                const uint32_t mw[4] = {mc.x, mc.y, mc.z, mc.w};
+                int cnt = 0;
+                uint64_t msk = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    uint32_t x = (mw[i] & (mw[i] >> 1)) & 0x55555555u;
+                    cnt += __popc(x);
+                    x = (x | (x >> 1)) & 0x33333333u;
+                    x = (x | (x >> 2)) & 0x0F0F0F0Fu;
+                    x = (x | (x >> 4)) & 0x00FF00FFu;
+                    x = (x | (x >> 8)) & 0x0000FFFFu;
+                    msk |= (uint64_t)x << (16 * i);
+                }
+                // ordinal of the first outlier: outliers of the quarters before
+                int incl = cnt;
+                int up = __shfl_up(incl, 16, 64);
+                if (lg >= 1) incl += up;
+                up = __shfl_up(incl, 32, 64);
+                if (lg >= 2) incl += up;
+                int j = incl - cnt;
+                // sign bits (bytes 29..35) and nibbles (bytes 4..28) in outlier
+                // order; only ordinals < 50 are stored (others: sign -1, residual 0)
+                const uint64_t signs = ((uint64_t)krow[7] | ((uint64_t)krow[8] << 32)) >> 8;
+                const int nv0 = max(0, min(64, 50 - j));
+                uint64_t sw = (j < 64 ? (signs >> j) : 0ull) &
+                              (nv0 >= 64 ? ~0ull : ((1ull << nv0) - 1ull));
+                uint64_t nw = 0;
+                int left = 0;
+                while (msk) {
+                    if (left == 0) {
+                        // 16 nibbles from ordinal j: bit 32 + 4 j of the row
+                        const int dwi = 1 + (j >> 3), sh = 4 * (j & 7);
+                        const uint64_t lo64 = (uint64_t)krow[min(dwi, 9)] |
+                                              ((uint64_t)krow[min(dwi + 1, 9)] << 32);
+                        const uint32_t d2 = krow[min(dwi + 2, 9)];
+                        nw = (lo64 >> sh) | (sh ? ((uint64_t)d2 << (64 - sh)) : 0ull);
+                        const int nvn = max(0, min(16, 50 - j));
+                        nw &= (nvn >= 16) ? ~0ull : ((1ull << (4 * nvn)) - 1ull);
+                        left = 16;
+                    }
+                    const int bpos = __builtin_ctzll(msk);
+                    msk &= msk - 1;
+                    const float r = fmaf((float)(uint32_t)(nw & 15ull), rr, (float)cbq[bpos]);
+                    orow[bpos] = (_Float16)((sw & 1ull) ? r : -r);
+                    nw >>= 4;
+                    sw >>= 1;
+                    left--;
+                    j++;
+                }
+            }
+
+            // ---- b operand + pass / fold MFMAs (the strip is cleared as read)
+            f4 cs = f4{0.f, 0.f, 0.f, 0.f};
+            f4 zt[4];
+#pragma unroll
+            for (int T = 0; T < 4; T++) zt[T] = f4{0.f, 0.f, 0.f, 0.f};
+            {
+                const uint32_t mw[4] = {mc.x, mc.y, mc.z, mc.w};
+#pragma unroll
+                for (int st = 0; st < 8; st++) {
+                    const uint32_t word = mw[st >> 1];
+                    const int sh = 16 * (st & 1);
+                    const uint2 sg0 = S.sgn[(word >> sh) & 0xFFu];
+                    const uint2 sg1 = S.sgn[(word >> (sh + 8)) & 0xFFu];
+                    const h8 cb8 = *reinterpret_cast<const h8*>(&cbq[8 * st]);
+                    const h8 o8 = *reinterpret_cast<const h8*>(&orow[8 * st]);
+                    *reinterpret_cast<uint4*>(&orow[8 * st]) = uint4{0, 0, 0, 0};
+                    const h4 s0v = __builtin_bit_cast(h4, sg0), s1v = __builtin_bit_cast(h4, sg1);
+                    const h8 sg = __builtin_shufflevector(s0v, s1v, 0, 1, 2, 3, 4, 5, 6, 7);
+                    const h8 bv = sg * cb8 + o8;
+                    cs = mfma32(At[st], bv, cs);
+                    zt[st >> 1] = mfma32((st & 1) == s_fold ? Aw[st >> 1] : hzero, bv, zt[st >> 1]);
+                }
+            }
+
+            // ---- H_64 (1/(256 d)) on z, split hi + lo
+            f4 kr[4];
+            {
+                h8 zb[4];
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const int T0 = e >> 2, c = e & 3;
+                    _Float16 a0, a1, a2, a3;
+                    split2(zt[T0][c], zt[T0][c + 1], a0, a1, a2, a3);
+                    zb[0][e] = a0; zb[0][e + 1] = a1; zb[2][e] = a2; zb[2][e + 1] = a3;
+                    split2(zt[2 + T0][c], zt[2 + T0][c + 1], a0, a1, a2, a3);
+                    zb[1][e] = a0; zb[1][e + 1] = a1; zb[3][e] = a2; zb[3][e + 1] = a3;
+                }
+                // H_4 rows: T'=0 [+ + + +], 1 [+ - + -], 2 [+ + - -], 3 [+ - - +]
+                const h8 A00 = Ag[0], A01 = Ag[1], A10 = -Ag[0], A11 = -Ag[1];
+#pragma unroll
+                for (int Tp = 0; Tp < 4; Tp++) {
+                    const h8 k0 = (Tp & 1) ? A01 : A00;
+                    const h8 k1 = (Tp == 0) ? A00 : (Tp == 1) ? A01 : (Tp == 2) ? A10 : A11;
+                    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+                    acc = mfma32(k0, zb[0], acc);
+                    acc = mfma32(k1, zb[1], acc);
+                    acc = mfma32(k0, zb[2], acc);
+                    acc = mfma32(k1, zb[3], acc);
+#pragma unroll
+                    for (int c = 0; c < 4; c++) acc[c] *= dsg[Tp][c];
+                    kr[Tp] = acc;
+                }
+            }
+
+            // ---- RoPE at absolute position start_pos + s0 + li
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int T0 = u >> 2, cc = u & 3;
+                const float x0 = kr[T0][cc], x1 = kr[T0 + 2][cc];
+                kr[T0][cc] = fmaf(x0, bc[u], -(x1 * bs[u]));
+                kr[T0 + 2][cc] = fmaf(x0, bs[u], x1 * bc[u]);
+            }
+
+            // ---- roped part of the score on MFMA (key split hi + lo)
+            {
+                h8 kb[4];
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const int T0 = e >> 2, c = e & 3;
+                    _Float16 a0, a1, a2, a3;
+                    split2(kr[T0][c], kr[T0][c + 1], a0, a1, a2, a3);
+                    kb[0][e] = a0; kb[0][e + 1] = a1; kb[2][e] = a2; kb[2][e + 1] = a3;
+                    split2(kr[2 + T0][c], kr[2 + T0][c + 1], a0, a1, a2, a3);
+                    kb[1][e] = a0; kb[1][e + 1] = a1; kb[3][e] = a2; kb[3][e + 1] = a3;
+                }
+                cs = mfma32(Aq[0], kb[0], cs);
+                cs = mfma32(Aq[1], kb[1], cs);
+                cs = mfma32(Aq[0], kb[2], cs);
+                cs = mfma32(Aq[1], kb[3], cs);
+            }
+
+            // ---- scores of heads 2 lg, 2 lg + 1 for token li
+            const bool tok_ok = (s0 + li) < s_hi;
+            const float fsc = a.a_k * nk * mult * a.sc;
+            float sc2[2];
+            sc2[0] = tok_ok ? (cs[0] + cs[1]) * fsc : -INFINITY;
+            sc2[1] = tok_ok ? (cs[2] + cs[3]) * fsc : -INFINITY;
+            if (lg == 3) {
+                sc2[0] = -INFINITY;
+                sc2[1] = -INFINITY;
+            }
+
+            // ---- softmax with a lazily raised reference maximum
+            float fac[2] = {1.0f, 1.0f};
+            float mx[2];
+#pragma unroll
+            for (int x = 0; x < 2; x++) mx[x] = row16_max(sc2[x]);
+            const bool need = (mx[0] > Mref[0] + RESCALE_GAP) || (mx[1] > Mref[1] + RESCALE_GAP);
+            if (__ballot(need) != 0ull) {
+#pragma unroll
+                for (int x = 0; x < 2; x++) {
+                    const bool upx = mx[x] > Mref[x] + RESCALE_GAP;
+                    const float nm = upx ? mx[x] : Mref[x];
+                    fac[x] = (nm == -INFINITY) ? 1.0f : fexp(Mref[x] - nm);
+                    Mref[x] = nm;
+                    lsum[x] *= fac[x];
+                }
+            }
+            const int buf = t & 1;
+#pragma unroll
+            for (int x = 0; x < 2; x++) {
+                const float pr = (sc2[x] == -INFINITY) ? 0.0f : fexp(sc2[x] - Mref[x]);
+                lsum[x] += pr;
+                if (lg < 3) S.pw[buf][h][2 * lg + x][li] = pr;
+            }
+            if (li == 0 && lg < 3) {
+                S.fac[buf][h][2 * lg] = fac[0];
+                S.fac[buf][h][2 * lg + 1] = fac[1];
+            }
+
+            // ---- advance the lane's RoPE angles by 16 tokens
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const float sc16 = S.rope[lg][1][u], ss16 = S.rope[lg][2][u];
+                const float nc = fmaf(bc[u], sc16, -(bs[u] * ss16));
+                const float ns = fmaf(bs[u], sc16, bc[u] * ss16);
+                bc[u] = nc;
+                bs[u] = ns;
+            }
+        }
+        __syncthreads();  // (2) tile hand-off
+    }
+
+    // ---- epilogue: (max, sum) per query head
+#pragma unroll
+    for (int x = 0; x < 2; x++) lsum[x] = row16_sum(lsum[x]);
+    if (li == 0 && lg < 3) {
+#pragma unroll
+        for (int x = 0; x < 2; x++) {
+            S.ml[h][2 * lg + x][0] = Mref[x];
+            S.ml[h][2 * lg + x][1] = lsum[x];
+        }
+    }
+    __syncthreads();  // (3) maxima / sums / dump sums published
+    __syncthreads();  // (4) V sums in place
+}
+
+// -------------------------------------------------------------- value role
+__device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, int h, int lane,
+                                           int s_lo, int s_hi, int n_tiles) {
+    const int li = lane & 15, lg = lane >> 4;
+    __syncthreads();  // (1)
+
+    // lane constants: patch p = 16 g + li for g = 0..3
+    const _Float16* cvh = reinterpret_cast<const _Float16*>(a.cents_v);
+    _Float16 c3a[4], c3b[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const int p = 16 * g + li;
+        c3a[g] = cvh[p * 4 + 3];
+        c3b[g] = cvh[256 + p * 4 + 3];
+    }
+    const int r_head = li >> 1;       // A row li: head li / 2, hi (even) or lo (odd)
+    const bool r_lo = (li & 1) != 0;
+    const bool r_ok = li < 12;
+
+    // staging: vpay rows (13 uint2 per token) by lane, norms of token li
+    int vp_tok[4], vp_part[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        vp_tok[k] = (lane + 64 * k) / 13;
+        vp_part[k] = (lane + 64 * k) % 13;
+    }
+    uint2 vp_nx[4];
+    unsigned short vn_nx = 0, ve_nx = 0;
+    float vm_nx = 0.0f;
+    auto prefetch = [&](int s0) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int tok = vp_tok[k];
+            vp_nx[k] = (lane + 64 * k < TT * 13 && s0 + tok < s_hi)
+                           ? reinterpret_cast<const uint2*>(a.vpay + ((size_t)(s0 + tok) * 4 + h) * 104)[vp_part[k]]
+                           : uint2{0, 0};
+        }
+        const int s = s0 + li;
+        const bool ok = s < s_hi;
+        const size_t row = (size_t)s * 4 + h;
+        vn_nx = ok ? reinterpret_cast<const unsigned short*>(a.vnorm)[row] : (unsigned short)0;
+        ve_nx = ok ? reinterpret_cast<const unsigned short*>(a.vrn)[row] : (unsigned short)0;
+        vm_nx = ok ? reinterpret_cast<const float*>(a.vsm)[row] : 0.0f;
+    };
+    if (n_tiles > 0) prefetch(s_lo);
+
+    f4 pv[20];
+#pragma unroll
+    for (int n = 0; n < 20; n++) pv[n] = f4{0.f, 0.f, 0.f, 0.f};
+    float s3p = 0.0f;  // sum of w * norm * smeta / 7 over this lane's tokens (hi rows)
+    const float av = a.a_v;
+    uint32_t* vpw = S.vp[h];
+
+    for (int it = 0; it <= n_tiles; it++) {
+        if (it >= 1) {
+            const int t = it - 1;
+            const int buf = t & 1;
+            // ---- take the staged tile, start loading the next one
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                if (lane + 64 * k < TT * 13)
+                    *reinterpret_cast<uint2*>(&vpw[vp_tok[k] * VP_TS + vp_part[k] * 2]) = vp_nx[k];
+            if (lg == 0) {
+                const float nv = __half2float(__ushort_as_half(vn_nx));
+                const float en = __half2float(__ushort_as_half(ve_nx));
+                S.vsc[h][0][li] = (av * nv) * en;
+                S.vsc[h][1][li] = av * nv;
+                S.vsc[h][2][li] = nv * vm_nx / 7.0f;
+            }
+            if (t + 1 < n_tiles) prefetch(s_lo + (t + 1) * TT);
+            wave_sync();
+
+            // ---- rescale for a raised maximum (rows 4 lg + c: head 2 lg + c / 2)
+            {
+                const float f0 = lg < 3 ? S.fac[buf][h][2 * lg] : 1.0f;
+                const float f1 = lg < 3 ? S.fac[buf][h][2 * lg + 1] : 1.0f;
+                const float fr = r_ok ? S.fac[buf][h][r_head] : 1.0f;
+                if (__ballot(f0 != 1.0f || f1 != 1.0f || fr != 1.0f) != 0ull) {
+#pragma unroll
+                    for (int n = 0; n < 20; n++) {
+                        pv[n][0] *= f0;
+                        pv[n][1] *= f0;
+                        pv[n][2] *= f1;
+                        pv[n][3] *= f1;
+                    }
+                    s3p *= fr;
+                }
+            }
+
+            // ---- weights x V scalings -> A operands (rows head hi/lo, K = tokens 4 lg..)
+            h4 Ap[3];
+            {
+                f4 pw4 = f4{0.f, 0.f, 0.f, 0.f};
+                if (r_ok) pw4 = *reinterpret_cast<const f4*>(&S.pw[buf][h][r_head][4 * lg]);
+#pragma unroll
+                for (int v = 0; v < 3; v++) {
+                    const f4 sv = *reinterpret_cast<const f4*>(&S.vsc[h][v][4 * lg]);
+                    const f4 w = pw4 * sv;
+                    if (v == 2 && !r_lo) s3p += (w[0] + w[1]) + (w[2] + w[3]);
+#pragma unroll
+                    for (int e = 0; e < 4; e += 2) {
+                        _Float16 h0, h1, l0, l1;
+                        split2(w[e], w[e + 1], h0, h1, l0, l1);
+                        Ap[v][e] = r_lo ? l0 : h0;
+                        Ap[v][e + 1] = r_lo ? l1 : h1;
+                    }
+                }
+            }
+
+            // ---- decode V straight into B operands, P x V on MFMA
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int p = 16 * g + li;
+                const int vbit = 12 * (p & 7);
+                const int vw0 = (p >> 3) * 3 + (vbit >> 5);
+                const int vsh = vbit & 31;
+                const int vhw = 24 + (g >> 1), vhb = p & 31;
+                h4 b0, b1, b2, b3, b4;
+#pragma unroll
+                for (int tt = 0; tt < 4; tt++) {
+                    const uint32_t* vr = &vpw[(4 * lg + tt) * VP_TS];
+                    const uint32_t fld = __builtin_amdgcn_alignbit(vr[vw0 + 1], vr[vw0], vsh) & 0xFFFu;
+                    const uint32_t code = (fld & 0x7Fu) | (__builtin_amdgcn_ubfe(vr[vhw], vhb, 1) << 7);
+                    const _Float16* ce = &S.cb[p * CB_PS + code * 3];
+                    b0[tt] = ce[0];
+                    b1[tt] = ce[1];
+                    b2[tt] = ce[2];
+                    b3[tt] = ((fld >> 7) & 1u) ? c3b[g] : c3a[g];
+                    b4[tt] = (_Float16)(unsigned short)((fld >> 8) & 0xFu);
+                }
+                pv[5 * g + 0] = mfma16(Ap[0], b0, pv[5 * g + 0]);
+                pv[5 * g + 1] = mfma16(Ap[0], b1, pv[5 * g + 1]);
+                pv[5 * g + 2] = mfma16(Ap[0], b2, pv[5 * g + 2]);
+                pv[5 * g + 3] = mfma16(Ap[1], b3, pv[5 * g + 3]);
+                pv[5 * g + 4] = mfma16(Ap[2], b4, pv[5 * g + 4]);
+            }
+        }
+        __syncthreads();  // (2) tile hand-off
+    }
+
+    // ---- epilogue: dump sums per head (hi rows li = 2 hd, all lane groups)
+    s3p += __shfl_xor(s3p, 16, 64);
+    s3p += __shfl_xor(s3p, 32, 64);
+    if (lg == 0 && r_ok && !r_lo) S.s3[h][r_head] = s3p;
+    __syncthreads();  // (3)
+    // rotated-domain sums [6][256] in the key strip area of this KV head
+    float* ep = reinterpret_cast<float*>(S.o[h]);
+    if (lg < 3) {
+#pragma unroll
+        for (int x = 0; x < 2; x++) {
+            const int hd = 2 * lg + x;
+            const float off = 8.0f * S.s3[h][hd];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int p = 16 * g + li;
+#pragma unroll
+                for (int k = 0; k < 3; k++)
+                    ep[hd * 256 + 4 * p + k] = pv[5 * g + k][2 * x] + pv[5 * g + k][2 * x + 1];
+                ep[hd * 256 + 4 * p + 3] = (pv[5 * g + 3][2 * x] + pv[5 * g + 3][2 * x + 1]) +
+                                           (pv[5 * g + 4][2 * x] + pv[5 * g + 4][2 * x + 1]) - off;
+            }
+        }
+    }
+    __syncthreads();  // (4)
+}
+
+__global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_per_chunk) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    Smem& S = *reinterpret_cast<Smem*>(smem_raw);
+    const int tid = threadIdx.x;
+    const int wv = tid >> 6;
+    const int h = wv & 3;
+    const int lane = tid & 63;
+    const int chunk = blockIdx.x;
+    const int c_len = a.c_len;
+    const int s_lo = min(chunk * tiles_per_chunk * TT, c_len);
+    const int s_hi = min(s_lo + tiles_per_chunk * TT, c_len);
+    const int n_tiles = (s_hi - s_lo + TT - 1) / TT;
+
+    // ---- shared tables: codebook, sign table, cents_k[2], rotor_k, RoPE
+    {
+        const uint4* src = reinterpret_cast<const uint4*>(a.vq);
+        uint4* dst = reinterpret_cast<uint4*>(S.cb);
+        uint4 tmp[12];
+#pragma unroll
+        for (int i = 0; i < 12; i++) tmp[i] = src[tid + NTHR * i];
+#pragma unroll
+        for (int i = 0; i < 12; i++) dst[tid + NTHR * i] = tmp[i];
+        if (tid < 256) {
+            h4 s;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int code = (tid >> (2 * c)) & 3;
+                s[c] = code == 2 ? (_Float16)1.0f : (code == 1 ? (_Float16)-1.0f : (_Float16)0.0f);
+            }
+            S.sgn[tid] = __builtin_bit_cast(uint2, s);
+            S.cbk[tid] = reinterpret_cast<const _Float16*>(a.cents_k)[512 + tid];
+        } else if (tid < 256 + 128) {
+            reinterpret_cast<uint4*>(&S.vp[0][0])[tid - 256] =
+                reinterpret_cast<const uint4*>(a.rotor_k)[tid - 256];
+        } else if (tid >= 448) {
+            // lanes (u, lg) with u < 8 of the last wavefront: RoPE table
+            const int l = tid - 448, u = l & 15, g = l >> 4;
+            if (u < 8) {
+                const int m = 16 * (u >> 2) + 4 * g + (u & 3);
+                const float f = powf(a.rope_base, -2.0f * (float)m / 64.0f);
+                S.rope[g][0][u] = f;
+                S.rope[g][1][u] = cosf(16.0f * f);
+                S.rope[g][2][u] = sinf(16.0f * f);
+            }
+        }
+    }
+
+    if (wv < 4) {
+        key_role(a, S, h, lane, s_lo, s_hi, n_tiles);
+    } else {
+        value_role(a, S, h, lane, s_lo, s_hi, n_tiles);
+    }
+
+    // ---- output: wavefront wv handles query heads 3 (wv / 4) .. + 2 of KV head h
+    const float* ep = reinterpret_cast<const float*>(S.o[h]);
+    float rv[16];
+#pragma unroll
+    for (int t = 0; t < 16; t++) rv[t] = __half2float(a.rotor_v[lane * 16 + t]);
+    for (int hh = 0; hh < 3; hh++) {
+        const int hd = 3 * (wv >> 2) + hh;
+        float o[4], u[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) o[c] = ep[hd * 256 + lane * 4 + c];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float t = o[0] * rv[c * 4 + 0];
+            t = fmaf(o[1], rv[c * 4 + 1], t);
+            t = fmaf(o[2], rv[c * 4 + 2], t);
+            t = fmaf(o[3], rv[c * 4 + 3], t);
+            u[c] = t;
+        }
+        fwht256(u, lane);
+        const int hq = h * 6 + hd;
+        float* out = a.part + ((size_t)hq * a.part_stride + a.part_offset + chunk) * 258;
+        const float M = S.ml[h][hd][0];
+        const float L = S.ml[h][hd][1];
+        const bool empty = (M == -INFINITY);
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            out[lane * 4 + c] =
+                empty ? 0.0f : (u[c] * (1.0f / 16.0f)) / (__half2float(a.dv[lane * 4 + c]) + 1e-8f);
+        if (lane == 0) {
+            out[256] = empty ? -1e20f : M;
+            out[257] = empty ? 0.0f : L;
+        }
+    }
+}
+
+}  // namespace ws
+
+size_t attn_ws_smem_bytes() { return sizeof(ws::Smem); }
+
+hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks, hipStream_t st) {
+    static bool configured = false;
+    const size_t smem = sizeof(ws::Smem);
+    if (!configured) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ws::attn_ws_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        if (e != hipSuccess) return e;
+        configured = true;
+    }
+    hipLaunchKernelGGL(ws::attn_ws_kernel, dim3(n_chunks), dim3(ws::NTHR), smem, st, a,
+                       tiles_per_chunk);
+    return hipGetLastError();
+}
+
+}  // namespace khq

@@ -45,12 +45,13 @@ hipError_t workspace(size_t bytes, float** out) {
     return hipSuccess;
 }
 
-// 0 = automatic (matrix-core kernel for the 24/4/256 shape), 1 = portable
-// lane-per-patch kernel for every shape.
+// 0 = automatic (wavefront-specialised matrix-core kernel for the 24/4/256
+// shape), 1 = portable lane-per-patch kernel for every shape, 2 = the
+// single-role matrix-core kernel for the 24/4/256 shape.
 int g_kernel_choice = 0;
 
 bool use_mfma(int n_rep, int h_kv, int L_q) {
-    return g_kernel_choice == 0 && n_rep == 6 && h_kv == 4 && L_q == 1;
+    return g_kernel_choice != 1 && n_rep == 6 && h_kv == 4 && L_q == 1;
 }
 
 // Launches the compressed-region partials of query heads into part
@@ -61,7 +62,8 @@ hipError_t launch_compressed(khq::AttnArgs a, int n_rep, int L_q, int* parts_use
         int n_chunks = 0;
         const int per = khq::attn_mfma_tiles_per_chunk(a.c_len, &n_chunks);
         *parts_used = n_chunks;
-        return khq::launch_attn_mfma(a, per, n_chunks, stream);
+        if (g_kernel_choice == 2) return khq::launch_attn_mfma(a, per, n_chunks, stream);
+        return khq::launch_attn_ws(a, per, n_chunks, stream);
     }
     *parts_used = a.n_parts;
     return khq::launch_attn_parts(a, n_rep, dim3(a.n_parts, a.h_kv, L_q), stream);
@@ -114,7 +116,7 @@ const char* khq_version(void) { return "khq-mi355x 0.1 (gfx950)"; }
 int khq_attn_parts(int c_len) { return compressed_parts(c_len, 6, 4, 1); }
 
 int khq_select_kernel(int which) {
-    if (which < 0 || which > 1) return -100;
+    if (which < 0 || which > 2) return -100;
     g_kernel_choice = which;
     return 0;
 }

@@ -67,5 +67,9 @@ size_t attn_mfma_smem_bytes();
 int attn_mfma_tiles_per_chunk(int c_len, int* n_chunks);
 hipError_t launch_attn_mfma(const AttnArgs& a, int tiles_per_chunk, int n_chunks,
                             hipStream_t st);
+// Wavefront-specialised variant of the same contract (512 threads per block).
+size_t attn_ws_smem_bytes();
+hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks,
+                          hipStream_t st);
 
 }  // namespace khq

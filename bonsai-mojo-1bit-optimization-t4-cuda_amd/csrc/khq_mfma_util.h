@@ -1,0 +1,135 @@
+// khq_mfma_util.h -- device helpers shared by the matrix-core KHQ kernels
+// (gfx950: 64-lane wavefronts, 16x16x32 / 16x16x16 f16 MFMA).
+//
+// MFMA operand layouts (lane l, li = l % 16, lg = l / 16):
+//   16x16x32 f16: A lane holds A[li][8 lg .. 8 lg + 7], B lane holds
+//                 B[8 lg .. 8 lg + 7][li], C lane holds C[4 lg .. 4 lg + 3][li];
+//   16x16x16 f16: the same with 4 K values per lane (4 lg .. 4 lg + 3).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace khq {
+namespace mu {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f4 mfma32(h8 a, h8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// Orders this wavefront's LDS traffic (lanes exchange data through LDS).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Cross-lane moves inside a 16-lane row (DPP, no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// max / sum over the 16 lanes of a row: xor 1, xor 2 (quad_perm), then
+// row_half_mirror and row_mirror fold the quads and the half rows.
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x141>(v));
+    v = fmaxf(v, dpp<0x140>(v));
+    return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x141>(v);
+    v += dpp<0x140>(v);
+    return v;
+}
+
+// cos / sin of an fp32 angle (radians): exact reduction to [-1/2, 1/2]
+// revolutions in fp64, then the hardware sine/cosine (revolution input).
+__device__ __forceinline__ void sincos_rev(float th, float& c, float& s) {
+    double r = (double)th * 0.15915494309189535;  // 1 / (2 pi)
+    r -= rint(r);
+    const float rf = (float)r;
+    c = __builtin_amdgcn_cosf(rf);
+    s = __builtin_amdgcn_sinf(rf);
+}
+
+__device__ __forceinline__ float fexp(float x) { return __expf(x); }
+
+// hi + lo fp16 split of two floats (hi truncated, lo carries the rest).
+__device__ __forceinline__ void split2(float x, float y, _Float16& xh, _Float16& yh,
+                                       _Float16& xl, _Float16& yl) {
+    const h2 hi = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x, y));
+    const h2 lo = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x - (float)hi[0], y - (float)hi[1]));
+    xh = hi[0];
+    yh = hi[1];
+    xl = lo[0];
+    yl = lo[1];
+}
+
+__device__ __forceinline__ void split(float x, _Float16& hi, _Float16& lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+
+// Unnormalised FWHT-256 across a wavefront holding 4 consecutive dims per lane.
+__device__ __forceinline__ void fwht256(float (&v)[4], int lane) {
+    float a = v[0], b = v[1];
+    v[0] = a + b; v[1] = a - b;
+    a = v[2]; b = v[3];
+    v[2] = a + b; v[3] = a - b;
+    a = v[0]; b = v[2];
+    v[0] = a + b; v[2] = a - b;
+    a = v[1]; b = v[3];
+    v[1] = a + b; v[3] = a - b;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const bool lower = (lane & m) == 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float p = __shfl_xor(v[c], m, 64);
+            v[c] = lower ? (v[c] + p) : (p - v[c]);
+        }
+    }
+}
+
+// Two 16-point FWHT passes in LDS over n_vec vectors of 256 floats
+// (dim = 16 hi + lo: first along lo, then along hi), by one wavefront.
+__device__ __forceinline__ void fwht256_lds(float* v, int n_vec, int lane) {
+#pragma unroll
+    for (int pass = 0; pass < 2; pass++) {
+        for (int item = lane; item < n_vec * 16; item += 64) {
+            const int h = item >> 4, r = item & 15;
+            const int base = h * 256 + (pass == 0 ? r * 16 : r);
+            const int step = pass == 0 ? 1 : 16;
+            float x[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) x[i] = v[base + i * step];
+#pragma unroll
+            for (int m = 1; m < 16; m <<= 1)
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    if ((i & m) == 0) {
+                        const float p = x[i], q = x[i + m];
+                        x[i] = p + q;
+                        x[i + m] = p - q;
+                    }
+#pragma unroll
+            for (int i = 0; i < 16; i++) v[base + i * step] = x[i];
+        }
+        wave_sync();
+    }
+}
+
+}  // namespace mu
+}  // namespace khq

@@ -20,9 +20,10 @@ pytestmark = pytest.mark.gpu
 ATOL, RTOL = 2e-3, 1e-3
 
 
-@pytest.fixture(params=[0, 1], ids=["auto", "portable"])
+@pytest.fixture(params=[0, 1, 2], ids=["auto", "portable", "mfma-single"])
 def kernel(request, device):
-    """Runs a test with the automatic (matrix-core) and the portable kernel."""
+    """Runs a test with each compressed-region kernel: automatic (wavefront-
+    specialised matrix-core), portable, and the single-role matrix-core one."""
     from khq import _lib
 
     _lib.call("khq_select_kernel", request.param)
