@@ -43,6 +43,23 @@ namespace ws {
 
 using namespace mu;
 
+#ifdef KHQ_PHASE_TIMING
+__device__ unsigned long long phase_cycles[16];
+__device__ unsigned long long block_times[1024][2];
+#define PHASE(k)                                                              \
+    do {                                                                      \
+        const unsigned long long now_ = __builtin_amdgcn_s_memtime();         \
+        ph_acc[k] += (unsigned)(now_ - ph_t);                                 \
+        ph_t = now_;                                                          \
+    } while (0)
+#define PH_PARAMS , unsigned long long ph_t, unsigned (&ph_acc)[16]
+#define PH_ARGS , ph_t, ph_acc
+#else
+#define PHASE(k) do { } while (0)
+#define PH_PARAMS
+#define PH_ARGS
+#endif
+
 constexpr int TT = 16;          // tokens per tile
 constexpr int NTHR = 512;       // 4 key + 4 value wavefronts
 constexpr int CB_PS = 768;      // halves per codebook patch (256 codes x 3)
@@ -64,69 +81,128 @@ struct __align__(16) Smem {
     float fac[2][4][8];          // rescale factors of the same tile
     float vsc[4][3][TT];         // per token V scalings
     float rope[4][3][8];         // per lane group: freq, cos(16 f), sin(16 f)
+    _Float16 rotv[64 * 16];      // rotor_v
+    _Float16 dvh[256];           // d_v
+    _Float16 c3v[2][64];         // cents_v[c][4 p + 3]
     float ml[4][6][2];           // final (max, sum) per query head
     float s3[4][8];              // final dump-offset sums per query head
 };
 
+// Query side of the pass part for 3 query heads of KV head h (heads hd0 ..
+// hd0 + 2): tq_hd = R^T H (q_hd[64:] / (256 d)) into S.o[h] as floats [6][256].
+__device__ __forceinline__ void query_transform(const AttnArgs& a, Smem& S, int h, int hd0,
+                                                int lane) {
+    const __half* qbase = a.q + (size_t)(h * 6 + hd0) * 512;
+    float* tq = reinterpret_cast<float*>(S.o[h]) + hd0 * 256;
+    float dks[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        dks[c] = (1.0f / 256.0f) / (__half2float(a.dk[lane * 4 + c]) + 1e-8f);
+#pragma unroll
+    for (int hd = 0; hd < 3; hd++) {
+        const uint2 qr = *reinterpret_cast<const uint2*>(qbase + hd * 512 + lane * 4);
+        const __half* qh = reinterpret_cast<const __half*>(&qr);
+        f4 v;
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[c] = lane >= 16 ? __half2float(qh[c]) * dks[c] : 0.0f;
+        *reinterpret_cast<f4*>(&tq[hd * 256 + lane * 4]) = v;
+    }
+    wave_sync();
+    fwht256_lds(tq, 3, lane);
+    float rk[16];
+    {
+        const uint4* rp = reinterpret_cast<const uint4*>(a.rotor_k + lane * 16);
+        const uint4 r0 = rp[0], r1 = rp[1];
+        const __half* rh0 = reinterpret_cast<const __half*>(&r0);
+        const __half* rh1 = reinterpret_cast<const __half*>(&r1);
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            rk[t] = __half2float(rh0[t]);
+            rk[8 + t] = __half2float(rh1[t]);
+        }
+    }
+    // per patch: t[4p + k] = sum_c u[4p + c] R_p[c][k]
+#pragma unroll
+    for (int hd = 0; hd < 3; hd++) {
+        const f4 u = *reinterpret_cast<const f4*>(&tq[hd * 256 + lane * 4]);
+        f4 t;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float x = u[0] * rk[0 * 4 + k];
+            x = fmaf(u[1], rk[1 * 4 + k], x);
+            x = fmaf(u[2], rk[2 * 4 + k], x);
+            x = fmaf(u[3], rk[3 * 4 + k], x);
+            t[k] = x;
+        }
+        *reinterpret_cast<f4*>(&tq[hd * 256 + lane * 4]) = t;
+    }
+}
+
 // ---------------------------------------------------------------- key role
 __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int lane,
-                                         int s_lo, int s_hi, int n_tiles) {
+                                         int s_lo, int s_hi, int n_tiles PH_PARAMS) {
     const int li = lane & 15, lg = lane >> 4;
-    const __half* qbase = a.q + (size_t)(h * 6) * 512;
-
-    // ---- query side: tq_h = R^T H (q_h[64:] / (256 d)) in the strip area
-    float* tq = reinterpret_cast<float*>(S.o[h]);  // [6][256]
-    {
-        float dks[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-            dks[c] = (1.0f / 256.0f) / (__half2float(a.dk[lane * 4 + c]) + 1e-8f);
-#pragma unroll
-        for (int hd = 0; hd < 6; hd++) {
-            const uint2 qr = *reinterpret_cast<const uint2*>(qbase + hd * 512 + lane * 4);
-            const __half* qh = reinterpret_cast<const __half*>(&qr);
-            f4 v;
-#pragma unroll
-            for (int c = 0; c < 4; c++) v[c] = lane >= 16 ? __half2float(qh[c]) * dks[c] : 0.0f;
-            *reinterpret_cast<f4*>(&tq[hd * 256 + lane * 4]) = v;
-        }
-        wave_sync();
-        fwht256_lds(tq, 6, lane);
-        float rk[16];
-        {
-            const uint4* rp = reinterpret_cast<const uint4*>(a.rotor_k + lane * 16);
-            const uint4 r0 = rp[0], r1 = rp[1];
-            const __half* rh0 = reinterpret_cast<const __half*>(&r0);
-            const __half* rh1 = reinterpret_cast<const __half*>(&r1);
-#pragma unroll
-            for (int t = 0; t < 8; t++) {
-                rk[t] = __half2float(rh0[t]);
-                rk[8 + t] = __half2float(rh1[t]);
-            }
-        }
-        // per patch: t[4p + k] = sum_c u[4p + c] R_p[c][k]
-#pragma unroll
-        for (int hd = 0; hd < 6; hd++) {
-            const f4 u = *reinterpret_cast<const f4*>(&tq[hd * 256 + lane * 4]);
-            f4 t;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                float x = u[0] * rk[0 * 4 + k];
-                x = fmaf(u[1], rk[1 * 4 + k], x);
-                x = fmaf(u[2], rk[2 * 4 + k], x);
-                x = fmaf(u[3], rk[3 * 4 + k], x);
-                t[k] = x;
-            }
-            *reinterpret_cast<f4*>(&tq[hd * 256 + lane * 4]) = t;
-        }
-        wave_sync();
-    }
-    __syncthreads();  // (1) shared tables and the staged rotor are in place
+    const float* tq = reinterpret_cast<const float*>(S.o[h]);  // [6][256] query transforms
 
     // A operands (rows: 2 hd = hi, 2 hd + 1 = lo of head hd; rows 12..15 zero)
     const int arow_h = li >> 1;
     const bool arow_lo = (li & 1) != 0;
     const bool arow_ok = li < 12;
+    // output-row signs of 1/d (rows j = 16 T' + 4 lg + c') and q_rot (roped
+    // dims 0..63 at the K positions of the rope'd key layout); unconditional
+    // vector loads from a clamped head row, zeroed rows applied afterwards
+    float dsg[4][4];
+    h8 Aq[2];
+    {
+        uint2 dr[4], qv[4];
+        const __half* qrow = a.q + (size_t)(h * 6 + min(arow_h, 5)) * 512;
+#pragma unroll
+        for (int Tp = 0; Tp < 4; Tp++) {
+            dr[Tp] = *reinterpret_cast<const uint2*>(a.dk + 16 * Tp + 4 * lg);
+            qv[Tp] = *reinterpret_cast<const uint2*>(qrow + 16 * Tp + 4 * lg);
+        }
+#pragma unroll
+        for (int Tp = 0; Tp < 4; Tp++) {
+            const h4 d4 = __builtin_bit_cast(h4, dr[Tp]);
+#pragma unroll
+            for (int c = 0; c < 4; c++) dsg[Tp][c] = ((float)d4[c] < 0.0f) ? -1.0f : 1.0f;
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const h4 q4 = __builtin_bit_cast(h4, qv[2 * kk + (e >> 2)]);
+                _Float16 hi, lo;
+                split((float)q4[e & 3], hi, lo);
+                Aq[kk][e] = arow_ok ? (arow_lo ? lo : hi) : (_Float16)0.0f;
+            }
+    }
+    // ---- staging: mask words 4 lg .. 4 lg + 3 of (token li, head h) straight
+    // to registers; kpay rows through LDS; norms to registers.
+    const int kp_tok0 = lane / 5, kp_part0 = lane % 5;
+    const int kp_tok1 = min(lane + 64, 79) / 5, kp_part1 = min(lane + 64, 79) % 5;
+    // Prefetches read clamped (always valid) rows unconditionally, so no load
+    // sits in a branch; which rows are real is applied when the tile is taken.
+    uint4 m_nx = uint4{0, 0, 0, 0};
+    uint2 kp_nx0 = uint2{0, 0}, kp_nx1 = uint2{0, 0};
+    unsigned short nk_nx = 0, rs_nx = 0;
+    auto prefetch = [&](int s0) {
+        const int last = s_hi - 1;
+        const size_t row = (size_t)min(s0 + li, last) * 4 + h;
+        m_nx = reinterpret_cast<const uint4*>(a.kmask + row * 16)[lg];
+        nk_nx = reinterpret_cast<const unsigned short*>(a.knorm)[row];
+        rs_nx = reinterpret_cast<const unsigned short*>(a.krn)[row];
+        kp_nx0 = reinterpret_cast<const uint2*>(
+            a.kpay + ((size_t)min(s0 + kp_tok0, last) * 4 + h) * 40)[kp_part0];
+        kp_nx1 = reinterpret_cast<const uint2*>(
+            a.kpay + ((size_t)min(s0 + kp_tok1, last) * 4 + h) * 40)[kp_part1];
+    };
+    if (n_tiles > 0) prefetch(s_lo);
+    query_transform(a, S, h, 0, lane);
+
+    __syncthreads();  // (1) tables, staged rotors and query transforms in place
+    PHASE(1);
+
     h8 At[8];
 #pragma unroll
     for (int st = 0; st < 8; st++) {
@@ -168,52 +244,11 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
         Ag[0][e] = (_Float16)g;
         Ag[1][e] = (_Float16)((e >> 2) ? -g : g);
     }
-    float dsg[4][4];
-#pragma unroll
-    for (int Tp = 0; Tp < 4; Tp++)
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-            dsg[Tp][c] = (__half2float(a.dk[16 * Tp + 4 * lg + c]) < 0.0f) ? -1.0f : 1.0f;
-    // q_rot (roped dims 0..63), K positions matching the rope'd key layout
-    h8 Aq[2];
-#pragma unroll
-    for (int kk = 0; kk < 2; kk++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const int dim = 16 * (2 * kk + (e >> 2)) + 4 * lg + (e & 3);
-            _Float16 hi = (_Float16)0.0f, lo = (_Float16)0.0f;
-            if (arow_ok) split(__half2float(qbase[arow_h * 512 + dim]), hi, lo);
-            Aq[kk][e] = arow_lo ? lo : hi;
-        }
     wave_sync();
     // clear this lane's outlier strip (the query scratch is no longer needed)
     _Float16* orow = &S.o[h][lane * O_LS];
 #pragma unroll
     for (int i = 0; i < 8; i++) reinterpret_cast<uint4*>(orow)[i] = uint4{0, 0, 0, 0};
-
-    // ---- staging: mask words 4 lg .. 4 lg + 3 of (token li, head h) straight
-    // to registers; kpay rows through LDS; norms to registers.
-    const int kp_tok0 = lane / 5, kp_part0 = lane % 5;
-    const int kp_tok1 = (lane + 64) / 5, kp_part1 = (lane + 64) % 5;
-    uint4 m_nx = uint4{0, 0, 0, 0};
-    uint2 kp_nx0 = uint2{0, 0}, kp_nx1 = uint2{0, 0};
-    unsigned short nk_nx = 0, rs_nx = 0;
-    auto prefetch = [&](int s0) {
-        const int s = s0 + li;
-        const bool ok = s < s_hi;
-        const size_t row = (size_t)s * 4 + h;
-        m_nx = ok ? reinterpret_cast<const uint4*>(a.kmask + row * 16)[lg] : uint4{0, 0, 0, 0};
-        nk_nx = ok ? reinterpret_cast<const unsigned short*>(a.knorm)[row] : (unsigned short)0;
-        rs_nx = ok ? reinterpret_cast<const unsigned short*>(a.krn)[row] : (unsigned short)0;
-        kp_nx0 = (s0 + kp_tok0 < s_hi)
-                     ? reinterpret_cast<const uint2*>(a.kpay + ((size_t)(s0 + kp_tok0) * 4 + h) * 40)[kp_part0]
-                     : uint2{0, 0};
-        if (lane < 16)
-            kp_nx1 = (s0 + kp_tok1 < s_hi)
-                         ? reinterpret_cast<const uint2*>(a.kpay + ((size_t)(s0 + kp_tok1) * 4 + h) * 40)[kp_part1]
-                         : uint2{0, 0};
-    };
-    if (n_tiles > 0) prefetch(s_lo);
 
     float bc[8], bs[8];
 #pragma unroll
@@ -225,17 +260,22 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
     float lsum[2] = {0.f, 0.f};
     const _Float16* cbq = &S.cbk[64 * lg];
     uint32_t* kpw = S.kp[h];
+    PHASE(1);
 
     for (int it = 0; it <= n_tiles; it++) {
         if (it < n_tiles) {
             const int t = it;
             const int s0 = s_lo + t * TT;
             // ---- take the staged tile, start loading the next one
-            const uint4 mc = m_nx;
-            const float nk = __half2float(__ushort_as_half(nk_nx));
-            const float rs = __half2float(__ushort_as_half(rs_nx));
-            *reinterpret_cast<uint2*>(&kpw[kp_tok0 * KP_TS + kp_part0 * 2]) = kp_nx0;
-            if (lane < 16) *reinterpret_cast<uint2*>(&kpw[kp_tok1 * KP_TS + kp_part1 * 2]) = kp_nx1;
+            const bool ok = s0 + li < s_hi;
+            const uint4 mc = ok ? m_nx : uint4{0, 0, 0, 0};
+            const float nk = ok ? __half2float(__ushort_as_half(nk_nx)) : 0.0f;
+            const float rs = ok ? __half2float(__ushort_as_half(rs_nx)) : 0.0f;
+            *reinterpret_cast<uint2*>(&kpw[kp_tok0 * KP_TS + kp_part0 * 2]) =
+                s0 + kp_tok0 < s_hi ? kp_nx0 : uint2{0, 0};
+            if (lane < 16)
+                *reinterpret_cast<uint2*>(&kpw[kp_tok1 * KP_TS + kp_part1 * 2]) =
+                    s0 + kp_tok1 < s_hi ? kp_nx1 : uint2{0, 0};
             if (t + 1 < n_tiles) prefetch(s0 + TT);
             if ((t & 15) == 0) {
 #pragma unroll
@@ -243,6 +283,7 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
                     sincos_rev((float)(a.start_pos + s0 + li) * S.rope[lg][0][u], bc[u], bs[u]);
             }
             wave_sync();
+            PHASE(2);
 
             // ---- per-token scalars of this lane's token
             const uint32_t* krow = &kpw[li * KP_TS];
@@ -250,15 +291,19 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
             if (mult < 0.1f || mult > 10.0f || isnan(mult)) mult = 1.0f;
             const float rr = rs / mult;
 
-            // ---- outliers of dims 64 lg .. 64 lg + 63: value sgn (cb + nib rr)
+            // ---- outliers of dims 64 lg .. 64 lg + 63.  The sign goes back into
+            // the mask words (code 3 -> 2 for +, 1 for -), so the sign table
+            // yields +-cb; the strip keeps the signed residual nib * rs / mult.
+            uint32_t mw[4] = {mc.x, mc.y, mc.z, mc.w};
             {
-                const uint32_t mw[4] = {mc.x, mc.y, mc.z, mc.w};
+                uint32_t a3[4];
                 int cnt = 0;
                 uint64_t msk = 0;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    uint32_t x = (mw[i] & (mw[i] >> 1)) & 0x55555555u;
-                    cnt += __popc(x);
+                    a3[i] = (mw[i] & (mw[i] >> 1)) & 0x55555555u;
+                    cnt += __popc(a3[i]);
+                    uint32_t x = a3[i];
                     x = (x | (x >> 1)) & 0x33333333u;
                     x = (x | (x >> 2)) & 0x0F0F0F0Fu;
                     x = (x | (x >> 4)) & 0x00FF00FFu;
@@ -278,7 +323,7 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
                 const int nv0 = max(0, min(64, 50 - j));
                 uint64_t sw = (j < 64 ? (signs >> j) : 0ull) &
                               (nv0 >= 64 ? ~0ull : ((1ull << nv0) - 1ull));
-                uint64_t nw = 0;
+                uint64_t nw = 0, neg = 0;
                 int left = 0;
                 while (msk) {
                     if (left == 0) {
@@ -294,22 +339,33 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
                     }
                     const int bpos = __builtin_ctzll(msk);
                     msk &= msk - 1;
-                    const float r = fmaf((float)(uint32_t)(nw & 15ull), rr, (float)cbq[bpos]);
-                    orow[bpos] = (_Float16)((sw & 1ull) ? r : -r);
+                    const float r = (float)(uint32_t)(nw & 15ull) * rr;
+                    const bool pos = (sw & 1ull) != 0ull;
+                    orow[bpos] = (_Float16)(pos ? r : -r);
+                    neg |= (uint64_t)(!pos) << bpos;
                     nw >>= 4;
                     sw >>= 1;
                     left--;
                     j++;
                 }
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    uint32_t ng = (uint32_t)(neg >> (16 * i)) & 0xFFFFu;
+                    ng = (ng | (ng << 8)) & 0x00FF00FFu;
+                    ng = (ng | (ng << 4)) & 0x0F0F0F0Fu;
+                    ng = (ng | (ng << 2)) & 0x33333333u;
+                    ng = (ng | (ng << 1)) & 0x55555555u;
+                    mw[i] ^= (ng << 1) | (a3[i] & ~ng);
+                }
             }
 
+            PHASE(3);
             // ---- b operand + pass / fold MFMAs (the strip is cleared as read)
             f4 cs = f4{0.f, 0.f, 0.f, 0.f};
             f4 zt[4];
 #pragma unroll
             for (int T = 0; T < 4; T++) zt[T] = f4{0.f, 0.f, 0.f, 0.f};
             {
-                const uint32_t mw[4] = {mc.x, mc.y, mc.z, mc.w};
 #pragma unroll
                 for (int st = 0; st < 8; st++) {
                     const uint32_t word = mw[st >> 1];
@@ -327,6 +383,7 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
                 }
             }
 
+            PHASE(4);
             // ---- H_64 (1/(256 d)) on z, split hi + lo
             f4 kr[4];
             {
@@ -433,7 +490,9 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
                 bs[u] = ns;
             }
         }
+        PHASE(5);
         __syncthreads();  // (2) tile hand-off
+        PHASE(6);
     }
 
     // ---- epilogue: (max, sum) per query head
@@ -448,23 +507,14 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
     }
     __syncthreads();  // (3) maxima / sums / dump sums published
     __syncthreads();  // (4) V sums in place
+    PHASE(7);
 }
 
 // -------------------------------------------------------------- value role
 __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, int h, int lane,
-                                           int s_lo, int s_hi, int n_tiles) {
+                                           int s_lo, int s_hi, int n_tiles PH_PARAMS) {
     const int li = lane & 15, lg = lane >> 4;
-    __syncthreads();  // (1)
 
-    // lane constants: patch p = 16 g + li for g = 0..3
-    const _Float16* cvh = reinterpret_cast<const _Float16*>(a.cents_v);
-    _Float16 c3a[4], c3b[4];
-#pragma unroll
-    for (int g = 0; g < 4; g++) {
-        const int p = 16 * g + li;
-        c3a[g] = cvh[p * 4 + 3];
-        c3b[g] = cvh[256 + p * 4 + 3];
-    }
     const int r_head = li >> 1;       // A row li: head li / 2, hi (even) or lo (odd)
     const bool r_lo = (li & 1) != 0;
     const bool r_ok = li < 12;
@@ -473,28 +523,37 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, int h, in
     int vp_tok[4], vp_part[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        vp_tok[k] = (lane + 64 * k) / 13;
-        vp_part[k] = (lane + 64 * k) % 13;
+        const int idx = min(lane + 64 * k, TT * 13 - 1);
+        vp_tok[k] = idx / 13;
+        vp_part[k] = idx % 13;
     }
+    // Prefetches read clamped (always valid) rows unconditionally; which rows
+    // are real is applied when the tile is taken.
     uint2 vp_nx[4];
     unsigned short vn_nx = 0, ve_nx = 0;
     float vm_nx = 0.0f;
     auto prefetch = [&](int s0) {
+        const int last = s_hi - 1;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int tok = vp_tok[k];
-            vp_nx[k] = (lane + 64 * k < TT * 13 && s0 + tok < s_hi)
-                           ? reinterpret_cast<const uint2*>(a.vpay + ((size_t)(s0 + tok) * 4 + h) * 104)[vp_part[k]]
-                           : uint2{0, 0};
-        }
-        const int s = s0 + li;
-        const bool ok = s < s_hi;
-        const size_t row = (size_t)s * 4 + h;
-        vn_nx = ok ? reinterpret_cast<const unsigned short*>(a.vnorm)[row] : (unsigned short)0;
-        ve_nx = ok ? reinterpret_cast<const unsigned short*>(a.vrn)[row] : (unsigned short)0;
-        vm_nx = ok ? reinterpret_cast<const float*>(a.vsm)[row] : 0.0f;
+        for (int k = 0; k < 4; k++)
+            vp_nx[k] = reinterpret_cast<const uint2*>(
+                a.vpay + ((size_t)min(s0 + vp_tok[k], last) * 4 + h) * 104)[vp_part[k]];
+        const size_t row = (size_t)min(s0 + li, last) * 4 + h;
+        vn_nx = reinterpret_cast<const unsigned short*>(a.vnorm)[row];
+        ve_nx = reinterpret_cast<const unsigned short*>(a.vrn)[row];
+        vm_nx = reinterpret_cast<const float*>(a.vsm)[row];
     };
     if (n_tiles > 0) prefetch(s_lo);
+    query_transform(a, S, h, 3, lane);
+    __syncthreads();  // (1)
+    PHASE(8);
+    // lane constants: patch p = 16 g + li for g = 0..3
+    _Float16 c3a[4], c3b[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        c3a[g] = S.c3v[0][16 * g + li];
+        c3b[g] = S.c3v[1][16 * g + li];
+    }
 
     f4 pv[20];
 #pragma unroll
@@ -502,22 +561,27 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, int h, in
     float s3p = 0.0f;  // sum of w * norm * smeta / 7 over this lane's tokens (hi rows)
     const float av = a.a_v;
     uint32_t* vpw = S.vp[h];
+    PHASE(9);
 
     for (int it = 0; it <= n_tiles; it++) {
         if (it >= 1) {
             const int t = it - 1;
             const int buf = t & 1;
             // ---- take the staged tile, start loading the next one
+            const int s0 = s_lo + t * TT;
 #pragma unroll
             for (int k = 0; k < 4; k++)
                 if (lane + 64 * k < TT * 13)
-                    *reinterpret_cast<uint2*>(&vpw[vp_tok[k] * VP_TS + vp_part[k] * 2]) = vp_nx[k];
+                    *reinterpret_cast<uint2*>(&vpw[vp_tok[k] * VP_TS + vp_part[k] * 2]) =
+                        s0 + vp_tok[k] < s_hi ? vp_nx[k] : uint2{0, 0};
             if (lg == 0) {
-                const float nv = __half2float(__ushort_as_half(vn_nx));
-                const float en = __half2float(__ushort_as_half(ve_nx));
+                const bool ok = s0 + li < s_hi;
+                const float nv = ok ? __half2float(__ushort_as_half(vn_nx)) : 0.0f;
+                const float en = ok ? __half2float(__ushort_as_half(ve_nx)) : 0.0f;
+                const float vm = ok ? vm_nx : 0.0f;
                 S.vsc[h][0][li] = (av * nv) * en;
                 S.vsc[h][1][li] = av * nv;
-                S.vsc[h][2][li] = nv * vm_nx / 7.0f;
+                S.vsc[h][2][li] = nv * vm / 7.0f;
             }
             if (t + 1 < n_tiles) prefetch(s_lo + (t + 1) * TT);
             wave_sync();
@@ -539,6 +603,7 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, int h, in
                 }
             }
 
+            PHASE(10);
             // ---- weights x V scalings -> A operands (rows head hi/lo, K = tokens 4 lg..)
             h4 Ap[3];
             {
@@ -559,6 +624,7 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, int h, in
                 }
             }
 
+            PHASE(11);
             // ---- decode V straight into B operands, P x V on MFMA
 #pragma unroll
             for (int g = 0; g < 4; g++) {
@@ -587,7 +653,9 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, int h, in
                 pv[5 * g + 4] = mfma16(Ap[2], b4, pv[5 * g + 4]);
             }
         }
+        PHASE(12);
         __syncthreads();  // (2) tile hand-off
+        PHASE(13);
     }
 
     // ---- epilogue: dump sums per head (hi rows li = 2 hd, all lane groups)
@@ -614,6 +682,7 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, int h, in
         }
     }
     __syncthreads();  // (4)
+    PHASE(14);
 }
 
 __global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_per_chunk) {
@@ -628,6 +697,13 @@ __global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_
     const int s_lo = min(chunk * tiles_per_chunk * TT, c_len);
     const int s_hi = min(s_lo + tiles_per_chunk * TT, c_len);
     const int n_tiles = (s_hi - s_lo + TT - 1) / TT;
+#ifdef KHQ_PHASE_TIMING
+    unsigned long long ph_t = __builtin_amdgcn_s_memtime();
+    const unsigned long long rt0 = __builtin_amdgcn_s_memrealtime();
+    unsigned ph_acc[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) ph_acc[k] = 0;
+#endif
 
     // ---- shared tables: codebook, sign table, cents_k[2], rotor_k, RoPE
     {
@@ -650,6 +726,16 @@ __global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_
         } else if (tid < 256 + 128) {
             reinterpret_cast<uint4*>(&S.vp[0][0])[tid - 256] =
                 reinterpret_cast<const uint4*>(a.rotor_k)[tid - 256];
+        } else {
+            reinterpret_cast<uint4*>(S.rotv)[tid - 384] =
+                reinterpret_cast<const uint4*>(a.rotor_v)[tid - 384];
+        }
+        if (tid < 128) {
+            const _Float16* cvh = reinterpret_cast<const _Float16*>(a.cents_v);
+            S.c3v[tid >> 6][tid & 63] = cvh[(tid >> 6) * 256 + (tid & 63) * 4 + 3];
+        }
+        if (tid < 32) {
+            reinterpret_cast<uint4*>(S.dvh)[tid] = reinterpret_cast<const uint4*>(a.dv)[tid];
         } else if (tid >= 448) {
             // lanes (u, lg) with u < 8 of the last wavefront: RoPE table
             const int l = tid - 448, u = l & 15, g = l >> 4;
@@ -663,17 +749,23 @@ __global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_
         }
     }
 
+    PHASE(0);
+
     if (wv < 4) {
-        key_role(a, S, h, lane, s_lo, s_hi, n_tiles);
+        key_role(a, S, h, lane, s_lo, s_hi, n_tiles PH_ARGS);
     } else {
-        value_role(a, S, h, lane, s_lo, s_hi, n_tiles);
+        value_role(a, S, h, lane, s_lo, s_hi, n_tiles PH_ARGS);
     }
+#ifdef KHQ_PHASE_TIMING
+    ph_t = __builtin_amdgcn_s_memtime();
+#endif
 
     // ---- output: wavefront wv handles query heads 3 (wv / 4) .. + 2 of KV head h
     const float* ep = reinterpret_cast<const float*>(S.o[h]);
     float rv[16];
 #pragma unroll
-    for (int t = 0; t < 16; t++) rv[t] = __half2float(a.rotor_v[lane * 16 + t]);
+    for (int t = 0; t < 16; t++) rv[t] = (float)S.rotv[lane * 16 + t];
+#pragma unroll
     for (int hh = 0; hh < 3; hh++) {
         const int hd = 3 * (wv >> 2) + hh;
         float o[4], u[4];
@@ -696,12 +788,21 @@ __global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_
 #pragma unroll
         for (int c = 0; c < 4; c++)
             out[lane * 4 + c] =
-                empty ? 0.0f : (u[c] * (1.0f / 16.0f)) / (__half2float(a.dv[lane * 4 + c]) + 1e-8f);
+                empty ? 0.0f : (u[c] * (1.0f / 16.0f)) / ((float)S.dvh[lane * 4 + c] + 1e-8f);
         if (lane == 0) {
             out[256] = empty ? -1e20f : M;
             out[257] = empty ? 0.0f : L;
         }
     }
+    PHASE(15);
+#ifdef KHQ_PHASE_TIMING
+    if (blockIdx.x == 0 && (threadIdx.x & 0xFF) == 0)
+        for (int k = 0; k < 16; k++) phase_cycles[k] += ph_acc[k];
+    if (threadIdx.x == 0 && blockIdx.x < 1024) {
+        block_times[blockIdx.x][0] = rt0;
+        block_times[blockIdx.x][1] = __builtin_amdgcn_s_memrealtime();
+    }
+#endif
 }
 
 }  // namespace ws
@@ -723,3 +824,19 @@ hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks, 
 }
 
 }  // namespace khq
+
+#ifdef KHQ_PHASE_TIMING
+extern "C" int khq_ws_phase_cycles(unsigned long long* out, int reset) {
+    hipError_t e = hipMemcpyFromSymbol(out, HIP_SYMBOL(khq::ws::phase_cycles),
+                                       sizeof(unsigned long long) * 16);
+    if (e == hipSuccess && reset) {
+        unsigned long long z[16] = {0};
+        e = hipMemcpyToSymbol(HIP_SYMBOL(khq::ws::phase_cycles), z, sizeof(z));
+    }
+    return e == hipSuccess ? 0 : (int)e;
+}
+extern "C" int khq_ws_block_times(unsigned long long* out) {
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(khq::ws::block_times),
+                                    sizeof(unsigned long long) * 2048);
+}
+#endif

@@ -1,0 +1,190 @@
+// khq_finish.hip -- last stage of the fused two-region step: fp16 ring-window
+// attention, logsumexp merge with the compressed-region partials, division by
+// (den + eps) and the sigmoid gate, in one launch.
+//
+// One 256-thread block per (query head, 32-dim slice).  Every block of a head
+// recomputes the window scores (win_len <= 256 rows of 512 B, which stay in
+// L2) so no second launch is needed; each block then sums the window V and
+// the compressed partials for its 32 dims only.  All global loads of a stage
+// are issued before any of their values is used.
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "khq_internal.h"
+#include "khq_mfma_util.h"
+
+namespace khq {
+namespace fin {
+
+using namespace mu;
+
+constexpr int DS = 32;         // dims per block
+constexpr int MAX_WIN = 256;   // ring capacity bound
+constexpr int MAX_PARTS = 1024;
+
+__device__ __forceinline__ float block_max(float v, float* s_red) {
+    v = fmaxf(v, __shfl_xor(v, 1, 64));
+    v = fmaxf(v, __shfl_xor(v, 2, 64));
+    v = fmaxf(v, __shfl_xor(v, 4, 64));
+    v = fmaxf(v, __shfl_xor(v, 8, 64));
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    v = fmaxf(v, __shfl_xor(v, 32, 64));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+}
+
+__device__ __forceinline__ float block_sum(float v, float* s_red) {
+    v += __shfl_xor(v, 1, 64);
+    v += __shfl_xor(v, 2, 64);
+    v += __shfl_xor(v, 4, 64);
+    v += __shfl_xor(v, 8, 64);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+}
+
+__global__ __launch_bounds__(256) void step_finish_kernel(FinishArgs a) {
+    __shared__ float s_p[MAX_WIN];      // window weights
+    __shared__ float s_w[MAX_PARTS];    // compressed part weights
+    __shared__ float s_red[4];
+    __shared__ float s_acc[2][8][DS];
+    const int t = threadIdx.x;
+    const int hq = blockIdx.x;
+    const int d0 = blockIdx.y * DS;
+    const int hk = hq / a.n_rep;
+    const float* base = a.part + (size_t)hq * a.part_stride * 258;  // < 2^31 floats per head
+    const int d = t & (DS - 1), grp = t >> 5;
+    const int np = a.n_parts, wl = a.win_len;
+    const int last_p = max(np - 1, 0), last_w = max(wl - 1, 0);
+    const int cap = a.ring_cap;  // win_start < cap and win_len <= cap (host-checked)
+    auto slot_of = [&](int s) {
+        const int x = a.win_start + s;
+        return x >= cap ? x - cap : x;
+    };
+
+    // ---- every load of the block is issued here, from clamped indices
+    float mcv[MAX_PARTS / 256], lcv[MAX_PARTS / 256];
+#pragma unroll
+    for (int k = 0; k < MAX_PARTS / 256; k++) {
+        const float* pp = base + (size_t)min(t + 256 * k, last_p) * 258;
+        mcv[k] = pp[256];
+        lcv[k] = pp[257];
+    }
+    float pacc[32];  // parts grp + 8 u (first 256 parts)
+#pragma unroll
+    for (int u = 0; u < 32; u++) pacc[u] = base[min(grp + 8 * u, last_p) * 258 + d0 + d];
+    __half vw[32];   // window rows grp + 8 u
+#pragma unroll
+    for (int u = 0; u < 32; u++) {
+        const int slot = slot_of(min(grp + 8 * u, last_w));
+        vw[u] = a.ring_v[(slot * a.h_kv + hk) * 256 + d0 + d];
+    }
+    const int sub = t >> 4, l16 = t & 15;
+    const __half* qrow = a.q + (size_t)hq * 512 + 16 * l16;
+    const h8 qa = __builtin_bit_cast(h8, reinterpret_cast<const uint4*>(qrow)[0]);
+    const h8 qb = __builtin_bit_cast(h8, reinterpret_cast<const uint4*>(qrow)[1]);
+    const float gate = __half2float(a.q[(size_t)hq * 512 + 256 + d0 + (t & (DS - 1))]);
+
+    // ---- window scores: 16 threads per row (16 dims each), 16 rows per round
+    float wmax = -1e20f;
+    const int n_rounds = (wl + 15) / 16;
+    for (int r0 = 0; r0 < n_rounds; r0 += 8) {
+        uint4 kr[8][2];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int slot = slot_of(min(16 * (r0 + u) + sub, last_w));
+            const uint4* kp = reinterpret_cast<const uint4*>(
+                a.ring_k + (slot * a.h_kv + hk) * 256 + 16 * l16);
+            kr[u][0] = kp[0];
+            kr[u][1] = kp[1];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const h8 ka = __builtin_bit_cast(h8, kr[u][0]), kb = __builtin_bit_cast(h8, kr[u][1]);
+            float x0 = 0.0f, x1 = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                x0 = fmaf((float)qa[e], (float)ka[e], x0);
+                x1 = fmaf((float)qb[e], (float)kb[e], x1);
+            }
+            const float dot = row16_sum(x0 + x1);
+            const int s = 16 * (r0 + u) + sub;
+            if (s < wl) {
+                const float sc = dot * a.sc;
+                if (l16 == 0) s_p[s] = sc;
+                wmax = fmaxf(wmax, sc);
+            }
+        }
+    }
+    float mcmax = -1e20f;
+#pragma unroll
+    for (int k = 0; k < MAX_PARTS / 256; k++)
+        if (t + 256 * k < np) mcmax = fmaxf(mcmax, mcv[k]);
+    const float Mw = block_max(wmax, s_red);
+    const float Mc = block_max(mcmax, s_red);
+
+    // ---- weights: window exp(s - Mw), parts exp(m - Mc); zero past the ends,
+    // so the sums below need no bounds (clamped loads hold finite values)
+    float lw = 0.0f, lc = 0.0f;
+    {
+        const float p = t < wl ? expf(s_p[t] - Mw) : 0.0f;
+        s_p[t] = p;
+        lw = p;
+    }
+#pragma unroll
+    for (int k = 0; k < MAX_PARTS / 256; k++) {
+        const int s = t + 256 * k;
+        const float wgt = s < np ? expf(mcv[k] - Mc) : 0.0f;
+        s_w[s] = wgt;
+        lc = fmaf(s < np ? lcv[k] : 0.0f, wgt, lc);
+    }
+    const float Lw = block_sum(lw, s_red);
+    const float Lc = block_sum(lc, s_red);  // its barriers also publish s_p / s_w
+
+    // ---- numerators for dims d0 + d: rows / parts strided by the 8 groups
+    float aw[4] = {0.f, 0.f, 0.f, 0.f}, ac[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 32; u++) {
+        const int s = grp + 8 * u;
+        aw[u & 3] = fmaf(s_p[s], __half2float(vw[u]), aw[u & 3]);
+        ac[u & 3] = fmaf(s_w[s], pacc[u], ac[u & 3]);
+    }
+    for (int s = grp + 256; s < np; s += 8)  // parts beyond the first 256
+        ac[0] = fmaf(s_w[s], base[(size_t)s * 258 + d0 + d], ac[0]);
+    s_acc[0][grp][d] = (aw[0] + aw[1]) + (aw[2] + aw[3]);
+    s_acc[1][grp][d] = (ac[0] + ac[1]) + (ac[2] + ac[3]);
+    __syncthreads();
+    if (t < DS) {
+        float nw = 0.0f, nc = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            nw += s_acc[0][g][t];
+            nc += s_acc[1][g][t];
+        }
+        const float M = fmaxf(Mw, Mc);
+        const float fw = wl > 0 ? expf(Mw - M) : 0.0f;
+        const float fc = np > 0 ? expf(Mc - M) : 0.0f;
+        const float num = fmaf(nc, fc, nw * fw);
+        const float den = fmaf(Lc, fc, Lw * fw);
+        float val = num / (den + a.eps);
+        val = val * (1.0f / (1.0f + expf(-gate)));
+        a.out[(size_t)hq * 256 + d0 + t] = __float2half(val);
+    }
+}
+
+}  // namespace fin
+
+hipError_t launch_step_finish(const FinishArgs& a, int H_q, hipStream_t st) {
+    if (a.n_parts > fin::MAX_PARTS || a.win_len > fin::MAX_WIN || a.n_rep <= 0)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(fin::step_finish_kernel, dim3(H_q, 256 / fin::DS), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace khq

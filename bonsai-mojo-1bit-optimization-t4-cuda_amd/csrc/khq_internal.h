@@ -42,6 +42,20 @@ struct WinArgs {
     float sc;
 };
 
+// Window attention + merge with compressed partials + gate (fused step tail).
+// Compressed partial i of query head h at part[(h * part_stride + i) * 258].
+struct FinishArgs {
+    const float* part;
+    int n_parts, part_stride;
+    const __half* q;  // q_gate [H_q][512]
+    const __half* ring_k;
+    const __half* ring_v;
+    int win_start, win_len, ring_cap, h_kv, n_rep;
+    float sc, eps;
+    __half* out;  // [H_q][256]
+};
+hipError_t launch_step_finish(const FinishArgs& a, int H_q, hipStream_t st);
+
 hipError_t launch_compress(const __half* x, const __half* d_vec, const __half* rotor,
                            const __half* cents, const __half* vq, uint32_t* out_mask,
                            __half* out_norms, __half* out_rn, uint8_t* out_pay,

@@ -213,6 +213,38 @@ def test_window_and_merge(device, kernel):
     close(out3.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("case", ["window-only", "compressed-only", "wrap-216", "full-ring"])
+def test_fused_step_regions(device, kernel, case):
+    """khq_attn_step_fp16 for each region combination the layer runtime issues,
+    against the oracle's window / compressed triples merged and gated."""
+    st = two_region_state(seed=31, n_tokens=600, boundary=384)
+    c_len, win_start, win_len = 384, 384 % 256, 216
+    if case == "window-only":
+        c_len, win_start, win_len = 0, 0, 200
+    elif case == "compressed-only":
+        win_len = 0
+    elif case == "full-ring":
+        win_start, win_len = (600 - 256) % 256, 256
+    st.update(c_len=c_len, win_start=win_start, win_len=win_len)
+    pay, cents = _gpu_state(st)
+    q = t(st["q_gate"])
+    out = torch.zeros((H_Q, D), device=device, dtype=torch.float16)
+    ops.attn_step(q, pay, cents, t(st["ring_k"]), t(st["ring_v"]), out, H_q=H_Q, H_kv=H_KV,
+                  c_len=c_len, win_start=win_start, win_len=win_len, ring_cap=256, scale=SCALE)
+    torch.cuda.synchronize()
+    if c_len == 0:
+        _, ww = oracle_window(st)
+        _, want = oracle.merge_gate(ww, ww, st["q_gate"], H_q=H_Q, has_w=False)
+    elif win_len == 0:
+        _, wc, _ = oracle_attn(st)
+        _, want = oracle.merge_gate(wc, wc, st["q_gate"], H_q=H_Q, has_w=False)
+    else:
+        _, wc, _ = oracle_attn(st)
+        _, ww = oracle_window(st)
+        _, want = oracle.merge_gate(wc, ww, st["q_gate"], H_q=H_Q, has_w=True)
+    close(out.cpu().numpy(), want)
+
+
 def test_window_wrap_and_guards(device):
     st = two_region_state(seed=25, n_tokens=600, boundary=384)
     st["win_start"], st["win_len"] = 384 % 256, 216
