@@ -3,11 +3,13 @@
 
 One step = one decode token through the 16 full-attention layers: per layer
 one two-region KHQ attention step (32,640 compressed tokens + 128 raw ring
-tokens, H_q 24 / H_kv 4, D 256) with uniform-random packed codes resident in
-HBM (a separate 28.7 MB payload per layer, 460 MB in total, so the 256 MB
-last-level cache cannot hold the working set).  Prints one JSON line.
+tokens, H_q 24 / H_kv 4, D 256) over a packed payload resident in HBM (a
+separate 28.7 MB payload per layer, 460 MB in total, so the 256 MB last-level
+cache cannot hold the working set).  The payload is the library's own
+compression of N(0,1) K/V rows (--data uniform: uniform-random packed codes).
+Prints one JSON line.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--data compressed|uniform]
 
 value = microseconds per layer-step (lower is better), timed with HIP events
 over exactly K steps.  roofline = the compressed-region kernel alone, timed
@@ -47,6 +49,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--kernel", choices=["auto", "portable", "mfma-single"], default="auto",
                     help="compressed-region kernel (library default: auto)")
+    ap.add_argument("--data", choices=["compressed", "uniform"], default="compressed",
+                    help="payload: the library's compression of N(0,1) K/V rows (default) "
+                         "or uniform-random packed codes")
     ap.add_argument("--sweep", action="store_true",
                     help="also time the reference entry points at splits 1/8/32/64")
     return ap.parse_args()
@@ -72,17 +77,21 @@ def main():
     for l in range(args.layers):
         lc = synthetic_layer(l, seed=1234)
         pay = ops.Payload(c_len * H_KV, dev)
-        rows = synth.random_rows(c_len * H_KV, seed=1000 + l, device=dev)
-        for k, v in rows.items():
-            getattr(pay, k).copy_(v)
-        del rows
+        cents = ops.Centroids(lc, dev)
+        if args.data == "compressed":
+            synth.compressed_rows(pay, cents, seed=1000 + l)
+        else:
+            rows = synth.random_rows(c_len * H_KV, seed=1000 + l, device=dev)
+            for k, v in rows.items():
+                getattr(pay, k).copy_(v)
+            del rows
         g = torch.Generator(device=dev)
         g.manual_seed(5000 + l)
         ring_k = torch.randn((RING, H_KV, D), generator=g, device=dev).half()
         ring_v = torch.randn((RING, H_KV, D), generator=g, device=dev).half()
         q = synth.q_gate(H_Q, seed=7000 + l, device=dev)
         out = torch.empty((H_Q, D), device=dev, dtype=torch.float16)
-        layers.append(dict(lc=lc, cents=ops.Centroids(lc, dev), pay=pay, ring_k=ring_k,
+        layers.append(dict(lc=lc, cents=cents, pay=pay, ring_k=ring_k,
                            ring_v=ring_v, q=q, out=out))
     torch.cuda.synchronize()
     win_start = c_len % RING
@@ -144,7 +153,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded uniform-random packed codes, N(0,1) fp16 ring)",
+        "data": ("synthetic: N(0,1) K/V rows compressed by the library's KHQ compressor, "
+                 "N(0,1) fp16 ring" if args.data == "compressed" else
+                 "synthetic: uniform-random packed codes, N(0,1) fp16 ring"),
         "config": {
             "workload": f"C3: {args.layers} layers x ({c_len} compressed + {win_len} raw) tokens, "
                         f"batch 1, H_q {H_Q} / H_kv {H_KV}, D {D}, fused two-region step",
@@ -167,6 +178,25 @@ def main():
             "bytes_per_launch": c_bytes,
         },
     }
+
+    if args.data == "compressed":
+        # the same kernel on uniform-random packed codes (outlier counts U[0, 50])
+        L0 = layers[0]
+        upay = ops.Payload(c_len * H_KV, dev)
+        for k, v in synth.random_rows(c_len * H_KV, seed=99, device=dev).items():
+            getattr(upay, k).copy_(v)
+        ops.attn_partials(L0["q"], upay, L0["cents"], H_q=H_Q, H_kv=H_KV, c_len=c_len,
+                          scale=scale)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(args.steps):
+            ops.attn_partials(L0["q"], upay, L0["cents"], H_q=H_Q, H_kv=H_KV, c_len=c_len,
+                              scale=scale)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        result["roofline"]["avg_kernel_us_uniform_codes"] = round(
+            e0.elapsed_time(e1) * 1000.0 / args.steps, 3)
+        del upay
 
     if args.sweep:
         sweep = {}

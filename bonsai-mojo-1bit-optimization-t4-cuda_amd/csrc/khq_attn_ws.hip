@@ -148,25 +148,22 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
     const int arow_h = li >> 1;
     const bool arow_lo = (li & 1) != 0;
     const bool arow_ok = li < 12;
-    // output-row signs of 1/d (rows j = 16 T' + 4 lg + c') and q_rot (roped
-    // dims 0..63 at the K positions of the rope'd key layout); unconditional
-    // vector loads from a clamped head row, zeroed rows applied afterwards
-    float dsg[4][4];
+    // signs of 1/d for the H_64 output rows j = 16 T' + li held by this lane's
+    // A rows, and q_rot (roped dims 0..63 at the K positions of the rope'd key
+    // layout); unconditional loads from a clamped head row, zeroed rows after
+    float dsgn[4];
     h8 Aq[2];
     {
-        uint2 dr[4], qv[4];
+        uint2 qv[4];
+        __half dj[4];
         const __half* qrow = a.q + (size_t)(h * 6 + min(arow_h, 5)) * 512;
 #pragma unroll
         for (int Tp = 0; Tp < 4; Tp++) {
-            dr[Tp] = *reinterpret_cast<const uint2*>(a.dk + 16 * Tp + 4 * lg);
+            dj[Tp] = a.dk[16 * Tp + li];
             qv[Tp] = *reinterpret_cast<const uint2*>(qrow + 16 * Tp + 4 * lg);
         }
 #pragma unroll
-        for (int Tp = 0; Tp < 4; Tp++) {
-            const h4 d4 = __builtin_bit_cast(h4, dr[Tp]);
-#pragma unroll
-            for (int c = 0; c < 4; c++) dsg[Tp][c] = ((float)d4[c] < 0.0f) ? -1.0f : 1.0f;
-        }
+        for (int Tp = 0; Tp < 4; Tp++) dsgn[Tp] = (__half2float(dj[Tp]) < 0.0f) ? -1.0f : 1.0f;
 #pragma unroll
         for (int kk = 0; kk < 2; kk++)
 #pragma unroll
@@ -178,24 +175,32 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
             }
     }
     // ---- staging: mask words 4 lg .. 4 lg + 3 of (token li, head h) straight
-    // to registers; kpay rows through LDS; norms to registers.
+    // to registers; kpay rows through LDS; norms to registers.  Buffer loads
+    // with a per-lane offset and the tile offset in a scalar register; rows
+    // past c_len read as zeros, rows of the next chunk are dropped on commit.
     const int kp_tok0 = lane / 5, kp_part0 = lane % 5;
     const int kp_tok1 = min(lane + 64, 79) / 5, kp_part1 = min(lane + 64, 79) % 5;
-    // Prefetches read clamped (always valid) rows unconditionally, so no load
-    // sits in a branch; which rows are real is applied when the tile is taken.
-    uint4 m_nx = uint4{0, 0, 0, 0};
-    uint2 kp_nx0 = uint2{0, 0}, kp_nx1 = uint2{0, 0};
+    const uint32_t n_rows = (uint32_t)a.c_len * 4;
+    const rsrc_t rs_mask = make_rsrc(a.kmask, n_rows * 64);
+    const rsrc_t rs_kn = make_rsrc(a.knorm, n_rows * 2);
+    const rsrc_t rs_kr = make_rsrc(a.krn, n_rows * 2);
+    const rsrc_t rs_kp = make_rsrc(a.kpay, n_rows * 40);
+    const uint32_t vo_mask = (uint32_t)(li * 4 + h) * 64 + lg * 16;
+    const uint32_t vo_norm = (uint32_t)(li * 4 + h) * 2;
+    const uint32_t vo_kp0 = (uint32_t)(kp_tok0 * 4 + h) * 40 + kp_part0 * 8;
+    const uint32_t vo_kp1 = (uint32_t)(kp_tok1 * 4 + h) * 40 + kp_part1 * 8;
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+    u4v m_nx = u4v{0, 0, 0, 0};
+    u2v kp_nx0 = u2v{0, 0}, kp_nx1 = u2v{0, 0};
     unsigned short nk_nx = 0, rs_nx = 0;
     auto prefetch = [&](int s0) {
-        const int last = s_hi - 1;
-        const size_t row = (size_t)min(s0 + li, last) * 4 + h;
-        m_nx = reinterpret_cast<const uint4*>(a.kmask + row * 16)[lg];
-        nk_nx = reinterpret_cast<const unsigned short*>(a.knorm)[row];
-        rs_nx = reinterpret_cast<const unsigned short*>(a.krn)[row];
-        kp_nx0 = reinterpret_cast<const uint2*>(
-            a.kpay + ((size_t)min(s0 + kp_tok0, last) * 4 + h) * 40)[kp_part0];
-        kp_nx1 = reinterpret_cast<const uint2*>(
-            a.kpay + ((size_t)min(s0 + kp_tok1, last) * 4 + h) * 40)[kp_part1];
+        const int so = s0 * 4;  // first row of the tile
+        m_nx = __builtin_amdgcn_raw_buffer_load_b128(rs_mask, vo_mask, so * 64, 0);
+        nk_nx = __builtin_amdgcn_raw_buffer_load_b16(rs_kn, vo_norm, so * 2, 0);
+        rs_nx = __builtin_amdgcn_raw_buffer_load_b16(rs_kr, vo_norm, so * 2, 0);
+        kp_nx0 = __builtin_amdgcn_raw_buffer_load_b64(rs_kp, vo_kp0, so * 40, 0);
+        kp_nx1 = __builtin_amdgcn_raw_buffer_load_b64(rs_kp, vo_kp1, so * 40, 0);
     };
     if (n_tiles > 0) prefetch(s_lo);
     query_transform(a, S, h, 0, lane);
@@ -235,15 +240,21 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
     }
     const h8 hzero = {0, 0, 0, 0, 0, 0, 0, 0};
     // H_64 = H_4 (x) H_16 (j = 16 T' + li, m = 16 T + 4 lg + c'):
-    // A[T'][kk] = H_4[T'][2 kk + e/4] * H_16[li][4 lg + (e & 3)] / 256; the
-    // sign of 1/d_j is applied to the output rows instead.
-    h8 Ag[2];
+    // A[T'][kk] = sgn(d_j) H_4[T'][2 kk + e/4] H_16[li][4 lg + (e & 3)] / 256;
+    // H_4 rows: T'=0 [+ + + +], 1 [+ - + -], 2 [+ + - -], 3 [+ - - +] over
+    // T = (kk, e/4).
+    h8 Ah[4][2];
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const float g = ((__popc(li & (4 * lg + (e & 3))) & 1) ? -1.0f : 1.0f) / 256.0f;
-        Ag[0][e] = (_Float16)g;
-        Ag[1][e] = (_Float16)((e >> 2) ? -g : g);
-    }
+    for (int Tp = 0; Tp < 4; Tp++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float g = ((__popc(li & (4 * lg + (e & 3))) & 1) ? -dsgn[Tp] : dsgn[Tp]) / 256.0f;
+            const int T0 = e >> 2, T1 = 2 + (e >> 2);
+            const float h0 = (__popc(Tp & T0) & 1) ? -g : g;
+            const float h1 = (__popc(Tp & T1) & 1) ? -g : g;
+            Ah[Tp][0][e] = (_Float16)h0;
+            Ah[Tp][1][e] = (_Float16)h1;
+        }
     wave_sync();
     // clear this lane's outlier strip (the query scratch is no longer needed)
     _Float16* orow = &S.o[h][lane * O_LS];
@@ -268,14 +279,14 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
             const int s0 = s_lo + t * TT;
             // ---- take the staged tile, start loading the next one
             const bool ok = s0 + li < s_hi;
-            const uint4 mc = ok ? m_nx : uint4{0, 0, 0, 0};
+            const uint4 mc = ok ? uint4{m_nx[0], m_nx[1], m_nx[2], m_nx[3]} : uint4{0, 0, 0, 0};
             const float nk = ok ? __half2float(__ushort_as_half(nk_nx)) : 0.0f;
             const float rs = ok ? __half2float(__ushort_as_half(rs_nx)) : 0.0f;
-            *reinterpret_cast<uint2*>(&kpw[kp_tok0 * KP_TS + kp_part0 * 2]) =
-                s0 + kp_tok0 < s_hi ? kp_nx0 : uint2{0, 0};
+            *reinterpret_cast<u2v*>(&kpw[kp_tok0 * KP_TS + kp_part0 * 2]) =
+                s0 + kp_tok0 < s_hi ? kp_nx0 : u2v{0, 0};
             if (lane < 16)
-                *reinterpret_cast<uint2*>(&kpw[kp_tok1 * KP_TS + kp_part1 * 2]) =
-                    s0 + kp_tok1 < s_hi ? kp_nx1 : uint2{0, 0};
+                *reinterpret_cast<u2v*>(&kpw[kp_tok1 * KP_TS + kp_part1 * 2]) =
+                    s0 + kp_tok1 < s_hi ? kp_nx1 : u2v{0, 0};
             if (t + 1 < n_tiles) prefetch(s0 + TT);
             if ((t & 15) == 0) {
 #pragma unroll
@@ -387,29 +398,24 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
             // ---- H_64 (1/(256 d)) on z, split hi + lo
             f4 kr[4];
             {
-                h8 zb[4];
+                uint32_t zw[4][4];
 #pragma unroll
                 for (int e = 0; e < 8; e += 2) {
                     const int T0 = e >> 2, c = e & 3;
-                    _Float16 a0, a1, a2, a3;
-                    split2(zt[T0][c], zt[T0][c + 1], a0, a1, a2, a3);
-                    zb[0][e] = a0; zb[0][e + 1] = a1; zb[2][e] = a2; zb[2][e + 1] = a3;
-                    split2(zt[2 + T0][c], zt[2 + T0][c + 1], a0, a1, a2, a3);
-                    zb[1][e] = a0; zb[1][e + 1] = a1; zb[3][e] = a2; zb[3][e + 1] = a3;
+                    split_pk(zt[T0][c], zt[T0][c + 1], zw[0][e >> 1], zw[2][e >> 1]);
+                    split_pk(zt[2 + T0][c], zt[2 + T0][c + 1], zw[1][e >> 1], zw[3][e >> 1]);
                 }
-                // H_4 rows: T'=0 [+ + + +], 1 [+ - + -], 2 [+ + - -], 3 [+ - - +]
-                const h8 A00 = Ag[0], A01 = Ag[1], A10 = -Ag[0], A11 = -Ag[1];
+                h8 zb[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    zb[k] = __builtin_bit_cast(h8, uint4{zw[k][0], zw[k][1], zw[k][2], zw[k][3]});
 #pragma unroll
                 for (int Tp = 0; Tp < 4; Tp++) {
-                    const h8 k0 = (Tp & 1) ? A01 : A00;
-                    const h8 k1 = (Tp == 0) ? A00 : (Tp == 1) ? A01 : (Tp == 2) ? A10 : A11;
                     f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-                    acc = mfma32(k0, zb[0], acc);
-                    acc = mfma32(k1, zb[1], acc);
-                    acc = mfma32(k0, zb[2], acc);
-                    acc = mfma32(k1, zb[3], acc);
-#pragma unroll
-                    for (int c = 0; c < 4; c++) acc[c] *= dsg[Tp][c];
+                    acc = mfma32(Ah[Tp][0], zb[0], acc);
+                    acc = mfma32(Ah[Tp][1], zb[1], acc);
+                    acc = mfma32(Ah[Tp][0], zb[2], acc);
+                    acc = mfma32(Ah[Tp][1], zb[3], acc);
                     kr[Tp] = acc;
                 }
             }
@@ -425,16 +431,17 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
 
             // ---- roped part of the score on MFMA (key split hi + lo)
             {
-                h8 kb[4];
+                uint32_t kw[4][4];
 #pragma unroll
                 for (int e = 0; e < 8; e += 2) {
                     const int T0 = e >> 2, c = e & 3;
-                    _Float16 a0, a1, a2, a3;
-                    split2(kr[T0][c], kr[T0][c + 1], a0, a1, a2, a3);
-                    kb[0][e] = a0; kb[0][e + 1] = a1; kb[2][e] = a2; kb[2][e + 1] = a3;
-                    split2(kr[2 + T0][c], kr[2 + T0][c + 1], a0, a1, a2, a3);
-                    kb[1][e] = a0; kb[1][e + 1] = a1; kb[3][e] = a2; kb[3][e + 1] = a3;
+                    split_pk(kr[T0][c], kr[T0][c + 1], kw[0][e >> 1], kw[2][e >> 1]);
+                    split_pk(kr[2 + T0][c], kr[2 + T0][c + 1], kw[1][e >> 1], kw[3][e >> 1]);
                 }
+                h8 kb[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    kb[k] = __builtin_bit_cast(h8, uint4{kw[k][0], kw[k][1], kw[k][2], kw[k][3]});
                 cs = mfma32(Aq[0], kb[0], cs);
                 cs = mfma32(Aq[1], kb[1], cs);
                 cs = mfma32(Aq[0], kb[2], cs);
@@ -518,6 +525,7 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, int h, in
     const int r_head = li >> 1;       // A row li: head li / 2, hi (even) or lo (odd)
     const bool r_lo = (li & 1) != 0;
     const bool r_ok = li < 12;
+    const float m_lo = r_lo ? -1.0f : 0.0f;  // part_pk: lo rows take the remainder
 
     // staging: vpay rows (13 uint2 per token) by lane, norms of token li
     int vp_tok[4], vp_part[4];
@@ -527,21 +535,29 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, int h, in
         vp_tok[k] = idx / 13;
         vp_part[k] = idx % 13;
     }
-    // Prefetches read clamped (always valid) rows unconditionally; which rows
-    // are real is applied when the tile is taken.
-    uint2 vp_nx[4];
+    // Buffer loads: per-lane offsets, tile offset in a scalar register; rows
+    // past c_len read as zeros, rows of the next chunk are dropped on commit.
+    typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+    const uint32_t n_rows = (uint32_t)a.c_len * 4;
+    const rsrc_t rs_vp = make_rsrc(a.vpay, n_rows * 104);
+    const rsrc_t rs_vn = make_rsrc(a.vnorm, n_rows * 2);
+    const rsrc_t rs_ve = make_rsrc(a.vrn, n_rows * 2);
+    const rsrc_t rs_vm = make_rsrc(a.vsm, n_rows * 4);
+    uint32_t vo_vp[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) vo_vp[k] = (uint32_t)(vp_tok[k] * 4 + h) * 104 + vp_part[k] * 8;
+    const uint32_t vo_n = (uint32_t)(li * 4 + h);
+    u2v vp_nx[4];
     unsigned short vn_nx = 0, ve_nx = 0;
-    float vm_nx = 0.0f;
+    uint32_t vm_nx = 0;
     auto prefetch = [&](int s0) {
-        const int last = s_hi - 1;
+        const int so = s0 * 4;
 #pragma unroll
         for (int k = 0; k < 4; k++)
-            vp_nx[k] = reinterpret_cast<const uint2*>(
-                a.vpay + ((size_t)min(s0 + vp_tok[k], last) * 4 + h) * 104)[vp_part[k]];
-        const size_t row = (size_t)min(s0 + li, last) * 4 + h;
-        vn_nx = reinterpret_cast<const unsigned short*>(a.vnorm)[row];
-        ve_nx = reinterpret_cast<const unsigned short*>(a.vrn)[row];
-        vm_nx = reinterpret_cast<const float*>(a.vsm)[row];
+            vp_nx[k] = __builtin_amdgcn_raw_buffer_load_b64(rs_vp, vo_vp[k], so * 104, 0);
+        vn_nx = __builtin_amdgcn_raw_buffer_load_b16(rs_vn, vo_n * 2, so * 2, 0);
+        ve_nx = __builtin_amdgcn_raw_buffer_load_b16(rs_ve, vo_n * 2, so * 2, 0);
+        vm_nx = __builtin_amdgcn_raw_buffer_load_b32(rs_vm, vo_n * 4, so * 4, 0);
     };
     if (n_tiles > 0) prefetch(s_lo);
     query_transform(a, S, h, 3, lane);
@@ -572,13 +588,13 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, int h, in
 #pragma unroll
             for (int k = 0; k < 4; k++)
                 if (lane + 64 * k < TT * 13)
-                    *reinterpret_cast<uint2*>(&vpw[vp_tok[k] * VP_TS + vp_part[k] * 2]) =
-                        s0 + vp_tok[k] < s_hi ? vp_nx[k] : uint2{0, 0};
+                    *reinterpret_cast<u2v*>(&vpw[vp_tok[k] * VP_TS + vp_part[k] * 2]) =
+                        s0 + vp_tok[k] < s_hi ? vp_nx[k] : u2v{0, 0};
             if (lg == 0) {
                 const bool ok = s0 + li < s_hi;
                 const float nv = ok ? __half2float(__ushort_as_half(vn_nx)) : 0.0f;
                 const float en = ok ? __half2float(__ushort_as_half(ve_nx)) : 0.0f;
-                const float vm = ok ? vm_nx : 0.0f;
+                const float vm = ok ? __uint_as_float(vm_nx) : 0.0f;
                 S.vsc[h][0][li] = (av * nv) * en;
                 S.vsc[h][1][li] = av * nv;
                 S.vsc[h][2][li] = nv * vm / 7.0f;
@@ -614,13 +630,8 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, int h, in
                     const f4 sv = *reinterpret_cast<const f4*>(&S.vsc[h][v][4 * lg]);
                     const f4 w = pw4 * sv;
                     if (v == 2 && !r_lo) s3p += (w[0] + w[1]) + (w[2] + w[3]);
-#pragma unroll
-                    for (int e = 0; e < 4; e += 2) {
-                        _Float16 h0, h1, l0, l1;
-                        split2(w[e], w[e + 1], h0, h1, l0, l1);
-                        Ap[v][e] = r_lo ? l0 : h0;
-                        Ap[v][e + 1] = r_lo ? l1 : h1;
-                    }
+                    const uint2 pk = uint2{part_pk(w[0], w[1], m_lo), part_pk(w[2], w[3], m_lo)};
+                    Ap[v] = __builtin_bit_cast(h4, pk);
                 }
             }
 

@@ -82,6 +82,40 @@ __device__ __forceinline__ void split(float x, _Float16& hi, _Float16& lo) {
     lo = (_Float16)(x - (float)hi);
 }
 
+// x + m * (float)h where h is the low / high fp16 half of a packed pair
+// (v_fma_mix: the fp16 operand is widened exactly, one rounding).
+__device__ __forceinline__ float mix_lo(uint32_t hp, float m, float x) {
+    float d;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(hp), "v"(m), "v"(x));
+    return d;
+}
+__device__ __forceinline__ float mix_hi(uint32_t hp, float m, float x) {
+    float d;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "=v"(d) : "v"(hp), "v"(m), "v"(x));
+    return d;
+}
+__device__ __forceinline__ uint32_t pk_rtz(float x, float y) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x, y));
+}
+// Packed fp16 hi (truncated) and lo (remainder) parts of (x, y).
+__device__ __forceinline__ void split_pk(float x, float y, uint32_t& hi, uint32_t& lo) {
+    hi = pk_rtz(x, y);
+    lo = pk_rtz(mix_lo(hi, -1.0f, x), mix_hi(hi, -1.0f, y));
+}
+// One of the two parts per lane: m = 0 gives hi, m = -1 gives lo.
+__device__ __forceinline__ uint32_t part_pk(float x, float y, float m) {
+    const uint32_t hi = pk_rtz(x, y);
+    return pk_rtz(mix_lo(hi, m, x), mix_hi(hi, m, y));
+}
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// Buffer resource over n_bytes at p: loads past the end return zeros.
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t n_bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)n_bytes,
+                                             0x00020000);
+}
+
 // Unnormalised FWHT-256 across a wavefront holding 4 consecutive dims per lane.
 __device__ __forceinline__ void fwht256(float (&v)[4], int lane) {
     float a = v[0], b = v[1];

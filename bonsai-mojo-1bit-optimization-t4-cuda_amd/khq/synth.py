@@ -6,7 +6,8 @@ Two kinds of compressed rows:
     positions, the other dims uniform over {0, 1, 2}; uniform nibbles and sign
     bits; c_base_mult word uniform in [100, 10000]; norms ~ U(0.5, 2); small
     positive residual scales; uniform 12-bit V fields and VQ high bits.
-  * rows made by compressing N(0,1) K/V tokens (what a decode run produces).
+  * compressed_rows(): the library's own compression of N(0,1) K/V rows
+    (what a decode run produces; ~11% outlier dims per K row).
 Everything is generated with torch on the requested device from a seed.
 """
 from __future__ import annotations
@@ -63,6 +64,21 @@ def random_rows(rows: int, seed: int = 1234, device="cuda") -> dict:
     vsm = _uniform((rows,), 0.01, 0.05, g, dev, torch.float32).view(torch.uint8).view(rows, 4)
     return {"kmask": kmask, "kpay": kpay, "knorm": knorm, "krn": krn, "vpay": vpay,
             "vnorm": vnorm, "vrn": vrn, "vsm": vsm.contiguous()}
+
+
+def compressed_rows(pay, cents, seed: int = 1234, chunk: int = 32768) -> None:
+    """Fills every row of `pay` (row = token * H_kv + head) with the library's
+    own compression of N(0,1) fp16 K and V rows (what a decode run's cache
+    holds), seeded, chunk rows at a time on the payload's device."""
+    from . import ops
+
+    g = _gen(seed, pay.kmask.device)
+    for r0 in range(0, pay.rows, chunk):
+        n = min(chunk, pay.rows - r0)
+        xk = torch.randn((n, D), generator=g, device=pay.kmask.device).to(torch.float16)
+        ops.compress(xk, cents, pay, r0, is_v=False)
+        xv = torch.randn((n, D), generator=g, device=pay.kmask.device).to(torch.float16)
+        ops.compress(xv, cents, pay, r0, is_v=True)
 
 
 def rope_halfsplit(x: torch.Tensor, positions: torch.Tensor, rot: int = ROT_DIM,
