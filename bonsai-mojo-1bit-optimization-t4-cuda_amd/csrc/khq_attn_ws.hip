@@ -165,14 +165,13 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
 #pragma unroll
         for (int Tp = 0; Tp < 4; Tp++) dsgn[Tp] = (__half2float(dj[Tp]) < 0.0f) ? -1.0f : 1.0f;
 #pragma unroll
-        for (int kk = 0; kk < 2; kk++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const h4 q4 = __builtin_bit_cast(h4, qv[2 * kk + (e >> 2)]);
-                _Float16 hi, lo;
-                split((float)q4[e & 3], hi, lo);
-                Aq[kk][e] = arow_ok ? (arow_lo ? lo : hi) : (_Float16)0.0f;
-            }
+        for (int kk = 0; kk < 2; kk++) {
+            const h4 qa = __builtin_bit_cast(h4, qv[2 * kk]), qb = __builtin_bit_cast(h4, qv[2 * kk + 1]);
+            const float mq = arow_lo ? -1.0f : 0.0f;
+            const uint4 w = uint4{part_pk((float)qa[0], (float)qa[1], mq), part_pk((float)qa[2], (float)qa[3], mq),
+                                  part_pk((float)qb[0], (float)qb[1], mq), part_pk((float)qb[2], (float)qb[3], mq)};
+            Aq[kk] = __builtin_bit_cast(h8, arow_ok ? w : uint4{0u, 0u, 0u, 0u});
+        }
     }
     // ---- staging: mask words 4 lg .. 4 lg + 3 of (token li, head h) straight
     // to registers; kpay rows through LDS; norms to registers.  Buffer loads
@@ -208,6 +207,7 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
     __syncthreads();  // (1) tables, staged rotors and query transforms in place
     PHASE(1);
 
+    const float m_lo = arow_lo ? -1.0f : 0.0f;  // part_pk: lo rows take the remainder
     h8 At[8];
 #pragma unroll
     for (int st = 0; st < 8; st++) {
@@ -216,12 +216,8 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
             u0 = *reinterpret_cast<const f4*>(&tq[arow_h * 256 + 64 * lg + 8 * st]);
             u1 = *reinterpret_cast<const f4*>(&tq[arow_h * 256 + 64 * lg + 8 * st + 4]);
         }
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            _Float16 hi, lo;
-            split(e < 4 ? u0[e] : u1[e - 4], hi, lo);
-            At[st][e] = arow_lo ? lo : hi;
-        }
+        At[st] = __builtin_bit_cast(h8, uint4{part_pk(u0[0], u0[1], m_lo), part_pk(u0[2], u0[3], m_lo),
+                                              part_pk(u1[0], u1[1], m_lo), part_pk(u1[2], u1[3], m_lo)});
     }
     // fold: z_(4q+c') = sum over blocks b of sum_k R_(16b+q)[c'][k] b_(64b+4q+k).
     // K-step st carries q = 2 st + e/4 of block lg; M-tile T = st / 2 holds
@@ -230,13 +226,14 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
     const _Float16* rk_lds = reinterpret_cast<const _Float16*>(S.vp);
     const int s_fold = li >> 3;
     h8 Aw[4];
+    {
+        const bool upper = ((li >> 2) & 1) != 0;  // entries e = 4..7 (else 0..3)
 #pragma unroll
-    for (int T = 0; T < 4; T++) {
-        const int p = 16 * lg + 4 * T + (li >> 2);
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-            Aw[T][e] = ((e >> 2) == ((li >> 2) & 1)) ? rk_lds[p * 16 + (li & 3) * 4 + (e & 3)]
-                                                     : (_Float16)0.0f;
+        for (int T = 0; T < 4; T++) {
+            const int p = 16 * lg + 4 * T + (li >> 2);
+            const uint2 r = *reinterpret_cast<const uint2*>(&rk_lds[p * 16 + (li & 3) * 4]);
+            Aw[T] = __builtin_bit_cast(h8, upper ? uint4{0u, 0u, r.x, r.y} : uint4{r.x, r.y, 0u, 0u});
+        }
     }
     const h8 hzero = {0, 0, 0, 0, 0, 0, 0, 0};
     // H_64 = H_4 (x) H_16 (j = 16 T' + li, m = 16 T + 4 lg + c'):
@@ -244,17 +241,27 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
     // H_4 rows: T'=0 [+ + + +], 1 [+ - + -], 2 [+ + - -], 3 [+ - - +] over
     // T = (kk, e/4).
     h8 Ah[4][2];
+    {
+        float g4[4];
 #pragma unroll
-    for (int Tp = 0; Tp < 4; Tp++)
+        for (int c = 0; c < 4; c++)
+            g4[c] = ((__popc(li & (4 * lg + c)) & 1) ? -1.0f : 1.0f) / 256.0f;
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const float g = ((__popc(li & (4 * lg + (e & 3))) & 1) ? -dsgn[Tp] : dsgn[Tp]) / 256.0f;
-            const int T0 = e >> 2, T1 = 2 + (e >> 2);
-            const float h0 = (__popc(Tp & T0) & 1) ? -g : g;
-            const float h1 = (__popc(Tp & T1) & 1) ? -g : g;
-            Ah[Tp][0][e] = (_Float16)h0;
-            Ah[Tp][1][e] = (_Float16)h1;
+        for (int Tp = 0; Tp < 4; Tp++) {
+            _Float16 pos[4], neg[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                pos[c] = (_Float16)(g4[c] * dsgn[Tp]);
+                neg[c] = -pos[c];
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int T0 = e >> 2, T1 = 2 + (e >> 2);
+                Ah[Tp][0][e] = (__popc(Tp & T0) & 1) ? neg[e & 3] : pos[e & 3];
+                Ah[Tp][1][e] = (__popc(Tp & T1) & 1) ? neg[e & 3] : pos[e & 3];
+            }
         }
+    }
     wave_sync();
     // clear this lane's outlier strip (the query scratch is no longer needed)
     _Float16* orow = &S.o[h][lane * O_LS];
