@@ -88,37 +88,59 @@ struct __align__(16) Smem {
     float s3[4][8];              // final dump-offset sums per query head
 };
 
+// Per-lane global inputs of the block set-up, all loaded at kernel entry so
+// their latency overlaps the table copies.
+struct SetupIn {
+    uint2 qr[3];    // q dims 4 lane .. + 3 of the 3 heads this wavefront transforms
+    uint2 dkr;      // d_k dims 4 lane .. + 3
+    uint4 rk[2];    // rotor_k of patch `lane`
+    uint2 qv[4];    // key wavefronts: q dims 16 T' + 4 lg .. + 3 of head min(li / 2, 5)
+    unsigned short dj[4];  // key wavefronts: d_k[16 T' + li]
+};
+
+__device__ __forceinline__ void load_setup(const AttnArgs& a, int h, int wv, int lane, SetupIn& in) {
+    const int li = lane & 15, lg = lane >> 4;
+    const __half* qbase = a.q + (size_t)(h * 6 + 3 * (wv >> 2)) * 512;
+#pragma unroll
+    for (int hd = 0; hd < 3; hd++) in.qr[hd] = *reinterpret_cast<const uint2*>(qbase + hd * 512 + lane * 4);
+    in.dkr = *reinterpret_cast<const uint2*>(a.dk + lane * 4);
+    const uint4* rp = reinterpret_cast<const uint4*>(a.rotor_k + lane * 16);
+    in.rk[0] = rp[0];
+    in.rk[1] = rp[1];
+    const __half* qrow = a.q + (size_t)(h * 6 + min(li >> 1, 5)) * 512;
+#pragma unroll
+    for (int Tp = 0; Tp < 4; Tp++) {
+        in.dj[Tp] = reinterpret_cast<const unsigned short*>(a.dk)[16 * Tp + li];
+        in.qv[Tp] = *reinterpret_cast<const uint2*>(qrow + 16 * Tp + 4 * lg);
+    }
+}
+
 // Query side of the pass part for 3 query heads of KV head h (heads hd0 ..
 // hd0 + 2): tq_hd = R^T H (q_hd[64:] / (256 d)) into S.o[h] as floats [6][256].
-__device__ __forceinline__ void query_transform(const AttnArgs& a, Smem& S, int h, int hd0,
+__device__ __forceinline__ void query_transform(const SetupIn& in, Smem& S, int h, int hd0,
                                                 int lane) {
-    const __half* qbase = a.q + (size_t)(h * 6 + hd0) * 512;
     float* tq = reinterpret_cast<float*>(S.o[h]) + hd0 * 256;
+    const h4 dk4 = __builtin_bit_cast(h4, in.dkr);
     float dks[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++)
-        dks[c] = (1.0f / 256.0f) / (__half2float(a.dk[lane * 4 + c]) + 1e-8f);
+    for (int c = 0; c < 4; c++) dks[c] = (1.0f / 256.0f) / ((float)dk4[c] + 1e-8f);
 #pragma unroll
     for (int hd = 0; hd < 3; hd++) {
-        const uint2 qr = *reinterpret_cast<const uint2*>(qbase + hd * 512 + lane * 4);
-        const __half* qh = reinterpret_cast<const __half*>(&qr);
+        const h4 qh = __builtin_bit_cast(h4, in.qr[hd]);
         f4 v;
 #pragma unroll
-        for (int c = 0; c < 4; c++) v[c] = lane >= 16 ? __half2float(qh[c]) * dks[c] : 0.0f;
+        for (int c = 0; c < 4; c++) v[c] = lane >= 16 ? (float)qh[c] * dks[c] : 0.0f;
         *reinterpret_cast<f4*>(&tq[hd * 256 + lane * 4]) = v;
     }
     wave_sync();
     fwht256_lds(tq, 3, lane);
     float rk[16];
     {
-        const uint4* rp = reinterpret_cast<const uint4*>(a.rotor_k + lane * 16);
-        const uint4 r0 = rp[0], r1 = rp[1];
-        const __half* rh0 = reinterpret_cast<const __half*>(&r0);
-        const __half* rh1 = reinterpret_cast<const __half*>(&r1);
+        const h8 r0 = __builtin_bit_cast(h8, in.rk[0]), r1 = __builtin_bit_cast(h8, in.rk[1]);
 #pragma unroll
         for (int t = 0; t < 8; t++) {
-            rk[t] = __half2float(rh0[t]);
-            rk[8 + t] = __half2float(rh1[t]);
+            rk[t] = (float)r0[t];
+            rk[8 + t] = (float)r1[t];
         }
     }
     // per patch: t[4p + k] = sum_c u[4p + c] R_p[c][k]
@@ -139,8 +161,8 @@ __device__ __forceinline__ void query_transform(const AttnArgs& a, Smem& S, int 
 }
 
 // ---------------------------------------------------------------- key role
-__device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int lane,
-                                         int s_lo, int s_hi, int n_tiles PH_PARAMS) {
+__device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const SetupIn& in, int h,
+                                         int lane, int s_lo, int s_hi, int n_tiles PH_PARAMS) {
     const int li = lane & 15, lg = lane >> 4;
     const float* tq = reinterpret_cast<const float*>(S.o[h]);  // [6][256] query transforms
 
@@ -154,16 +176,10 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
     float dsgn[4];
     h8 Aq[2];
     {
-        uint2 qv[4];
-        __half dj[4];
-        const __half* qrow = a.q + (size_t)(h * 6 + min(arow_h, 5)) * 512;
+        const uint2* qv = in.qv;
 #pragma unroll
-        for (int Tp = 0; Tp < 4; Tp++) {
-            dj[Tp] = a.dk[16 * Tp + li];
-            qv[Tp] = *reinterpret_cast<const uint2*>(qrow + 16 * Tp + 4 * lg);
-        }
-#pragma unroll
-        for (int Tp = 0; Tp < 4; Tp++) dsgn[Tp] = (__half2float(dj[Tp]) < 0.0f) ? -1.0f : 1.0f;
+        for (int Tp = 0; Tp < 4; Tp++)
+            dsgn[Tp] = (__half2float(__ushort_as_half(in.dj[Tp])) < 0.0f) ? -1.0f : 1.0f;
 #pragma unroll
         for (int kk = 0; kk < 2; kk++) {
             const h4 qa = __builtin_bit_cast(h4, qv[2 * kk]), qb = __builtin_bit_cast(h4, qv[2 * kk + 1]);
@@ -202,7 +218,7 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
         kp_nx1 = __builtin_amdgcn_raw_buffer_load_b64(rs_kp, vo_kp1, so * 40, 0);
     };
     if (n_tiles > 0) prefetch(s_lo);
-    query_transform(a, S, h, 0, lane);
+    query_transform(in, S, h, 0, lane);
 
     __syncthreads();  // (1) tables, staged rotors and query transforms in place
     PHASE(1);
@@ -525,8 +541,8 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, int h, int 
 }
 
 // -------------------------------------------------------------- value role
-__device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, int h, int lane,
-                                           int s_lo, int s_hi, int n_tiles PH_PARAMS) {
+__device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const SetupIn& in, int h,
+                                           int lane, int s_lo, int s_hi, int n_tiles PH_PARAMS) {
     const int li = lane & 15, lg = lane >> 4;
 
     const int r_head = li >> 1;       // A row li: head li / 2, hi (even) or lo (odd)
@@ -567,9 +583,25 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, int h, in
         vm_nx = __builtin_amdgcn_raw_buffer_load_b32(rs_vm, vo_n * 4, so * 4, 0);
     };
     if (n_tiles > 0) prefetch(s_lo);
-    query_transform(a, S, h, 3, lane);
+    query_transform(in, S, h, 3, lane);
     __syncthreads();  // (1)
     PHASE(8);
+    // V codebook (96 KB), copied by these wavefronts alone while the key
+    // wavefronts start on the first tile; it is read from the first decode on,
+    // which comes after the next block barrier.
+    {
+        const int vt = h * 64 + lane;
+        const uint4* cbsrc = reinterpret_cast<const uint4*>(a.vq);
+        uint4* cbdst = reinterpret_cast<uint4*>(S.cb);
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            uint4 cbt[12];
+#pragma unroll
+            for (int i = 0; i < 12; i++) cbt[i] = cbsrc[vt + 256 * (12 * b + i)];
+#pragma unroll
+            for (int i = 0; i < 12; i++) cbdst[vt + 256 * (12 * b + i)] = cbt[i];
+        }
+    }
     // lane constants: patch p = 16 g + li for g = 0..3
     _Float16 c3a[4], c3b[4];
 #pragma unroll
@@ -723,15 +755,11 @@ __global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_
     for (int k = 0; k < 16; k++) ph_acc[k] = 0;
 #endif
 
-    // ---- shared tables: codebook, sign table, cents_k[2], rotor_k, RoPE
+    // ---- shared tables: sign table, cents_k[2], rotors, d_v, RoPE (the value
+    // wavefronts copy the codebook themselves, after this point)
+    SetupIn in;
     {
-        const uint4* src = reinterpret_cast<const uint4*>(a.vq);
-        uint4* dst = reinterpret_cast<uint4*>(S.cb);
-        uint4 tmp[12];
-#pragma unroll
-        for (int i = 0; i < 12; i++) tmp[i] = src[tid + NTHR * i];
-#pragma unroll
-        for (int i = 0; i < 12; i++) dst[tid + NTHR * i] = tmp[i];
+        load_setup(a, h, wv, lane, in);
         if (tid < 256) {
             h4 s;
 #pragma unroll
@@ -770,9 +798,9 @@ __global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_
     PHASE(0);
 
     if (wv < 4) {
-        key_role(a, S, h, lane, s_lo, s_hi, n_tiles PH_ARGS);
+        key_role(a, S, in, h, lane, s_lo, s_hi, n_tiles PH_ARGS);
     } else {
-        value_role(a, S, h, lane, s_lo, s_hi, n_tiles PH_ARGS);
+        value_role(a, S, in, h, lane, s_lo, s_hi, n_tiles PH_ARGS);
     }
 #ifdef KHQ_PHASE_TIMING
     ph_t = __builtin_amdgcn_s_memtime();
@@ -783,6 +811,9 @@ __global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_
     float rv[16];
 #pragma unroll
     for (int t = 0; t < 16; t++) rv[t] = (float)S.rotv[lane * 16 + t];
+    float rdv[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) rdv[c] = (1.0f / 16.0f) / ((float)S.dvh[lane * 4 + c] + 1e-8f);
 #pragma unroll
     for (int hh = 0; hh < 3; hh++) {
         const int hd = 3 * (wv >> 2) + hh;
@@ -806,7 +837,7 @@ __global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_
 #pragma unroll
         for (int c = 0; c < 4; c++)
             out[lane * 4 + c] =
-                empty ? 0.0f : (u[c] * (1.0f / 16.0f)) / ((float)S.dvh[lane * 4 + c] + 1e-8f);
+                empty ? 0.0f : u[c] * rdv[c];
         if (lane == 0) {
             out[256] = empty ? -1e20f : M;
             out[257] = empty ? 0.0f : L;
