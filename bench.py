@@ -176,7 +176,7 @@ def main():
             "unit": "GB/s",
             "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic.get("traffic_bytes_scaled"),
-            "traffic_128b_requests": traffic.get("traffic_bytes_128b_requests"),
+            "traffic_fetch_factor": traffic.get("fetch_factor"),
             "avg_kernel_us": round(kern_us, 3),
             "bytes_per_launch": c_bytes,
         },
