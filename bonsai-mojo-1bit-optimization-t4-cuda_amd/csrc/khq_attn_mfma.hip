@@ -910,7 +910,7 @@ int attn_mfma_tiles_per_chunk(int c_len, int* n_chunks) {
     static const int max_chunks = [] {
         const char* e = getenv("KHQ_MFMA_MAX_CHUNKS");
         const int v = e ? atoi(e) : 0;
-        return v > 0 ? v : 256;
+        return v > 0 ? v : 255;  // one CU left for the window block
     }();
     const int tiles = (c_len + mf::TT - 1) / mf::TT;
     int chunks = tiles < max_chunks ? tiles : max_chunks;

@@ -735,7 +735,139 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
     PHASE(14);
 }
 
-__global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_per_chunk) {
+// ------------------------------------------------------------ window block
+// The raw ring window (fp16, K already roped) for all 24 query heads, in the
+// block after the last compressed chunk.  Wavefront w serves KV head w % 4
+// and half w / 4 of the window rows (win_len <= 256):
+//   scores q.k on MFMA (A = the 6 query rows of the group, B = K rows, both
+//   exact fp16, fp32 accumulate) into LDS;
+//   softmax per query head over the whole window in LDS;
+//   P x V on the vector ALUs, lane l holding dims 4 l .. 4 l + 3;
+// then the two halves of each KV head are added into one partial triple.
+__device__ void window_block(const AttnArgs& a, Smem& S, int part_idx) {
+    constexpr int WMAX = 256;
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    const int li = lane & 15, lg = lane >> 4;
+    const int hk = wv & 3, half = wv >> 2;
+    const int wl = a.win_len;
+    const int hw = ((wl + 31) / 32) * 16;  // rows per half, a multiple of 16
+    const int r_lo = half * hw, r_hi = min(wl, r_lo + hw);
+    float* sp = reinterpret_cast<float*>(S.cb);          // [4][6][WMAX] scores, then weights
+    float* sml = sp + 4 * 6 * WMAX;                      // [4][6][2] max, sum
+    float* sacc = sml + 4 * 6 * 2;                       // [4][6][256] half-1 numerators
+    auto slot_of = [&](int s) {
+        const int x = a.win_start + s;
+        return x >= a.ring_cap ? x - a.ring_cap : x;
+    };
+    // ---- scores: rows 0..5 of A are the group's query heads (hi only: q is fp16)
+    h8 Aqk[8];
+    {
+        const __half* qrow = a.q + (size_t)(hk * 6 + min(li, 5)) * 512;
+#pragma unroll
+        for (int st = 0; st < 8; st++) {
+            const uint4 v = *reinterpret_cast<const uint4*>(qrow + 32 * st + 8 * lg);
+            Aqk[st] = __builtin_bit_cast(h8, li < 6 ? v : uint4{0u, 0u, 0u, 0u});
+        }
+    }
+    for (int r0 = r_lo; r0 < r_hi; r0 += 32) {  // two 16-row tiles' loads in flight
+        uint4 kv[2][8];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int slot = slot_of(min(r0 + 16 * u + li, wl - 1));
+            const __half* krow = a.ring_k + ((size_t)slot * a.h_kv + hk) * 256 + 8 * lg;
+#pragma unroll
+            for (int st = 0; st < 8; st++) kv[u][st] = *reinterpret_cast<const uint4*>(krow + 32 * st);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int s = r0 + 16 * u + li;
+            if (r0 + 16 * u >= r_hi) break;
+            f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 8; st++) acc = mfma32(Aqk[st], __builtin_bit_cast(h8, kv[u][st]), acc);
+            // C rows 4 lg + c = query head, column li = row s
+            if (lg < 2) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const int hd = 4 * lg + c;
+                    if (hd < 6 && s < r_hi) sp[(hk * 6 + hd) * WMAX + s] = acc[c] * a.sc;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // ---- softmax: wavefront (hk, half) owns heads 3 half .. + 2 of KV head hk
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        float* row = sp + (hk * 6 + 3 * half + i) * WMAX;
+        float m = -INFINITY;
+        for (int s = lane; s < wl; s += 64) m = fmaxf(m, row[s]);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        float l = 0.0f;
+        for (int s = lane; s < wl; s += 64) {
+            const float p = __expf(row[s] - m);
+            row[s] = p;
+            l += p;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
+        if (lane == 0) {
+            sml[(hk * 6 + 3 * half + i) * 2 + 0] = m;
+            sml[(hk * 6 + 3 * half + i) * 2 + 1] = l;
+        }
+    }
+    __syncthreads();
+    // ---- P x V over this half's rows
+    float acc[6][4];
+#pragma unroll
+    for (int i = 0; i < 6; i++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[i][c] = 0.0f;
+    for (int s0 = r_lo; s0 < r_hi; s0 += 16) {  // 16 rows' loads in flight at once
+        uint2 vr[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int slot = slot_of(min(s0 + u, r_hi - 1));
+            vr[u] = *reinterpret_cast<const uint2*>(a.ring_v + ((size_t)slot * a.h_kv + hk) * 256 + 4 * lane);
+        }
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            if (s0 + u >= r_hi) break;
+            const h4 vh = __builtin_bit_cast(h4, vr[u]);
+#pragma unroll
+            for (int i = 0; i < 6; i++) {
+                const float p = sp[(hk * 6 + i) * WMAX + s0 + u];
+#pragma unroll
+                for (int c = 0; c < 4; c++) acc[i][c] = fmaf(p, (float)vh[c], acc[i][c]);
+            }
+        }
+    }
+    if (half == 1) {
+#pragma unroll
+        for (int i = 0; i < 6; i++)
+            *reinterpret_cast<f4*>(&sacc[(hk * 6 + i) * 256 + 4 * lane]) =
+                f4{acc[i][0], acc[i][1], acc[i][2], acc[i][3]};
+    }
+    __syncthreads();
+    if (half == 0) {
+#pragma unroll
+        for (int i = 0; i < 6; i++) {
+            const f4 o = *reinterpret_cast<const f4*>(&sacc[(hk * 6 + i) * 256 + 4 * lane]);
+            const int hq = hk * 6 + i;
+            float* out = a.part + ((size_t)hq * a.part_stride + part_idx) * 258;
+            *reinterpret_cast<f4*>(&out[4 * lane]) =
+                f4{acc[i][0] + o[0], acc[i][1] + o[1], acc[i][2] + o[2], acc[i][3] + o[3]};
+            if (lane == 0) {
+                out[256] = sml[(hk * 6 + i) * 2 + 0];
+                out[257] = sml[(hk * 6 + i) * 2 + 1];
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_per_chunk,
+                                                          int n_chunks) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem& S = *reinterpret_cast<Smem*>(smem_raw);
     const int tid = threadIdx.x;
@@ -743,6 +875,10 @@ __global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_
     const int h = wv & 3;
     const int lane = tid & 63;
     const int chunk = blockIdx.x;
+    if (chunk >= n_chunks) {  // the block after the compressed chunks
+        window_block(a, S, a.part_offset + n_chunks);
+        return;
+    }
     const int c_len = a.c_len;
     const int s_lo = min(chunk * tiles_per_chunk * TT, c_len);
     const int s_hi = min(s_lo + tiles_per_chunk * TT, c_len);
@@ -867,8 +1003,9 @@ hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks, 
         if (e != hipSuccess) return e;
         configured = true;
     }
-    hipLaunchKernelGGL(ws::attn_ws_kernel, dim3(n_chunks), dim3(ws::NTHR), smem, st, a,
-                       tiles_per_chunk);
+    const int blocks = n_chunks + (a.win_len > 0 ? 1 : 0);
+    hipLaunchKernelGGL(ws::attn_ws_kernel, dim3(blocks), dim3(ws::NTHR), smem, st, a,
+                       tiles_per_chunk, n_chunks);
     return hipGetLastError();
 }
 

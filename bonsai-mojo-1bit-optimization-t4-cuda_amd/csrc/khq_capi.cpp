@@ -334,14 +334,20 @@ int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_
     if (win_len > 0 && (ring_cap <= 0 || win_len > ring_cap || win_start < 0)) return -100;
     const int n_rep = H_q / H_kv;
     const int npc = compressed_parts(c_len, n_rep, H_kv, 1);
-    // Short windows (the KHQ ring holds 256 slots): window, merge and gate in
-    // one finishing launch.  Longer ones: window partials + combine.
-    const bool fused_tail = win_len <= 256 && npc <= 1024;
-    const int npw = (win_len > 0 && !fused_tail) ? window_parts(win_len) : 0;
+    // Short windows (the KHQ ring holds 256 slots): window, merge and gate
+    // without window partials.  With the wavefront-specialised kernel the
+    // window is one extra block of the compressed launch (partial npc) and the
+    // finishing launch only merges; otherwise the finishing launch computes
+    // the window too.  Longer windows: window partials + combine.
+    const bool fused_tail = win_len <= 256 && npc <= 1000;
+    const bool win_in_ws = fused_tail && npc > 0 && win_len > 0 && g_kernel_choice == 0 &&
+                           use_mfma(n_rep, H_kv, 1);
+    const int npw = (win_len > 0 && !fused_tail) ? window_parts(win_len) : (win_in_ws ? 1 : 0);
     const int np = npc + npw;
     float* ws = nullptr;
     hipError_t e = workspace((size_t)H_q * std::max(np, 1) * 258 * sizeof(float), &ws);
     if (e != hipSuccess) return rc_of(e);
+    const int ring = ring_cap > 0 ? ring_cap : 1;
     if (npc > 0) {
         khq::AttnArgs a = attn_args(q_gate, k_payload, v_payload, v_shared_meta, k_mask,
                                     k_norms, k_r_norms, v_norms, v_r_norms, centroids_k,
@@ -359,6 +365,13 @@ int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_
         a.a_k = alpha_k;
         a.a_v = alpha_v;
         a.rope_base = rope_base;
+        if (win_in_ws) {
+            a.ring_k = static_cast<const __half*>(ring_k);
+            a.ring_v = static_cast<const __half*>(ring_v);
+            a.win_start = win_start % ring;
+            a.win_len = win_len;
+            a.ring_cap = ring;
+        }
         int used = 0;
         e = launch_compressed(a, n_rep, 1, &used, stream);
         if (e != hipSuccess) return rc_of(e);
@@ -366,14 +379,14 @@ int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_
     if (fused_tail) {
         khq::FinishArgs f{};
         f.part = ws;
-        f.n_parts = npc;
+        f.n_parts = np;
         f.part_stride = np;
         f.q = static_cast<const __half*>(q_gate);
         f.ring_k = static_cast<const __half*>(ring_k);
         f.ring_v = static_cast<const __half*>(ring_v);
-        f.ring_cap = ring_cap > 0 ? ring_cap : 1;
-        f.win_start = win_start % f.ring_cap;
-        f.win_len = win_len;
+        f.ring_cap = ring;
+        f.win_start = win_start % ring;
+        f.win_len = win_in_ws ? 0 : win_len;
         f.h_kv = H_kv;
         f.n_rep = n_rep;
         f.sc = scale;

@@ -21,7 +21,7 @@ using namespace mu;
 
 constexpr int DS = 32;         // dims per block
 constexpr int MAX_WIN = 256;   // ring capacity bound
-constexpr int MAX_PARTS = 1024;
+constexpr int MAX_PARTS = 1024;  // compressed partials (+ a window partial)
 
 __device__ __forceinline__ float block_max(float v, float* s_red) {
     v = fmaxf(v, __shfl_xor(v, 1, 64));

@@ -30,6 +30,12 @@ struct AttnArgs {
     float* part;
     int c_len, h_kv, L_q, start_pos, n_parts, part_stride, part_offset;
     float sc, a_k, a_v, rope_base;
+    // Optional raw ring window, computed by one extra block of the
+    // wavefront-specialised kernel into partial part_offset + n_chunks
+    // (win_len = 0: none).
+    const __half* ring_k;
+    const __half* ring_v;
+    int win_start, win_len, ring_cap;
 };
 
 // fp16 ring-window work, same partial layout (query = head).
