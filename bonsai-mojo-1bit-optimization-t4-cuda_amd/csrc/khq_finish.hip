@@ -23,36 +23,42 @@ constexpr int DS = 32;         // dims per block
 constexpr int MAX_WIN = 256;   // ring capacity bound
 constexpr int MAX_PARTS = 1024;  // compressed partials (+ a window partial)
 
-__device__ __forceinline__ float block_max(float v, float* s_red) {
-    v = fmaxf(v, __shfl_xor(v, 1, 64));
-    v = fmaxf(v, __shfl_xor(v, 2, 64));
-    v = fmaxf(v, __shfl_xor(v, 4, 64));
-    v = fmaxf(v, __shfl_xor(v, 8, 64));
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    v = fmaxf(v, __shfl_xor(v, 32, 64));
+// Block-wide max of (x, y) in one pass; s_red holds 8 floats.
+__device__ __forceinline__ void block_max2(float& x, float& y, float* s_red) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        x = fmaxf(x, __shfl_xor(x, o, 64));
+        y = fmaxf(y, __shfl_xor(y, o, 64));
+    }
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+    if ((threadIdx.x & 63) == 0) {
+        s_red[threadIdx.x >> 6] = x;
+        s_red[4 + (threadIdx.x >> 6)] = y;
+    }
     __syncthreads();
-    return fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    x = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    y = fmaxf(fmaxf(s_red[4], s_red[5]), fmaxf(s_red[6], s_red[7]));
 }
-
-__device__ __forceinline__ float block_sum(float v, float* s_red) {
-    v += __shfl_xor(v, 1, 64);
-    v += __shfl_xor(v, 2, 64);
-    v += __shfl_xor(v, 4, 64);
-    v += __shfl_xor(v, 8, 64);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
+__device__ __forceinline__ void block_sum2(float& x, float& y, float* s_red) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        x += __shfl_xor(x, o, 64);
+        y += __shfl_xor(y, o, 64);
+    }
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+    if ((threadIdx.x & 63) == 0) {
+        s_red[threadIdx.x >> 6] = x;
+        s_red[4 + (threadIdx.x >> 6)] = y;
+    }
     __syncthreads();
-    return (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    x = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    y = (s_red[4] + s_red[5]) + (s_red[6] + s_red[7]);
 }
 
 __global__ __launch_bounds__(256) void step_finish_kernel(FinishArgs a) {
     __shared__ float s_p[MAX_WIN];      // window weights
     __shared__ float s_w[MAX_PARTS];    // compressed part weights
-    __shared__ float s_red[4];
+    __shared__ float s_red[8];
     __shared__ float s_acc[2][8][DS];
     const int t = threadIdx.x;
     const int hq = blockIdx.x;
@@ -81,9 +87,13 @@ __global__ __launch_bounds__(256) void step_finish_kernel(FinishArgs a) {
     for (int u = 0; u < 32; u++) pacc[u] = base[min(grp + 8 * u, last_p) * 258 + d0 + d];
     __half vw[32];   // window rows grp + 8 u
 #pragma unroll
-    for (int u = 0; u < 32; u++) {
-        const int slot = slot_of(min(grp + 8 * u, last_w));
-        vw[u] = a.ring_v[(slot * a.h_kv + hk) * 256 + d0 + d];
+    for (int u = 0; u < 32; u++) vw[u] = __ushort_as_half((unsigned short)0);
+    if (wl > 0) {
+#pragma unroll
+        for (int u = 0; u < 32; u++) {
+            const int slot = slot_of(min(grp + 8 * u, last_w));
+            vw[u] = a.ring_v[(slot * a.h_kv + hk) * 256 + d0 + d];
+        }
     }
     const int sub = t >> 4, l16 = t & 15;
     const __half* qrow = a.q + (size_t)hq * 512 + 16 * l16;
@@ -126,8 +136,8 @@ __global__ __launch_bounds__(256) void step_finish_kernel(FinishArgs a) {
 #pragma unroll
     for (int k = 0; k < MAX_PARTS / 256; k++)
         if (t + 256 * k < np) mcmax = fmaxf(mcmax, mcv[k]);
-    const float Mw = block_max(wmax, s_red);
-    const float Mc = block_max(mcmax, s_red);
+    float Mw = wmax, Mc = mcmax;
+    block_max2(Mw, Mc, s_red);
 
     // ---- weights: window exp(s - Mw), parts exp(m - Mc); zero past the ends,
     // so the sums below need no bounds (clamped loads hold finite values)
@@ -144,8 +154,8 @@ __global__ __launch_bounds__(256) void step_finish_kernel(FinishArgs a) {
         s_w[s] = wgt;
         lc = fmaf(s < np ? lcv[k] : 0.0f, wgt, lc);
     }
-    const float Lw = block_sum(lw, s_red);
-    const float Lc = block_sum(lc, s_red);  // its barriers also publish s_p / s_w
+    float Lw = lw, Lc = lc;
+    block_sum2(Lw, Lc, s_red);  // its barriers also publish s_p / s_w
 
     // ---- numerators for dims d0 + d: rows / parts strided by the 8 groups
     float aw[4] = {0.f, 0.f, 0.f, 0.f}, ac[4] = {0.f, 0.f, 0.f, 0.f};
