@@ -1,0 +1,219 @@
+// khq_layer.cpp -- per-layer KHQ runtime behind the C ABI (khq_layer_*).
+//
+// Native counterpart of the reference's per-layer state and step
+// (ref:src/khq/runtime.mojo:77-152 KhqLayer, :395-429 khq_init_layer,
+// :432-451 khq_capture_unroped, :454-613 khq_step): a 256-slot fp16 ring for
+// roped K, V and unroped K, the packed payload for cap tokens, the boundary /
+// write_pos cadence (compress 128 tokens once the raw window reaches 256) and
+// the two-region attention, all issued on the caller's stream.  Per-layer
+// constant tensors (centroids, rotors, d vectors) are device buffers owned by
+// the caller; the layer owns its rings, payload and scratch.
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include <algorithm>
+#include <new>
+
+#include "khq.h"
+
+namespace {
+
+constexpr int kRing = 256;       // ref runtime.mojo:36
+constexpr int kWatermark = 256;  // :37
+constexpr int kChunk = 128;      // :38
+constexpr int kMaxSplits = 64;   // workspace bound of the reference-sequence path
+constexpr int kD = 256;
+
+}  // namespace
+
+struct khq_layer {
+    int H_q = 0, H_kv = 0, cap = 0, splits = 1, fused = 1;
+    float ts_k = 0, alpha_k = 0, ts_v = 0, alpha_v = 0, rope_base = 0;
+    const void *cents_k = nullptr, *cents_v = nullptr, *vq = nullptr;
+    const void *rotor_k = nullptr, *rotor_v = nullptr, *d_k = nullptr, *d_v = nullptr;
+    // owned device memory
+    __half *ring_k = nullptr, *ring_v = nullptr, *ring_u = nullptr;
+    uint32_t* kmask = nullptr;
+    uint8_t *kpay = nullptr, *vpay = nullptr, *vsm = nullptr;
+    __half *knorm = nullptr, *krn = nullptr, *vnorm = nullptr, *vrn = nullptr;
+    float *ac = nullptr, *aw = nullptr, *ap = nullptr;
+    int boundary = 0, write_pos = 0, n_events = 0;
+};
+
+namespace {
+
+void release(khq_layer* L) {
+    void* ptrs[] = {L->ring_k, L->ring_v, L->ring_u, L->kmask, L->kpay, L->vpay, L->vsm,
+                    L->knorm, L->krn, L->vnorm, L->vrn, L->ac, L->aw, L->ap};
+    for (void* p : ptrs)
+        if (p) (void)hipFree(p);
+}
+
+template <typename T>
+bool alloc_zero(T** p, size_t bytes) {
+    if (hipMalloc(reinterpret_cast<void**>(p), bytes) != hipSuccess) {
+        *p = nullptr;
+        return false;
+    }
+    return hipMemset(*p, 0, bytes) == hipSuccess;
+}
+
+int split_count(int c_len, int splits) {  // ref runtime.mojo:211-222
+    if (splits <= 1 || c_len <= 0) return 1;
+    return std::max(1, std::min(c_len / 8, splits));
+}
+
+}  // namespace
+
+extern "C" {
+
+khq_layer* khq_layer_create(int H_q, int H_kv, int cap_tokens, const void* centroids_k,
+                            const void* centroids_v, const void* vq_centroids,
+                            const void* k_rotor, const void* v_rotor, const void* d_vec_k,
+                            const void* d_vec_v, float ts_k, float alpha_k, float ts_v,
+                            float alpha_v, float rope_base, int splits, int fused) {
+    if (H_kv <= 0 || H_q <= 0 || H_q % H_kv != 0 || H_q / H_kv > 8 || cap_tokens < kChunk ||
+        !centroids_k || !centroids_v || !vq_centroids || !k_rotor || !v_rotor || !d_vec_k ||
+        !d_vec_v)
+        return nullptr;
+    khq_layer* L = new (std::nothrow) khq_layer();
+    if (!L) return nullptr;
+    L->H_q = H_q;
+    L->H_kv = H_kv;
+    L->cap = cap_tokens;
+    L->splits = std::max(1, std::min(splits, kMaxSplits));
+    L->fused = fused ? 1 : 0;
+    L->ts_k = ts_k;
+    L->alpha_k = alpha_k;
+    L->ts_v = ts_v;
+    L->alpha_v = alpha_v;
+    L->rope_base = rope_base;
+    L->cents_k = centroids_k;
+    L->cents_v = centroids_v;
+    L->vq = vq_centroids;
+    L->rotor_k = k_rotor;
+    L->rotor_v = v_rotor;
+    L->d_k = d_vec_k;
+    L->d_v = d_vec_v;
+    const size_t ring = (size_t)kRing * H_kv * kD * sizeof(__half);
+    const size_t rows = (size_t)cap_tokens * H_kv;
+    const size_t trip = (size_t)H_q * (kD + 2) * sizeof(float);
+    const bool ok = alloc_zero(&L->ring_k, ring) && alloc_zero(&L->ring_v, ring) &&
+                    alloc_zero(&L->ring_u, ring) && alloc_zero(&L->kmask, rows * 64) &&
+                    alloc_zero(&L->kpay, rows * 40) && alloc_zero(&L->vpay, rows * 104) &&
+                    alloc_zero(&L->vsm, rows * 4) && alloc_zero(&L->knorm, rows * 2) &&
+                    alloc_zero(&L->krn, rows * 2) && alloc_zero(&L->vnorm, rows * 2) &&
+                    alloc_zero(&L->vrn, rows * 2) && alloc_zero(&L->ac, trip) &&
+                    alloc_zero(&L->aw, trip) && alloc_zero(&L->ap, trip * L->splits);
+    if (!ok) {
+        release(L);
+        delete L;
+        return nullptr;
+    }
+    return L;
+}
+
+void khq_layer_destroy(khq_layer* L) {
+    if (!L) return;
+    (void)hipDeviceSynchronize();
+    release(L);
+    delete L;
+}
+
+int khq_layer_reset(khq_layer* L) {
+    if (!L) return -100;
+    L->boundary = 0;
+    L->write_pos = 0;
+    L->n_events = 0;
+    return 0;
+}
+
+int khq_layer_state(const khq_layer* L, int* boundary, int* write_pos, int* n_events) {
+    if (!L) return -100;
+    if (boundary) *boundary = L->boundary;
+    if (write_pos) *write_pos = L->write_pos;
+    if (n_events) *n_events = L->n_events;
+    return 0;
+}
+
+int khq_layer_payload(const khq_layer* L, void** ptrs) {
+    if (!L || !ptrs) return -100;
+    void* p[] = {L->kmask, L->kpay, L->knorm, L->krn, L->vpay, L->vnorm, L->vrn, L->vsm,
+                 L->ring_k, L->ring_v, L->ring_u};
+    for (int i = 0; i < 11; i++) ptrs[i] = p[i];
+    return 0;
+}
+
+int khq_layer_capture_unroped(khq_layer* L, const void* k_unroped, hipStream_t stream) {
+    if (!L || !k_unroped) return -100;
+    const int slot = L->write_pos % kRing;
+    return launch_khq_ring_write_fp16(nullptr, nullptr, L->ring_u, nullptr, nullptr, k_unroped,
+                                      slot, L->H_kv * kD, stream);
+}
+
+int khq_layer_step(khq_layer* L, const void* q_gate, const void* k_roped, const void* v,
+                   const void* k_unroped, void* out, float scale, hipStream_t stream) {
+    if (!L || !q_gate || !k_roped || !v || !out) return -100;
+    const int kv = L->H_kv * kD;
+    const int slot = L->write_pos % kRing;
+    int rc = launch_khq_ring_write_fp16(L->ring_k, L->ring_v, k_unroped ? L->ring_u : nullptr,
+                                        k_roped, v, k_unroped, slot, kv, stream);
+    if (rc) return rc;
+    L->write_pos += 1;
+    if (L->write_pos - L->boundary >= kWatermark && L->boundary + kChunk <= L->cap) {
+        // compression event: ring slots [boundary % 256, + 128) -> payload rows
+        const int s0 = L->boundary % kRing;
+        const size_t r0 = (size_t)L->boundary * L->H_kv;
+        const int n = kChunk * L->H_kv;
+        rc = launch_khq_compress_fp16(L->ring_u + (size_t)s0 * kv, L->d_k, L->rotor_k, L->cents_k,
+                                      L->cents_k, L->kmask + r0 * 16, L->knorm + r0, L->krn + r0,
+                                      L->kpay + r0 * 40, L->vsm + r0 * 4, n, kD, L->ts_k,
+                                      L->alpha_k, 0, stream);
+        if (rc) return rc;
+        rc = launch_khq_compress_fp16(L->ring_v + (size_t)s0 * kv, L->d_v, L->rotor_v, L->cents_v,
+                                      L->vq, L->kmask + r0 * 16, L->vnorm + r0, L->vrn + r0,
+                                      L->vpay + r0 * 104, L->vsm + r0 * 4, n, kD, L->ts_v,
+                                      L->alpha_v, 1, stream);
+        if (rc) return rc;
+        L->boundary += kChunk;
+        L->n_events += 1;
+    }
+    const int c_len = L->boundary;
+    const int win_len = L->write_pos - c_len;
+    if (c_len <= 0 && win_len <= 0) return 0;
+    // The reference reads overwritten ring slots once cap is reached
+    // (README:259); refuse instead.
+    if (win_len > kRing) return -102;
+    const int win_start = c_len % kRing;
+    if (L->fused) {
+        rc = khq_attn_step_fp16(q_gate, L->kpay, L->vpay, L->vsm, L->kmask, L->knorm, L->krn,
+                                L->vnorm, L->vrn, L->cents_k, L->cents_v, L->vq, L->rotor_k,
+                                L->rotor_v, L->d_k, L->d_v, L->ring_k, L->ring_v, out, L->H_q,
+                                L->H_kv, c_len, win_start, win_len, kRing, scale, L->alpha_k,
+                                L->alpha_v, L->rope_base, stream);
+        return rc ? rc : 1;
+    }
+    const int has_c = c_len > 0, has_w = win_len > 0;
+    if (has_c) {
+        const int n_sp = split_count(c_len, L->splits);
+        rc = launch_khq_attn_fp16(q_gate, L->kpay, L->vpay, L->vsm, L->kmask, L->knorm, L->krn,
+                                  L->vnorm, L->vrn, L->cents_k, L->cents_v, L->vq, L->rotor_k,
+                                  L->rotor_v, L->d_k, L->d_v, L->ac, n_sp > 1 ? L->ap : nullptr,
+                                  L->H_q, L->H_q, 1, c_len, 0, L->H_q / L->H_kv, scale,
+                                  L->alpha_k, L->alpha_v, L->rope_base, 0, n_sp, stream);
+        if (rc) return rc;
+    }
+    if (has_w) {
+        rc = launch_khq_window_attn_fp16(q_gate, L->ring_k, L->ring_v, L->aw, win_start, win_len,
+                                         kRing, L->H_q, L->H_kv, kD, scale, stream);
+        if (rc) return rc;
+    }
+    // has_c = 0: the window triple stands in for the compressed one
+    // (ref ops.mojo:1255-1279)
+    rc = launch_khq_merge_gate_fp16(has_c ? L->ac : L->aw, L->aw, q_gate, out, L->H_q, kD,
+                                    has_c && has_w, stream);
+    return rc ? rc : 1;
+}
+
+}  // extern "C"

@@ -35,7 +35,17 @@ SIGNATURES = {
     "khq_attn_parts": [I],
     "khq_select_kernel": [I],
     "khq_workspace_reserve": [ctypes.c_size_t],
+    # per-layer runtime
+    "khq_layer_create": [I, I, I] + [P] * 7 + [F, F, F, F, F, I, I],
+    "khq_layer_destroy": [P],
+    "khq_layer_reset": [P],
+    "khq_layer_state": [P, P, P, P],
+    "khq_layer_payload": [P, P],
+    "khq_layer_capture_unroped": [P, P, P],
+    "khq_layer_step": [P] * 6 + [F, P],
 }
+# return types other than int
+RESTYPES = {"khq_layer_create": ctypes.c_void_p, "khq_layer_destroy": None}
 
 
 class KhqError(RuntimeError):
@@ -57,7 +67,7 @@ def lib() -> ctypes.CDLL:
         for name, argtypes in SIGNATURES.items():
             fn = getattr(_lib, name)
             fn.argtypes = argtypes
-            fn.restype = ctypes.c_int
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
         _lib.khq_version.restype = ctypes.c_char_p
     return _lib
 

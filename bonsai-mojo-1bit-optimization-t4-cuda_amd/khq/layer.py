@@ -8,6 +8,7 @@ and libkhq_hip.so in place of libbonsai_qmv_sm75.so.
 """
 from __future__ import annotations
 
+import ctypes
 import os
 import time
 from dataclasses import dataclass, field
@@ -235,6 +236,68 @@ class KhqLayer:
         for dst, src in ((self.ring_k, ring_k), (self.ring_v, ring_v), (self.ring_u, ring_u)):
             if src is not None:
                 dst.copy_(src.reshape(dst.shape))
+
+
+class NativeKhqLayer:
+    """The same per-layer runtime driven through the C ABI (khq_layer_*): the
+    ring, payload, cadence and attention issue all live in libkhq_hip.so; this
+    class only holds the handle and the caller-owned constant tensors."""
+
+    def __init__(self, cents: C.LayerCentroids, *, H_q: int = 24, H_kv: int = 4,
+                 cap: int = 4096, device="cuda", options: KhqOptions | None = None):
+        from . import _lib
+
+        self.opt = options or KhqOptions.from_env()
+        self.cents = Centroids(cents, device)
+        self.H_q, self.H_kv, self.cap = H_q, H_kv, cap
+        c = self.cents
+        self._lib = _lib.lib()
+        self.handle = self._lib.khq_layer_create(
+            H_q, H_kv, cap, c.cents_k.data_ptr(), c.cents_v.data_ptr(), c.vq.data_ptr(),
+            c.rotor_k.data_ptr(), c.rotor_v.data_ptr(), c.d_k.data_ptr(), c.d_v.data_ptr(),
+            c.ts_k, c.alpha_k, c.ts_v, c.alpha_v, ROPE_BASE, self.opt.splits,
+            1 if self.opt.fused else 0)
+        if not self.handle:
+            raise RuntimeError("khq_layer_create failed")
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h:
+            self._lib.khq_layer_destroy(h)
+            self.handle = None
+
+    def state(self) -> tuple[int, int, int]:
+        b, w, n = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        self._lib.khq_layer_state(self.handle, ctypes.byref(b), ctypes.byref(w), ctypes.byref(n))
+        return b.value, w.value, n.value
+
+    def reset(self) -> None:
+        self._lib.khq_layer_reset(self.handle)
+
+    def payload_ptrs(self) -> list[int]:
+        arr = (ctypes.c_void_p * 11)()
+        self._lib.khq_layer_payload(self.handle, arr)
+        return [int(p or 0) for p in arr]
+
+    def capture_unroped(self, k: torch.Tensor) -> None:
+        from ._lib import KhqError, stream_handle
+
+        rc = self._lib.khq_layer_capture_unroped(self.handle, k.data_ptr(), stream_handle())
+        if rc:
+            raise KhqError("khq_layer_capture_unroped", rc)
+
+    def step(self, q_gate, k_roped, v, out, scale: float, k_unroped=None) -> bool:
+        from ._lib import KhqError, stream_handle
+
+        rc = self._lib.khq_layer_step(self.handle, q_gate.data_ptr(), k_roped.data_ptr(),
+                                      v.data_ptr(),
+                                      k_unroped.data_ptr() if k_unroped is not None else None,
+                                      out.data_ptr(), scale, stream_handle())
+        if rc == -102:
+            raise RuntimeError(f"raw window exceeds the {RING}-slot ring (cap {self.cap} reached)")
+        if rc < 0 or rc > 1:
+            raise KhqError("khq_layer_step", rc)
+        return rc == 1
 
 
 class KhqRuntime:

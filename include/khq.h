@@ -155,6 +155,40 @@ int khq_workspace_reserve(size_t bytes);
 /* Library version string. */
 const char* khq_version(void);
 
+/* ---- per-layer runtime (replaces KhqLayer / khq_init_layer /
+ * khq_capture_unroped / khq_step, ref:src/khq/runtime.mojo:77-152,395-613;
+ * the reference keeps this state in Mojo host structs) ----
+ * A layer owns its 256-slot rings (roped K, V, unroped K), the packed payload
+ * for cap_tokens tokens and its scratch; the constant tensors (centroids,
+ * VQ codebook, rotors, d vectors, fp16 device buffers in the KHQK layouts)
+ * stay owned by the caller and must outlive the layer.  splits follows
+ * BONSAI_KHQ_SPLITS (clamped to [1, 64]) and only matters when fused = 0
+ * (the reference's attn + window + merge launch sequence); fused = 1 issues
+ * khq_attn_step_fp16.  Returns NULL on bad arguments or allocation failure. */
+typedef struct khq_layer khq_layer;
+khq_layer* khq_layer_create(int H_q, int H_kv, int cap_tokens, const void* centroids_k,
+                            const void* centroids_v, const void* vq_centroids,
+                            const void* k_rotor, const void* v_rotor, const void* d_vec_k,
+                            const void* d_vec_v, float ts_k, float alpha_k, float ts_v,
+                            float alpha_v, float rope_base, int splits, int fused);
+void khq_layer_destroy(khq_layer* layer);
+/* boundary = write_pos = 0 (the reference has none, README:260). */
+int khq_layer_reset(khq_layer* layer);
+int khq_layer_state(const khq_layer* layer, int* boundary, int* write_pos, int* n_events);
+/* Device pointers of kmask, kpay, knorm, krn, vpay, vnorm, vrn, vsm, ring_k,
+ * ring_v, ring_u (11 entries), for inspection. */
+int khq_layer_payload(const khq_layer* layer, void** ptrs);
+/* Post-norm, pre-RoPE K [H_kv][256] of the token about to be stepped into
+ * ring_u[write_pos % 256] (ref runtime.mojo:432-451). */
+int khq_layer_capture_unroped(khq_layer* layer, const void* k_unroped, hipStream_t stream);
+/* One decode step (ref runtime.mojo:454-613): ring write (k_unroped may be
+ * NULL when captured before), compression event at the watermark, then the
+ * two-region attention into out f16 [H_q][256].  Returns 1 when out was
+ * written, 0 when neither region exists, -100 on bad arguments, -102 when the
+ * raw window would exceed the ring (capacity reached), else an error code. */
+int khq_layer_step(khq_layer* layer, const void* q_gate, const void* k_roped, const void* v,
+                   const void* k_unroped, void* out, float scale, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

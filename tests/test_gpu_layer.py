@@ -79,6 +79,16 @@ class Sim:
         return out, ev
 
 
+def _hip_d2d(dst: int, src: int, nbytes: int) -> int:
+    """hipMemcpy device to device (kind 3) on raw pointers."""
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipMemcpy.restype = ctypes.c_int
+    return hip.hipMemcpy(dst, src, nbytes, 3)
+
+
 def _tokens(n, seed):
     rng = np.random.default_rng(seed)
     k = rng.standard_normal((n, H_KV, D)).astype(np.float16)
@@ -132,6 +142,43 @@ def test_layer_matches_simulation(device, fused):
             if 0 <= lo and lo + 128 <= N_STEPS:
                 wrong = np.mean(np.abs(got - true_norm[lo:lo + 128]) / true_norm[lo:lo + 128])
                 assert wrong > 5 * rel
+
+
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "reference-sequence"])
+def test_native_layer_matches_python_layer(device, fused):
+    """The C-ABI layer runtime (khq_layer_*) against the Python one: same
+    kernels, so identical outputs, cadence and payload bytes, step by step."""
+    lc, _ = layer_consts(layer_id=5)
+    opt = KL.KhqOptions(splits=8, fused=fused)
+    py = KL.KhqLayer(lc, H_q=H_Q, H_kv=H_KV, cap=1024, device=device, options=opt)
+    na = KL.NativeKhqLayer(lc, H_q=H_Q, H_kv=H_KV, cap=1024, device=device, options=opt)
+    k, kr, v, q = _tokens(400, seed=11)
+    o1 = torch.empty((H_Q, D), device=device, dtype=torch.float16)
+    o2 = torch.empty_like(o1)
+    for t in range(400):
+        qt, kt, vt = (torch.from_numpy(a[t]).to(device) for a in (q, kr, v))
+        ku = torch.from_numpy(k[t]).to(device)
+        if t % 2:
+            assert py.step(qt, kt, vt, o1, SCALE, k_unroped=ku)
+            assert na.step(qt, kt, vt, o2, SCALE, k_unroped=ku)
+        else:  # the reference's two-call order
+            py.capture_unroped(ku)
+            na.capture_unroped(ku)
+            assert py.step(qt, kt, vt, o1, SCALE)
+            assert na.step(qt, kt, vt, o2, SCALE)
+        if t % 17 == 0 or t in (255, 256, 383, 384, 399):
+            assert torch.equal(o1, o2), t
+    assert na.state() == (py.boundary, py.write_pos, len(py.events)) == (256, 400, 2)
+    ptrs = na.payload_ptrs()
+    n = 256 * H_KV
+    for i, name in enumerate(("kmask", "kpay", "knorm", "krn", "vpay", "vnorm", "vrn", "vsm")):
+        ref = getattr(py.pay, name)[:n]
+        got = torch.empty_like(ref)
+        torch.cuda.synchronize()
+        assert _hip_d2d(got.data_ptr(), ptrs[i], got.numel() * got.element_size()) == 0
+        assert torch.equal(got, ref), name
+    na.reset()
+    assert na.state() == (0, 0, 0)
 
 
 def test_capture_unroped_then_step(device):
