@@ -266,7 +266,7 @@ def cpu_baseline(L, c_len, win_len, win_start, scale, budget_s):
         if el >= budget_s or reps >= 50:
             break
     return {"value": round(el / reps * 1e6, 1), "unit": "us/layer-step", "cores": threads,
-            "kind": "port",
+            "host_nproc": os.cpu_count(), "kind": "port",
             "sample": f"{reps} layer-step(s) of layer 0 at the same shape "
                       f"({c_len} compressed + {win_len} raw, splits {n_sp}), OpenMP over "
                       f"(query head x split)"}
