@@ -866,15 +866,16 @@ __device__ void window_block(const AttnArgs& a, Smem& S, int part_idx) {
     }
 }
 
-__global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_per_chunk,
-                                                          int n_chunks) {
+// One block of work: compressed chunk `chunk` of the sequence described by a
+// (chunk == n_chunks: its raw window).
+__device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles_per_chunk,
+                                         int n_chunks) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem& S = *reinterpret_cast<Smem*>(smem_raw);
     const int tid = threadIdx.x;
     const int wv = tid >> 6;
     const int h = wv & 3;
     const int lane = tid & 63;
-    const int chunk = blockIdx.x;
     if (chunk >= n_chunks) {  // the block after the compressed chunks
         window_block(a, S, a.part_offset + n_chunks);
         return;
@@ -990,6 +991,21 @@ __global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_
 #endif
 }
 
+__global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_per_chunk,
+                                                          int n_chunks) {
+    ws_block(a, blockIdx.x, tiles_per_chunk, n_chunks);
+}
+
+// Batched form: block b works on sequence map[b].x, chunk map[b].y (the
+// sequence's n_parts compressed chunks, then its window block).
+__global__ __launch_bounds__(NTHR, 1) void attn_ws_batched_kernel(const AttnArgs* __restrict__ args,
+                                                                  const int2* __restrict__ map,
+                                                                  int tiles_per_chunk) {
+    const int2 m = map[blockIdx.x];
+    const AttnArgs a = args[m.x];
+    ws_block(a, m.y, tiles_per_chunk, a.n_parts);
+}
+
 }  // namespace ws
 
 size_t attn_ws_smem_bytes() { return sizeof(ws::Smem); }
@@ -1006,6 +1022,21 @@ hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks, 
     const int blocks = n_chunks + (a.win_len > 0 ? 1 : 0);
     hipLaunchKernelGGL(ws::attn_ws_kernel, dim3(blocks), dim3(ws::NTHR), smem, st, a,
                        tiles_per_chunk, n_chunks);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_ws_batched(const AttnArgs* args, const int2* map, int n_blocks,
+                                  int tiles_per_chunk, hipStream_t st) {
+    static bool configured = false;
+    const size_t smem = sizeof(ws::Smem);
+    if (!configured) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ws::attn_ws_batched_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        if (e != hipSuccess) return e;
+        configured = true;
+    }
+    hipLaunchKernelGGL(ws::attn_ws_batched_kernel, dim3(n_blocks), dim3(ws::NTHR), smem, st,
+                       args, map, tiles_per_chunk);
     return hipGetLastError();
 }
 

@@ -7,6 +7,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <vector>
 
 #include "khq.h"
 #include "khq_internal.h"
@@ -413,6 +414,142 @@ int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_
     }
     return rc_of(khq::launch_combine_gate(ws, static_cast<const __half*>(q_gate),
                                           static_cast<__half*>(out), H_q, np, 1e-8f, stream));
+}
+
+int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centroids_k,
+                               const void* centroids_v, const void* vq_centroids,
+                               const void* k_rotor, const void* v_rotor, const void* d_vec_k,
+                               const void* d_vec_v, int H_q, int H_kv, float scale,
+                               float alpha_k, float alpha_v, float rope_base, hipStream_t stream) {
+    if (!seqs || n_seq <= 0 || n_seq > 4096) return -100;
+    if (H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || H_q / H_kv > 8) return -100;
+    for (int i = 0; i < n_seq; i++) {
+        const khq_seq& q = seqs[i];
+        if (q.c_len < 0 || q.win_len < 0 || (q.c_len == 0 && q.win_len == 0)) return -100;
+        if (q.win_len > 0 && (q.ring_cap <= 0 || q.win_len > q.ring_cap || q.win_start < 0))
+            return -100;
+    }
+    const int n_rep = H_q / H_kv;
+    bool batched = g_kernel_choice == 0 && use_mfma(n_rep, H_kv, 1);
+    for (int i = 0; i < n_seq && batched; i++) batched = seqs[i].win_len <= 256;
+    if (!batched) {  // one fused step per sequence
+        for (int i = 0; i < n_seq; i++) {
+            const khq_seq& q = seqs[i];
+            const int rc = khq_attn_step_fp16(
+                q.q_gate, q.k_payload, q.v_payload, q.v_shared_meta, q.k_mask, q.k_norms,
+                q.k_r_norms, q.v_norms, q.v_r_norms, centroids_k, centroids_v, vq_centroids,
+                k_rotor, v_rotor, d_vec_k, d_vec_v, q.ring_k, q.ring_v, q.out, H_q, H_kv, q.c_len,
+                q.win_start, q.win_len, q.ring_cap, scale, alpha_k, alpha_v, rope_base, stream);
+            if (rc) return rc;
+        }
+        return 0;
+    }
+    // Chunk length: the smallest tile count per chunk whose blocks (compressed
+    // chunks plus one window block per sequence with a window) fit the CUs.
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess)
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    std::vector<int> tiles(n_seq);
+    long total_tiles = 0;
+    int n_win = 0, max_tiles = 1;
+    for (int i = 0; i < n_seq; i++) {
+        tiles[i] = (seqs[i].c_len + 15) / 16;
+        total_tiles += tiles[i];
+        max_tiles = std::max(max_tiles, tiles[i]);
+        n_win += seqs[i].win_len > 0 ? 1 : 0;
+    }
+    const int budget = std::max(1, cus - n_win);
+    int per = std::max(1, (int)((total_tiles + budget - 1) / budget));
+    auto blocks_for = [&](int p) {
+        long b = n_win;
+        for (int i = 0; i < n_seq; i++) b += (tiles[i] + p - 1) / p;
+        return b;
+    };
+    while (per < max_tiles && blocks_for(per) > cus) per++;
+    // partial layout: sequence i owns H_q x np_i triples from float offset off_i
+    static thread_local std::vector<khq::AttnArgs> h_args;
+    static thread_local std::vector<khq::FinishArgs> h_fin;
+    static thread_local std::vector<int2> h_map;
+    h_args.assign(n_seq, khq::AttnArgs{});
+    h_fin.assign(n_seq, khq::FinishArgs{});
+    h_map.clear();
+    size_t part_floats = 0;
+    std::vector<size_t> off(n_seq);
+    std::vector<int> chunks(n_seq), np(n_seq);
+    for (int i = 0; i < n_seq; i++) {
+        chunks[i] = (tiles[i] + per - 1) / per;
+        np[i] = chunks[i] + (seqs[i].win_len > 0 ? 1 : 0);
+        if (np[i] > 1024) return -100;  // finishing kernel's part limit
+        off[i] = part_floats;
+        part_floats += (size_t)H_q * np[i] * 258;
+    }
+    const size_t meta_off = (part_floats * sizeof(float) + 255) & ~(size_t)255;
+    const size_t n_blocks = blocks_for(per);
+    const size_t meta_bytes = n_seq * (sizeof(khq::AttnArgs) + sizeof(khq::FinishArgs)) +
+                              n_blocks * sizeof(int2) + 512;
+    float* ws = nullptr;
+    hipError_t e = workspace(meta_off + meta_bytes, &ws);
+    if (e != hipSuccess) return rc_of(e);
+    char* meta = reinterpret_cast<char*>(ws) + meta_off;
+    khq::AttnArgs* d_args = reinterpret_cast<khq::AttnArgs*>(meta);
+    khq::FinishArgs* d_fin = reinterpret_cast<khq::FinishArgs*>(
+        (reinterpret_cast<uintptr_t>(d_args + n_seq) + 15) & ~(uintptr_t)15);
+    int2* d_map = reinterpret_cast<int2*>(
+        (reinterpret_cast<uintptr_t>(d_fin + n_seq) + 15) & ~(uintptr_t)15);
+    for (int i = 0; i < n_seq; i++) {
+        const khq_seq& q = seqs[i];
+        khq::AttnArgs a = attn_args(q.q_gate, q.k_payload, q.v_payload, q.v_shared_meta, q.k_mask,
+                                    q.k_norms, q.k_r_norms, q.v_norms, q.v_r_norms, centroids_k,
+                                    centroids_v, vq_centroids, k_rotor, v_rotor, d_vec_k, d_vec_v);
+        const int ring = q.ring_cap > 0 ? q.ring_cap : 1;
+        a.part = ws + off[i];
+        a.c_len = q.c_len;
+        a.h_kv = H_kv;
+        a.L_q = 1;
+        a.start_pos = 0;
+        a.n_parts = chunks[i];
+        a.part_offset = 0;
+        a.part_stride = np[i];
+        a.sc = scale;
+        a.a_k = alpha_k;
+        a.a_v = alpha_v;
+        a.rope_base = rope_base;
+        a.ring_k = static_cast<const __half*>(q.ring_k);
+        a.ring_v = static_cast<const __half*>(q.ring_v);
+        a.win_start = q.win_start % ring;
+        a.win_len = q.win_len;
+        a.ring_cap = ring;
+        h_args[i] = a;
+        for (int c = 0; c < np[i]; c++) h_map.push_back(int2{i, c});
+        khq::FinishArgs f{};
+        f.part = ws + off[i];
+        f.n_parts = np[i];
+        f.part_stride = np[i];
+        f.q = static_cast<const __half*>(q.q_gate);
+        f.ring_k = a.ring_k;
+        f.ring_v = a.ring_v;
+        f.ring_cap = ring;
+        f.win_start = a.win_start;
+        f.win_len = 0;  // computed by the window blocks
+        f.h_kv = H_kv;
+        f.n_rep = n_rep;
+        f.sc = scale;
+        f.eps = 1e-8f;
+        f.out = static_cast<__half*>(q.out);
+        h_fin[i] = f;
+    }
+    e = hipMemcpyAsync(d_args, h_args.data(), n_seq * sizeof(khq::AttnArgs),
+                       hipMemcpyHostToDevice, stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d_fin, h_fin.data(), n_seq * sizeof(khq::FinishArgs),
+                           hipMemcpyHostToDevice, stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d_map, h_map.data(), h_map.size() * sizeof(int2),
+                           hipMemcpyHostToDevice, stream);
+    if (e != hipSuccess) return rc_of(e);
+    e = khq::launch_attn_ws_batched(d_args, d_map, (int)h_map.size(), per, stream);
+    if (e != hipSuccess) return rc_of(e);
+    return rc_of(khq::launch_step_finish_batched(d_fin, n_seq, H_q, stream));
 }
 
 }  // extern "C"

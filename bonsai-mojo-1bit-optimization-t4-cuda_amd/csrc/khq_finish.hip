@@ -55,14 +55,13 @@ __device__ __forceinline__ void block_sum2(float& x, float& y, float* s_red) {
     y = (s_red[4] + s_red[5]) + (s_red[6] + s_red[7]);
 }
 
-__global__ __launch_bounds__(256) void step_finish_kernel(FinishArgs a) {
+__device__ __forceinline__ void finish_block(const FinishArgs& a, int hq, int slice) {
     __shared__ float s_p[MAX_WIN];      // window weights
     __shared__ float s_w[MAX_PARTS];    // compressed part weights
     __shared__ float s_red[8];
     __shared__ float s_acc[2][8][DS];
     const int t = threadIdx.x;
-    const int hq = blockIdx.x;
-    const int d0 = blockIdx.y * DS;
+    const int d0 = slice * DS;
     const int hk = hq / a.n_rep;
     const float* base = a.part + (size_t)hq * a.part_stride * 258;  // < 2^31 floats per head
     const int d = t & (DS - 1), grp = t >> 5;
@@ -188,7 +187,25 @@ __global__ __launch_bounds__(256) void step_finish_kernel(FinishArgs a) {
     }
 }
 
+__global__ __launch_bounds__(256) void step_finish_kernel(FinishArgs a) {
+    finish_block(a, blockIdx.x, blockIdx.y);
+}
+
+// Batched form: blockIdx.x = sequence * H_q + query head.
+__global__ __launch_bounds__(256) void step_finish_batched_kernel(const FinishArgs* __restrict__ args,
+                                                                  int H_q) {
+    const FinishArgs a = args[blockIdx.x / H_q];
+    finish_block(a, blockIdx.x % H_q, blockIdx.y);
+}
+
 }  // namespace fin
+
+hipError_t launch_step_finish_batched(const FinishArgs* args, int n_seq, int H_q,
+                                      hipStream_t st) {
+    hipLaunchKernelGGL(fin::step_finish_batched_kernel, dim3(n_seq * H_q, 256 / fin::DS),
+                       dim3(256), 0, st, args, H_q);
+    return hipGetLastError();
+}
 
 hipError_t launch_step_finish(const FinishArgs& a, int H_q, hipStream_t st) {
     if (a.n_parts > fin::MAX_PARTS || a.win_len > fin::MAX_WIN || a.n_rep <= 0)

@@ -61,6 +61,10 @@ struct FinishArgs {
     __half* out;  // [H_q][256]
 };
 hipError_t launch_step_finish(const FinishArgs& a, int H_q, hipStream_t st);
+// n_seq sequences, args a device array (window computed upstream or not, per
+// sequence as in FinishArgs; parts <= 1024, win_len <= 256 each).
+hipError_t launch_step_finish_batched(const FinishArgs* args, int n_seq, int H_q,
+                                      hipStream_t st);
 
 hipError_t launch_compress(const __half* x, const __half* d_vec, const __half* rotor,
                            const __half* cents, const __half* vq, uint32_t* out_mask,
@@ -91,5 +95,10 @@ hipError_t launch_attn_mfma(const AttnArgs& a, int tiles_per_chunk, int n_chunks
 size_t attn_ws_smem_bytes();
 hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks,
                           hipStream_t st);
+// Batched: args[seq] (device) with n_parts = that sequence's chunk count and
+// its window fields; map[b] = (seq, chunk) for each of n_blocks blocks (chunk
+// == n_parts: the sequence's window block).
+hipError_t launch_attn_ws_batched(const AttnArgs* args, const int2* map, int n_blocks,
+                                  int tiles_per_chunk, hipStream_t st);
 
 }  // namespace khq

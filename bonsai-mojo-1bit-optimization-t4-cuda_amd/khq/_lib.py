@@ -31,6 +31,7 @@ SIGNATURES = {
     "launch_khq_partial_rope_fp16": [P, I, I, I, I, F, I, P],
     "launch_khq_gqa_attn_fp16": [P] * 4 + [I, I, I, I, F, P],
     "khq_attn_step_fp16": [P] * 19 + [I, I, I, I, I, I, F, F, F, F, P],
+    "khq_attn_step_batched_fp16": [P, I] + [P] * 7 + [I, I, F, F, F, F, P],
     "khq_attn_partials_fp16": [P] * 16 + [I, I, I, F, F, F, F, P],
     "khq_attn_parts": [I],
     "khq_select_kernel": [I],
@@ -46,6 +47,15 @@ SIGNATURES = {
 }
 # return types other than int
 RESTYPES = {"khq_layer_create": ctypes.c_void_p, "khq_layer_destroy": None}
+
+
+class KhqSeq(ctypes.Structure):
+    """struct khq_seq of include/khq.h: one sequence of a batched step."""
+
+    _fields_ = [(n, P) for n in ("q_gate", "k_payload", "v_payload", "v_shared_meta", "k_mask",
+                                 "k_norms", "k_r_norms", "v_norms", "v_r_norms", "ring_k",
+                                 "ring_v", "out")] + [
+        (n, I) for n in ("c_len", "win_start", "win_len", "ring_cap")]
 
 
 class KhqError(RuntimeError):

@@ -7,6 +7,8 @@ meaning follow the reference's FFI wrappers (ref:src/ops.mojo:1101-1279).
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -182,6 +184,31 @@ def attn_step(q_gate, pay: Payload, cents: Centroids, ring_k, ring_v, out, *, H_
                 ptr(cents.rotor_v), ptr(cents.d_k), ptr(cents.d_v), ptr(ring_k), ptr(ring_v),
                 ptr(out), H_q, H_kv, c_len, win_start, win_len, ring_cap, scale,
                 cents.alpha_k, cents.alpha_v, rope_base, stream_handle(stream), check=check)
+
+
+def attn_step_batched(seqs, cents: Centroids, *, H_q: int, H_kv: int, scale: float,
+                      rope_base: float = 1e7, check: bool = True, stream=None) -> int:
+    """khq_attn_step_batched_fp16 over a list of per-sequence dicts with keys
+    q_gate, pay (Payload), ring_k, ring_v, out, c_len, win_start, win_len,
+    ring_cap: every sequence's attention step in one library call."""
+    arr = (_lib.KhqSeq * len(seqs))()
+    for i, s in enumerate(seqs):
+        pay = s["pay"]
+        _need(s["q_gate"], torch.float16, H_q * 2 * D, "q_gate")
+        _need(s["out"], torch.float16, H_q * D, "out")
+        if s["c_len"] * H_kv > pay.rows:
+            raise ValueError("c_len exceeds payload rows")
+        if s["win_len"] > 0:
+            _need(s["ring_k"], torch.float16, s["ring_cap"] * H_kv * D, "ring_k")
+            _need(s["ring_v"], torch.float16, s["ring_cap"] * H_kv * D, "ring_v")
+        arr[i] = _lib.KhqSeq(ptr(s["q_gate"]), ptr(pay.kpay), ptr(pay.vpay), ptr(pay.vsm),
+                             ptr(pay.kmask), ptr(pay.knorm), ptr(pay.krn), ptr(pay.vnorm),
+                             ptr(pay.vrn), ptr(s["ring_k"]), ptr(s["ring_v"]), ptr(s["out"]),
+                             s["c_len"], s["win_start"], s["win_len"], s["ring_cap"])
+    return call("khq_attn_step_batched_fp16", ctypes.cast(arr, ctypes.c_void_p), len(seqs), ptr(cents.cents_k),
+                ptr(cents.cents_v), ptr(cents.vq), ptr(cents.rotor_k), ptr(cents.rotor_v),
+                ptr(cents.d_k), ptr(cents.d_v), H_q, H_kv, scale, cents.alpha_k, cents.alpha_v,
+                rope_base, stream_handle(stream), check=check)
 
 
 def attn_partials(q_gate, pay: Payload, cents: Centroids, *, H_q: int, H_kv: int, c_len: int,

@@ -125,6 +125,34 @@ int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_
                        int win_start, int win_len, int ring_cap, float scale,
                        float alpha_k, float alpha_v, float rope_base, hipStream_t stream);
 
+/* ---- batched decode (no reference counterpart: the reference decodes one
+ * sequence at a time through khq_step, ref:src/khq/runtime.mojo:454-613) ----
+ * n_seq independent sequences of one layer (shared constant tensors), one
+ * query token each, each with its own payload, ring, c_len and window, as in
+ * khq_attn_step_fp16.  seqs is a host array.  With the 24/4/256 shape one
+ * launch covers every sequence's compressed chunks and windows and a second
+ * one merges and gates; other shapes run one fused step per sequence. */
+typedef struct khq_seq {
+    const void* q_gate;  /* f16 [H_q][512] */
+    const void* k_payload;
+    const void* v_payload;
+    const void* v_shared_meta;
+    const void* k_mask;
+    const void* k_norms;
+    const void* k_r_norms;
+    const void* v_norms;
+    const void* v_r_norms;
+    const void* ring_k;  /* f16 [ring_cap][H_kv][256] */
+    const void* ring_v;
+    void* out;           /* f16 [H_q][256] */
+    int c_len, win_start, win_len, ring_cap;
+} khq_seq;
+int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centroids_k,
+                               const void* centroids_v, const void* vq_centroids,
+                               const void* k_rotor, const void* v_rotor, const void* d_vec_k,
+                               const void* d_vec_v, int H_q, int H_kv, float scale,
+                               float alpha_k, float alpha_v, float rope_base, hipStream_t stream);
+
 /* Profiling entry (no reference counterpart): launches only the
  * compressed-region kernel of khq_attn_step_fp16 (partials into the library
  * workspace, nothing merged), so its duration can be timed on its own. */

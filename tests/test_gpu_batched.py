@@ -1,0 +1,133 @@
+"""GPU parity of the batched decode step (khq_attn_step_batched_fp16): ragged
+sequences in one call, each against the oracle (small cases) or against the
+library's own single-sequence step (the 32-sequence ragged configuration,
+L ~ U[1024, 16384]).
+
+Bar: attention outputs within max-abs 2e-3 and rel 1e-3 of the oracle; the
+single-step comparison uses the same tolerance (the two calls partition the
+tokens differently, so their fp32 sums round differently).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from khq import ops, synth
+from khqdata import (D, H_KV, H_Q, SCALE, layer_consts, oracle_attn, oracle_window,
+                     random_rows_np)
+from test_gpu_parity import close, payload_from_rows, t
+
+pytestmark = pytest.mark.gpu
+
+
+def _seq_state(rng, lc, h, c_len, win_start, win_len, seed):
+    rows = random_rows_np(max(c_len, 1) * H_KV, seed=seed)
+    ring_k = rng.standard_normal((256, H_KV, D)).astype(np.float16)
+    ring_v = rng.standard_normal((256, H_KV, D)).astype(np.float16)
+    q = rng.standard_normal((H_Q, 2 * D)).astype(np.float16)
+    return dict(rows=rows, h=h, lc=lc, q_gate=q, c_len=c_len, ring_k=ring_k, ring_v=ring_v,
+                win_start=win_start, win_len=win_len)
+
+
+def _oracle_out(st):
+    if st["c_len"] == 0:
+        _, ww = oracle_window(st)
+        return oracle.merge_gate(ww, ww, st["q_gate"], H_q=H_Q, has_w=False)[1]
+    _, wc, _ = oracle_attn(st)
+    if st["win_len"] == 0:
+        return oracle.merge_gate(wc, wc, st["q_gate"], H_q=H_Q, has_w=False)[1]
+    _, ww = oracle_window(st)
+    return oracle.merge_gate(wc, ww, st["q_gate"], H_q=H_Q, has_w=True)[1]
+
+
+# (c_len, win_start, win_len): window only, compressed only, wrapped window,
+# full ring, a single tile, a ragged tail, long and short sequences together.
+CASES = [(0, 0, 200), (2048, 0, 0), (384, 128, 216), (1280, 88, 256), (16, 16, 1), (37, 37, 5),
+         (5000, 136, 128), (129, 129, 130)]
+
+
+@pytest.mark.parametrize("order", ["given", "reversed"])
+def test_batched_matches_oracle(device, order):
+    lc, h = layer_consts()
+    rng = np.random.default_rng(11)
+    cases = CASES if order == "given" else CASES[::-1]
+    states = [_seq_state(rng, lc, h, c, ws, wl, seed=100 + i)
+              for i, (c, ws, wl) in enumerate(cases)]
+    cents = ops.Centroids(lc, device)
+    seqs = []
+    for st in states:
+        n_rows = st["rows"]["kmask"].shape[0]
+        seqs.append(dict(q_gate=t(st["q_gate"]), pay=payload_from_rows(st["rows"], n_rows),
+                         ring_k=t(st["ring_k"]), ring_v=t(st["ring_v"]),
+                         out=torch.zeros((H_Q, D), device=device, dtype=torch.float16),
+                         c_len=st["c_len"], win_start=st["win_start"], win_len=st["win_len"],
+                         ring_cap=256))
+    ops.attn_step_batched(seqs, cents, H_q=H_Q, H_kv=H_KV, scale=SCALE)
+    torch.cuda.synchronize()
+    for st, s in zip(states, seqs):
+        close(s["out"].cpu().numpy(), _oracle_out(st))
+
+
+def test_batched_error_codes(device):
+    lc, _ = layer_consts()
+    cents = ops.Centroids(lc, device)
+    pay = ops.Payload(64 * H_KV, device)
+    z = torch.zeros((H_Q, 2 * D), device=device, dtype=torch.float16)
+    rk = torch.zeros((256, H_KV, D), device=device, dtype=torch.float16)
+    out = torch.zeros((H_Q, D), device=device, dtype=torch.float16)
+    base = dict(q_gate=z, pay=pay, ring_k=rk, ring_v=rk, out=out, c_len=64, win_start=0,
+                win_len=10, ring_cap=256)
+    bad = [dict(base, c_len=0, win_len=0), dict(base, win_len=257), dict(base, c_len=-1)]
+    for b in bad:
+        assert ops.attn_step_batched([base, b], cents, H_q=H_Q, H_kv=H_KV, scale=SCALE,
+                                     check=False) == -100
+    assert ops.attn_step_batched([dict(base, c_len=16, win_len=0)], cents, H_q=H_Q, H_kv=5, scale=SCALE,
+                                 check=False) == -100
+
+
+def test_batched_c4_ragged_32(device):
+    """32 ragged sequences, L ~ U[1024, 16384] compressed tokens each plus a
+    raw window of L % 256 + 1 tokens, against one single-sequence step each;
+    then the oracle on the two shortest."""
+    lc, h = layer_consts()
+    rng = np.random.default_rng(44)
+    lens = rng.integers(1024, 16385, 32)
+    cents = ops.Centroids(lc, device)
+    seqs, singles = [], []
+    for i, L in enumerate(lens):
+        L = int(L)
+        rows = synth.random_rows(L * H_KV, seed=500 + i, device=device)
+        pay = ops.Payload(L * H_KV, device)
+        for k in ("kmask", "kpay", "knorm", "krn", "vpay", "vnorm", "vrn", "vsm"):
+            getattr(pay, k).copy_(rows[k])
+        wl = L % 256 + 1
+        s = dict(q_gate=synth.q_gate(H_Q, seed=900 + i, device=device), pay=pay,
+                 ring_k=torch.randn((256, H_KV, D), device=device).half(),
+                 ring_v=torch.randn((256, H_KV, D), device=device).half(),
+                 out=torch.zeros((H_Q, D), device=device, dtype=torch.float16),
+                 c_len=L, win_start=L % 256, win_len=wl, ring_cap=256)
+        seqs.append(s)
+    ops.attn_step_batched(seqs, cents, H_q=H_Q, H_kv=H_KV, scale=SCALE)
+    for s in seqs:
+        o = torch.zeros_like(s["out"])
+        ops.attn_step(s["q_gate"], s["pay"], cents, s["ring_k"], s["ring_v"], o, H_q=H_Q,
+                      H_kv=H_KV, c_len=s["c_len"], win_start=s["win_start"],
+                      win_len=s["win_len"], ring_cap=256, scale=SCALE)
+        singles.append(o)
+    torch.cuda.synchronize()
+    for s, o in zip(seqs, singles):
+        close(s["out"].float().cpu().numpy(), o.float().cpu().numpy())
+    # the batched call is deterministic
+    first = [s["out"].clone() for s in seqs]
+    ops.attn_step_batched(seqs, cents, H_q=H_Q, H_kv=H_KV, scale=SCALE)
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, s["out"]) for a, s in zip(first, seqs))
+    for i in np.argsort(lens)[:2]:
+        s = seqs[int(i)]
+        rows = {k: getattr(s["pay"], k).cpu().numpy() for k in
+                ("kmask", "kpay", "knorm", "krn", "vpay", "vnorm", "vrn", "vsm")}
+        rows["kmask"] = rows["kmask"].view(np.uint32)
+        st = dict(rows=rows, h=h, lc=lc, q_gate=s["q_gate"].cpu().numpy(), c_len=s["c_len"],
+                  ring_k=s["ring_k"].cpu().numpy(), ring_v=s["ring_v"].cpu().numpy(),
+                  win_start=s["win_start"], win_len=s["win_len"])
+        close(s["out"].cpu().numpy(), _oracle_out(st))
