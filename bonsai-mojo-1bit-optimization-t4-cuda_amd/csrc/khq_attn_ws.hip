@@ -21,8 +21,14 @@
 //               and the dot with q (key split hi + lo), all on MFMA.
 // K contraction order: K-step st, lane group lg, element e <-> dim
 // 64 lg + 8 st + e, so lane (token li, lg) owns dims 64 lg .. 64 lg + 63 of
-// its token in every K-step: it walks the outliers of exactly those dims and
-// keeps their values in a lane-private LDS strip.
+// its token in every K-step.  Outliers are expanded per K-step without a
+// walk: the 8-dim outlier pattern p indexes byte-permute tables that place
+// the nibbles and signs of outlier ordinals q .. q + 7 (q = outliers before
+// these dims) at their dims.  The B operand splits into
+//   b1 = sgn * cb (outliers take their stored sign), exact fp16;
+//   b2 = sgn * nib / 1024 at outliers, 0 elsewhere, exact fp16;
+// both go through the same A operands and b2's products are scaled by
+// 1024 rs / mult afterwards, per token.
 // V is accumulated in the rotated domain; lane (patch 16 g + li, tokens
 // 4 lg .. 4 lg + 3) decodes straight into the B operand of 16x16x16 MFMAs:
 //   dims (p, k<3): codebook value * (w * a_v * norm * energy)
@@ -63,19 +69,20 @@ __device__ unsigned long long block_times[1024][2];
 constexpr int TT = 16;          // tokens per tile
 constexpr int NTHR = 512;       // 4 key + 4 value wavefronts
 constexpr int CB_PS = 768;      // halves per codebook patch (256 codes x 3)
-constexpr int O_LS = 72;        // halves per lane strip of the outlier buffer
-constexpr int KP_TS = 10;       // words per staged kpay row
+constexpr int KP_TS = 14;       // words per staged kpay row (see key_role staging)
 constexpr int VP_TS = 26;       // words per staged vpay row
 constexpr float RESCALE_GAP = 8.0f;
 
 struct __align__(16) Smem {
     _Float16 cb[64 * CB_PS];     // V codebook, [patch][code][3]       98304 B
-    _Float16 o[4][64 * O_LS];    // outlier values per key lane strip   36864 B
-                                 // (setup: query transform; end: V sums)
+    float o[4][6 * 256];         // setup: query transforms; end: V sums 24576 B
     uint32_t vp[4][TT * VP_TS];  // staged vpay rows per KV head         6656 B
                                  // (setup: rotor_k)
-    uint32_t kp[4][TT * KP_TS];  // staged kpay rows per KV head         2560 B
+    uint32_t kp[4][TT * KP_TS];  // staged kpay rows per KV head         3584 B
     uint2 sgn[256];              // mask byte -> 4 fp16 signs {0,-1,+1,0}
+    uint4 seln[256];             // outlier pattern -> nibble byte selectors
+    uint4 sels[256];             // outlier pattern -> sign byte selectors
+    uint2 sgnb[256];             // 8 sign bits -> sign bytes (even, odd ordinals)
     _Float16 cbk[256];           // cents_k[2]
     float pw[2][4][6][TT];       // softmax weights, by tile parity
     float fac[2][4][8];          // rescale factors of the same tile
@@ -87,6 +94,26 @@ struct __align__(16) Smem {
     float ml[4][6][2];           // final (max, sum) per query head
     float s3[4][8];              // final dump-offset sums per query head
 };
+
+// Loads / stores through global-memory pointers (the batched kernel reads its
+// pointers from memory, where the compiler cannot tell their address space
+// and would otherwise use flat accesses).
+template <typename T>
+__device__ __forceinline__ T ldg(const void* p) {
+    if constexpr (sizeof(T) % 4 == 0) {
+        typedef uint32_t wv __attribute__((ext_vector_type(sizeof(T) / 4)));
+        return __builtin_bit_cast(T, *(const __attribute__((address_space(1))) wv*)p);
+    } else {
+        static_assert(sizeof(T) == 2, "2-byte or word-multiple types");
+        return __builtin_bit_cast(T, *(const __attribute__((address_space(1))) unsigned short*)p);
+    }
+}
+template <typename T>
+__device__ __forceinline__ void stg(void* p, T v) {
+    static_assert(sizeof(T) % 4 == 0, "word-multiple types");
+    typedef uint32_t wv __attribute__((ext_vector_type(sizeof(T) / 4)));
+    *(__attribute__((address_space(1))) wv*)p = __builtin_bit_cast(wv, v);
+}
 
 // Per-lane global inputs of the block set-up, all loaded at kernel entry so
 // their latency overlaps the table copies.
@@ -102,16 +129,16 @@ __device__ __forceinline__ void load_setup(const AttnArgs& a, int h, int wv, int
     const int li = lane & 15, lg = lane >> 4;
     const __half* qbase = a.q + (size_t)(h * 6 + 3 * (wv >> 2)) * 512;
 #pragma unroll
-    for (int hd = 0; hd < 3; hd++) in.qr[hd] = *reinterpret_cast<const uint2*>(qbase + hd * 512 + lane * 4);
-    in.dkr = *reinterpret_cast<const uint2*>(a.dk + lane * 4);
+    for (int hd = 0; hd < 3; hd++) in.qr[hd] = ldg<uint2>(qbase + hd * 512 + lane * 4);
+    in.dkr = ldg<uint2>(a.dk + lane * 4);
     const uint4* rp = reinterpret_cast<const uint4*>(a.rotor_k + lane * 16);
-    in.rk[0] = rp[0];
-    in.rk[1] = rp[1];
+    in.rk[0] = ldg<uint4>(rp);
+    in.rk[1] = ldg<uint4>(rp + 1);
     const __half* qrow = a.q + (size_t)(h * 6 + min(li >> 1, 5)) * 512;
 #pragma unroll
     for (int Tp = 0; Tp < 4; Tp++) {
-        in.dj[Tp] = reinterpret_cast<const unsigned short*>(a.dk)[16 * Tp + li];
-        in.qv[Tp] = *reinterpret_cast<const uint2*>(qrow + 16 * Tp + 4 * lg);
+        in.dj[Tp] = ldg<unsigned short>(a.dk + 16 * Tp + li);
+        in.qv[Tp] = ldg<uint2>(qrow + 16 * Tp + 4 * lg);
     }
 }
 
@@ -119,7 +146,7 @@ __device__ __forceinline__ void load_setup(const AttnArgs& a, int h, int wv, int
 // hd0 + 2): tq_hd = R^T H (q_hd[64:] / (256 d)) into S.o[h] as floats [6][256].
 __device__ __forceinline__ void query_transform(const SetupIn& in, Smem& S, int h, int hd0,
                                                 int lane) {
-    float* tq = reinterpret_cast<float*>(S.o[h]) + hd0 * 256;
+    float* tq = S.o[h] + hd0 * 256;
     const h4 dk4 = __builtin_bit_cast(h4, in.dkr);
     float dks[4];
 #pragma unroll
@@ -164,7 +191,7 @@ __device__ __forceinline__ void query_transform(const SetupIn& in, Smem& S, int 
 __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const SetupIn& in, int h,
                                          int lane, int s_lo, int s_hi, int n_tiles PH_PARAMS) {
     const int li = lane & 15, lg = lane >> 4;
-    const float* tq = reinterpret_cast<const float*>(S.o[h]);  // [6][256] query transforms
+    const float* tq = S.o[h];  // [6][256] query transforms
 
     // A operands (rows: 2 hd = hi, 2 hd + 1 = lo of head hd; rows 12..15 zero)
     const int arow_h = li >> 1;
@@ -278,11 +305,6 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
             }
         }
     }
-    wave_sync();
-    // clear this lane's outlier strip (the query scratch is no longer needed)
-    _Float16* orow = &S.o[h][lane * O_LS];
-#pragma unroll
-    for (int i = 0; i < 8; i++) reinterpret_cast<uint4*>(orow)[i] = uint4{0, 0, 0, 0};
 
     float bc[8], bs[8];
 #pragma unroll
@@ -294,6 +316,27 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
     float lsum[2] = {0.f, 0.f};
     const _Float16* cbq = &S.cbk[64 * lg];
     uint32_t* kpw = S.kp[h];
+    // Staged kpay row of a token, in words: 0 c_base_mult, 1..7 nibbles 0..55
+    // with 50..55 (sign bits in the packed row) cleared, 8..9 zero (nibble
+    // reads at ordinals up to 56 + 15), 10 sign bits 0..23, 11 sign bits
+    // 24..55 (bits past 49 cleared when read).  Ordinals >= 50 so read
+    // nibble 0 and sign 0 (negative), the stored format's default.
+    auto stage_kp = [&](int tok, int part, u2v v) {
+        uint32_t w0 = v[0], w1 = v[1], extra = v[0];
+        int eslot = 11;
+        if (part == 3) {
+            extra = w1 >> 8;
+            eslot = 10;
+            w1 &= 0xFFu;
+        }
+        if (part == 4) {
+            w0 = 0u;
+            w1 = 0u;
+        }
+        uint32_t* row = &kpw[tok * KP_TS];
+        *reinterpret_cast<u2v*>(&row[2 * part]) = u2v{w0, w1};
+        if (part >= 3) row[eslot] = extra;
+    };
     PHASE(1);
 
     for (int it = 0; it <= n_tiles; it++) {
@@ -305,11 +348,8 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
             const uint4 mc = ok ? uint4{m_nx[0], m_nx[1], m_nx[2], m_nx[3]} : uint4{0, 0, 0, 0};
             const float nk = ok ? __half2float(__ushort_as_half(nk_nx)) : 0.0f;
             const float rs = ok ? __half2float(__ushort_as_half(rs_nx)) : 0.0f;
-            *reinterpret_cast<u2v*>(&kpw[kp_tok0 * KP_TS + kp_part0 * 2]) =
-                s0 + kp_tok0 < s_hi ? kp_nx0 : u2v{0, 0};
-            if (lane < 16)
-                *reinterpret_cast<u2v*>(&kpw[kp_tok1 * KP_TS + kp_part1 * 2]) =
-                    s0 + kp_tok1 < s_hi ? kp_nx1 : u2v{0, 0};
+            stage_kp(kp_tok0, kp_part0, s0 + kp_tok0 < s_hi ? kp_nx0 : u2v{0, 0});
+            if (lane < 16) stage_kp(kp_tok1, kp_part1, s0 + kp_tok1 < s_hi ? kp_nx1 : u2v{0, 0});
             if (t + 1 < n_tiles) prefetch(s0 + TT);
             if ((t & 15) == 0) {
 #pragma unroll
@@ -325,80 +365,43 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
             if (mult < 0.1f || mult > 10.0f || isnan(mult)) mult = 1.0f;
             const float rr = rs / mult;
 
-            // ---- outliers of dims 64 lg .. 64 lg + 63.  The sign goes back into
-            // the mask words (code 3 -> 2 for +, 1 for -), so the sign table
-            // yields +-cb; the strip keeps the signed residual nib * rs / mult.
-            uint32_t mw[4] = {mc.x, mc.y, mc.z, mc.w};
-            {
-                uint32_t a3[4];
-                int cnt = 0;
-                uint64_t msk = 0;
+            // ---- outliers of dims 64 lg .. 64 lg + 63: pattern bits and the
+            // ordinal of the first one (outliers of the quarters before)
+            const uint32_t mw[4] = {mc.x, mc.y, mc.z, mc.w};
+            uint64_t msk = 0;
+            int cnt = 0;
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    a3[i] = (mw[i] & (mw[i] >> 1)) & 0x55555555u;
-                    cnt += __popc(a3[i]);
-                    uint32_t x = a3[i];
-                    x = (x | (x >> 1)) & 0x33333333u;
-                    x = (x | (x >> 2)) & 0x0F0F0F0Fu;
-                    x = (x | (x >> 4)) & 0x00FF00FFu;
-                    x = (x | (x >> 8)) & 0x0000FFFFu;
-                    msk |= (uint64_t)x << (16 * i);
-                }
-                // ordinal of the first outlier: outliers of the quarters before
+            for (int i = 0; i < 4; i++) {
+                uint32_t x = (mw[i] & (mw[i] >> 1)) & 0x55555555u;
+                cnt += __popc(x);
+                x = (x | (x >> 1)) & 0x33333333u;
+                x = (x | (x >> 2)) & 0x0F0F0F0Fu;
+                x = (x | (x >> 4)) & 0x00FF00FFu;
+                x = (x | (x >> 8)) & 0x0000FFFFu;
+                msk |= (uint64_t)x << (16 * i);
+            }
+            int qrun;
+            {
                 int incl = cnt;
                 int up = __shfl_up(incl, 16, 64);
                 if (lg >= 1) incl += up;
                 up = __shfl_up(incl, 32, 64);
                 if (lg >= 2) incl += up;
-                int j = incl - cnt;
-                // sign bits (bytes 29..35) and nibbles (bytes 4..28) in outlier
-                // order; only ordinals < 50 are stored (others: sign -1, residual 0)
-                const uint64_t signs = ((uint64_t)krow[7] | ((uint64_t)krow[8] << 32)) >> 8;
-                const int nv0 = max(0, min(64, 50 - j));
-                uint64_t sw = (j < 64 ? (signs >> j) : 0ull) &
-                              (nv0 >= 64 ? ~0ull : ((1ull << nv0) - 1ull));
-                uint64_t nw = 0, neg = 0;
-                int left = 0;
-                while (msk) {
-                    if (left == 0) {
-                        // 16 nibbles from ordinal j: bit 32 + 4 j of the row
-                        const int dwi = 1 + (j >> 3), sh = 4 * (j & 7);
-                        const uint64_t lo64 = (uint64_t)krow[min(dwi, 9)] |
-                                              ((uint64_t)krow[min(dwi + 1, 9)] << 32);
-                        const uint32_t d2 = krow[min(dwi + 2, 9)];
-                        nw = (lo64 >> sh) | (sh ? ((uint64_t)d2 << (64 - sh)) : 0ull);
-                        const int nvn = max(0, min(16, 50 - j));
-                        nw &= (nvn >= 16) ? ~0ull : ((1ull << (4 * nvn)) - 1ull);
-                        left = 16;
-                    }
-                    const int bpos = __builtin_ctzll(msk);
-                    msk &= msk - 1;
-                    const float r = (float)(uint32_t)(nw & 15ull) * rr;
-                    const bool pos = (sw & 1ull) != 0ull;
-                    orow[bpos] = (_Float16)(pos ? r : -r);
-                    neg |= (uint64_t)(!pos) << bpos;
-                    nw >>= 4;
-                    sw >>= 1;
-                    left--;
-                    j++;
-                }
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    uint32_t ng = (uint32_t)(neg >> (16 * i)) & 0xFFFFu;
-                    ng = (ng | (ng << 8)) & 0x00FF00FFu;
-                    ng = (ng | (ng << 4)) & 0x0F0F0F0Fu;
-                    ng = (ng | (ng << 2)) & 0x33333333u;
-                    ng = (ng | (ng << 1)) & 0x55555555u;
-                    mw[i] ^= (ng << 1) | (a3[i] & ~ng);
-                }
+                qrun = incl - cnt;
             }
+            const uint32_t sw10 = krow[10], sw11 = krow[11];
+            const uint64_t sig = (uint64_t)(sw10 | (sw11 << 24)) |
+                                 ((uint64_t)((sw11 >> 8) & 0x3FFFFu) << 32);
 
             PHASE(3);
-            // ---- b operand + pass / fold MFMAs (the strip is cleared as read)
-            f4 cs = f4{0.f, 0.f, 0.f, 0.f};
-            f4 zt[4];
+            // ---- b1 / b2 operands + pass / fold MFMAs
+            f4 cs = f4{0.f, 0.f, 0.f, 0.f}, cs2 = cs;
+            f4 zt[4], zt2[4];
 #pragma unroll
-            for (int T = 0; T < 4; T++) zt[T] = f4{0.f, 0.f, 0.f, 0.f};
+            for (int T = 0; T < 4; T++) {
+                zt[T] = f4{0.f, 0.f, 0.f, 0.f};
+                zt2[T] = zt[T];
+            }
             {
 #pragma unroll
                 for (int st = 0; st < 8; st++) {
@@ -406,39 +409,63 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
                     const int sh = 16 * (st & 1);
                     const uint2 sg0 = S.sgn[(word >> sh) & 0xFFu];
                     const uint2 sg1 = S.sgn[(word >> (sh + 8)) & 0xFFu];
-                    const h8 cb8 = *reinterpret_cast<const h8*>(&cbq[8 * st]);
-                    const h8 o8 = *reinterpret_cast<const h8*>(&orow[8 * st]);
-                    *reinterpret_cast<uint4*>(&orow[8 * st]) = uint4{0, 0, 0, 0};
-                    const h4 s0v = __builtin_bit_cast(h4, sg0), s1v = __builtin_bit_cast(h4, sg1);
-                    const h8 sg = __builtin_shufflevector(s0v, s1v, 0, 1, 2, 3, 4, 5, 6, 7);
-                    const h8 bv = sg * cb8 + o8;
-                    cs = mfma32(At[st], bv, cs);
-                    zt[st >> 1] = mfma32((st & 1) == s_fold ? Aw[st >> 1] : hzero, bv, zt[st >> 1]);
+                    const uint32_t pat = (uint32_t)(msk >> (8 * st)) & 0xFFu;
+                    const int q = min(qrun, 56);
+                    qrun += __popc(pat);
+                    const uint4 sn = S.seln[pat], ss = S.sels[pat];
+                    const uint32_t* nrow = krow + 1 + (q >> 3);
+                    const uint32_t nw = __builtin_amdgcn_alignbit(nrow[1], nrow[0], (q & 7) * 4);
+                    const uint32_t nl = nw & 0x0F0F0F0Fu, nh = (nw >> 4) & 0x0F0F0F0Fu;
+                    const uint2 sb = S.sgnb[(uint32_t)(sig >> q) & 0xFFu];
+                    const uint4 cbw = *reinterpret_cast<const uint4*>(&cbq[8 * st]);
+                    const uint32_t sgw[4] = {sg0.x, sg0.y, sg1.x, sg1.y};
+                    const uint32_t cbv[4] = {cbw.x, cbw.y, cbw.z, cbw.w};
+                    const uint32_t snv[4] = {sn.x, sn.y, sn.z, sn.w};
+                    const uint32_t ssv[4] = {ss.x, ss.y, ss.z, ss.w};
+                    uint32_t b1w[4], b2w[4];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        // xs = +-1 at outlier dims, x = +-(1 + nib / 1024)
+                        const uint32_t xs = __builtin_amdgcn_perm(sb.y, sb.x, ssv[k]);
+                        const uint32_t x = __builtin_amdgcn_perm(nh, nl, snv[k]) | xs;
+                        b2w[k] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, x) -
+                                                                  __builtin_bit_cast(h2, xs));
+                        b1w[k] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, sgw[k] | xs) *
+                                                                  __builtin_bit_cast(h2, cbv[k]));
+                    }
+                    const h8 b1 = __builtin_bit_cast(h8, uint4{b1w[0], b1w[1], b1w[2], b1w[3]});
+                    const h8 b2 = __builtin_bit_cast(h8, uint4{b2w[0], b2w[1], b2w[2], b2w[3]});
+                    cs = mfma32(At[st], b1, cs);
+                    cs2 = mfma32(At[st], b2, cs2);
+                    const h8 aw = (st & 1) == s_fold ? Aw[st >> 1] : hzero;
+                    zt[st >> 1] = mfma32(aw, b1, zt[st >> 1]);
+                    zt2[st >> 1] = mfma32(aw, b2, zt2[st >> 1]);
+                }
+                const float rr1024 = rr * 1024.0f;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    cs[c] = fmaf(rr1024, cs2[c], cs[c]);
+#pragma unroll
+                    for (int T = 0; T < 4; T++) zt[T][c] = fmaf(rr1024, zt2[T][c], zt[T][c]);
                 }
             }
 
             PHASE(4);
-            // ---- H_64 (1/(256 d)) on z, split hi + lo
+            // ---- H_64 (1/(256 d)) on z (z rounded to fp16, nearest)
             f4 kr[4];
             {
-                uint32_t zw[4][4];
+                h8 zb[2];
 #pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    const int T0 = e >> 2, c = e & 3;
-                    split_pk(zt[T0][c], zt[T0][c + 1], zw[0][e >> 1], zw[2][e >> 1]);
-                    split_pk(zt[2 + T0][c], zt[2 + T0][c + 1], zw[1][e >> 1], zw[3][e >> 1]);
-                }
-                h8 zb[4];
-#pragma unroll
-                for (int k = 0; k < 4; k++)
-                    zb[k] = __builtin_bit_cast(h8, uint4{zw[k][0], zw[k][1], zw[k][2], zw[k][3]});
+                for (int k = 0; k < 2; k++)
+                    zb[k] = __builtin_bit_cast(
+                        h8, uint4{pk_rne(zt[2 * k][0], zt[2 * k][1]), pk_rne(zt[2 * k][2], zt[2 * k][3]),
+                                  pk_rne(zt[2 * k + 1][0], zt[2 * k + 1][1]),
+                                  pk_rne(zt[2 * k + 1][2], zt[2 * k + 1][3])});
 #pragma unroll
                 for (int Tp = 0; Tp < 4; Tp++) {
                     f4 acc = f4{0.f, 0.f, 0.f, 0.f};
                     acc = mfma32(Ah[Tp][0], zb[0], acc);
                     acc = mfma32(Ah[Tp][1], zb[1], acc);
-                    acc = mfma32(Ah[Tp][0], zb[2], acc);
-                    acc = mfma32(Ah[Tp][1], zb[3], acc);
                     kr[Tp] = acc;
                 }
             }
@@ -452,23 +479,17 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
                 kr[T0 + 2][cc] = fmaf(x0, bs[u], x1 * bc[u]);
             }
 
-            // ---- roped part of the score on MFMA (key split hi + lo)
+            // ---- roped part of the score on MFMA (key rounded to fp16, nearest)
             {
-                uint32_t kw[4][4];
+                h8 kb[2];
 #pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    const int T0 = e >> 2, c = e & 3;
-                    split_pk(kr[T0][c], kr[T0][c + 1], kw[0][e >> 1], kw[2][e >> 1]);
-                    split_pk(kr[2 + T0][c], kr[2 + T0][c + 1], kw[1][e >> 1], kw[3][e >> 1]);
-                }
-                h8 kb[4];
-#pragma unroll
-                for (int k = 0; k < 4; k++)
-                    kb[k] = __builtin_bit_cast(h8, uint4{kw[k][0], kw[k][1], kw[k][2], kw[k][3]});
+                for (int k = 0; k < 2; k++)
+                    kb[k] = __builtin_bit_cast(
+                        h8, uint4{pk_rne(kr[2 * k][0], kr[2 * k][1]), pk_rne(kr[2 * k][2], kr[2 * k][3]),
+                                  pk_rne(kr[2 * k + 1][0], kr[2 * k + 1][1]),
+                                  pk_rne(kr[2 * k + 1][2], kr[2 * k + 1][3])});
                 cs = mfma32(Aq[0], kb[0], cs);
                 cs = mfma32(Aq[1], kb[1], cs);
-                cs = mfma32(Aq[0], kb[2], cs);
-                cs = mfma32(Aq[1], kb[3], cs);
             }
 
             // ---- scores of heads 2 lg, 2 lg + 1 for token li
@@ -597,7 +618,7 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
         for (int b = 0; b < 2; b++) {
             uint4 cbt[12];
 #pragma unroll
-            for (int i = 0; i < 12; i++) cbt[i] = cbsrc[vt + 256 * (12 * b + i)];
+            for (int i = 0; i < 12; i++) cbt[i] = ldg<uint4>(cbsrc + vt + 256 * (12 * b + i));
 #pragma unroll
             for (int i = 0; i < 12; i++) cbdst[vt + 256 * (12 * b + i)] = cbt[i];
         }
@@ -629,6 +650,7 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
                 if (lane + 64 * k < TT * 13)
                     *reinterpret_cast<u2v*>(&vpw[vp_tok[k] * VP_TS + vp_part[k] * 2]) =
                         s0 + vp_tok[k] < s_hi ? vp_nx[k] : u2v{0, 0};
+            PHASE(10);
             if (lg == 0) {
                 const bool ok = s0 + li < s_hi;
                 const float nv = ok ? __half2float(__ushort_as_half(vn_nx)) : 0.0f;
@@ -658,7 +680,6 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
                 }
             }
 
-            PHASE(10);
             // ---- weights x V scalings -> A operands (rows head hi/lo, K = tokens 4 lg..)
             h4 Ap[3];
             {
@@ -714,7 +735,7 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
     if (lg == 0 && r_ok && !r_lo) S.s3[h][r_head] = s3p;
     __syncthreads();  // (3)
     // rotated-domain sums [6][256] in the key strip area of this KV head
-    float* ep = reinterpret_cast<float*>(S.o[h]);
+    float* ep = S.o[h];
     if (lg < 3) {
 #pragma unroll
         for (int x = 0; x < 2; x++) {
@@ -765,7 +786,7 @@ __device__ void window_block(const AttnArgs& a, Smem& S, int part_idx) {
         const __half* qrow = a.q + (size_t)(hk * 6 + min(li, 5)) * 512;
 #pragma unroll
         for (int st = 0; st < 8; st++) {
-            const uint4 v = *reinterpret_cast<const uint4*>(qrow + 32 * st + 8 * lg);
+            const uint4 v = ldg<uint4>(qrow + 32 * st + 8 * lg);
             Aqk[st] = __builtin_bit_cast(h8, li < 6 ? v : uint4{0u, 0u, 0u, 0u});
         }
     }
@@ -776,7 +797,7 @@ __device__ void window_block(const AttnArgs& a, Smem& S, int part_idx) {
             const int slot = slot_of(min(r0 + 16 * u + li, wl - 1));
             const __half* krow = a.ring_k + ((size_t)slot * a.h_kv + hk) * 256 + 8 * lg;
 #pragma unroll
-            for (int st = 0; st < 8; st++) kv[u][st] = *reinterpret_cast<const uint4*>(krow + 32 * st);
+            for (int st = 0; st < 8; st++) kv[u][st] = ldg<uint4>(krow + 32 * st);
         }
 #pragma unroll
         for (int u = 0; u < 2; u++) {
@@ -829,15 +850,16 @@ __device__ void window_block(const AttnArgs& a, Smem& S, int part_idx) {
 #pragma unroll
         for (int u = 0; u < 16; u++) {
             const int slot = slot_of(min(s0 + u, r_hi - 1));
-            vr[u] = *reinterpret_cast<const uint2*>(a.ring_v + ((size_t)slot * a.h_kv + hk) * 256 + 4 * lane);
+            vr[u] = ldg<uint2>(a.ring_v + ((size_t)slot * a.h_kv + hk) * 256 + 4 * lane);
         }
 #pragma unroll
-        for (int u = 0; u < 16; u++) {
-            if (s0 + u >= r_hi) break;
+        for (int u = 0; u < 16; u++) {  // rows past r_hi weigh 0 (no early exit: vr stays in registers)
+            const bool ok = s0 + u < r_hi;
+            const int su = min(s0 + u, WMAX - 1);
             const h4 vh = __builtin_bit_cast(h4, vr[u]);
 #pragma unroll
             for (int i = 0; i < 6; i++) {
-                const float p = sp[(hk * 6 + i) * WMAX + s0 + u];
+                const float p = ok ? sp[(hk * 6 + i) * WMAX + su] : 0.0f;
 #pragma unroll
                 for (int c = 0; c < 4; c++) acc[i][c] = fmaf(p, (float)vh[c], acc[i][c]);
             }
@@ -856,11 +878,10 @@ __device__ void window_block(const AttnArgs& a, Smem& S, int part_idx) {
             const f4 o = *reinterpret_cast<const f4*>(&sacc[(hk * 6 + i) * 256 + 4 * lane]);
             const int hq = hk * 6 + i;
             float* out = a.part + ((size_t)hq * a.part_stride + part_idx) * 258;
-            *reinterpret_cast<f4*>(&out[4 * lane]) =
-                f4{acc[i][0] + o[0], acc[i][1] + o[1], acc[i][2] + o[2], acc[i][3] + o[3]};
+            stg<f4>(&out[4 * lane], f4{acc[i][0] + o[0], acc[i][1] + o[1], acc[i][2] + o[2], acc[i][3] + o[3]});
             if (lane == 0) {
-                out[256] = sml[(hk * 6 + i) * 2 + 0];
-                out[257] = sml[(hk * 6 + i) * 2 + 1];
+                stg<float>(&out[256], sml[(hk * 6 + i) * 2 + 0]);
+                stg<float>(&out[257], sml[(hk * 6 + i) * 2 + 1]);
             }
         }
     }
@@ -905,20 +926,52 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
                 s[c] = code == 2 ? (_Float16)1.0f : (code == 1 ? (_Float16)-1.0f : (_Float16)0.0f);
             }
             S.sgn[tid] = __builtin_bit_cast(uint2, s);
-            S.cbk[tid] = reinterpret_cast<const _Float16*>(a.cents_k)[512 + tid];
+            S.cbk[tid] = ldg<_Float16>(a.cents_k + 512 + tid);
+            // outlier pattern tid (bit i: dim i of 8 is an outlier): output
+            // word k holds dims 2k, 2k + 1 as fp16 halves; the nibble selector
+            // puts the byte of ordinal rank(i) in the low byte of the half, the
+            // sign selector in the high byte.  Bytes of even ordinals come
+            // from the second perm source, odd ones from the first (4 + r / 2).
+            uint32_t sn[4], ss[4];
+            int r = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                uint32_t n = 0x0C0C0C0Cu, g = 0x0C0C0C0Cu;
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    if ((tid >> (2 * k + e)) & 1) {
+                        const uint32_t src = (r & 1) ? 4u + (uint32_t)(r >> 1) : (uint32_t)(r >> 1);
+                        n = (n & ~(0xFFu << (16 * e))) | (src << (16 * e));
+                        g = (g & ~(0xFFu << (16 * e + 8))) | (src << (16 * e + 8));
+                        r++;
+                    }
+                }
+                sn[k] = n;
+                ss[k] = g;
+            }
+            S.seln[tid] = uint4{sn[0], sn[1], sn[2], sn[3]};
+            S.sels[tid] = uint4{ss[0], ss[1], ss[2], ss[3]};
+            // sign bits tid (bit r: ordinal r positive) -> high bytes of +-1.0
+            uint32_t ev = 0, od = 0;
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                ev |= (((tid >> (2 * m)) & 1) ? 0x3Cu : 0xBCu) << (8 * m);
+                od |= (((tid >> (2 * m + 1)) & 1) ? 0x3Cu : 0xBCu) << (8 * m);
+            }
+            S.sgnb[tid] = uint2{ev, od};
         } else if (tid < 256 + 128) {
             reinterpret_cast<uint4*>(&S.vp[0][0])[tid - 256] =
-                reinterpret_cast<const uint4*>(a.rotor_k)[tid - 256];
+                ldg<uint4>(reinterpret_cast<const uint4*>(a.rotor_k) + tid - 256);
         } else {
             reinterpret_cast<uint4*>(S.rotv)[tid - 384] =
-                reinterpret_cast<const uint4*>(a.rotor_v)[tid - 384];
+                ldg<uint4>(reinterpret_cast<const uint4*>(a.rotor_v) + tid - 384);
         }
         if (tid < 128) {
-            const _Float16* cvh = reinterpret_cast<const _Float16*>(a.cents_v);
-            S.c3v[tid >> 6][tid & 63] = cvh[(tid >> 6) * 256 + (tid & 63) * 4 + 3];
+            const __half* cvh = a.cents_v;
+            S.c3v[tid >> 6][tid & 63] = ldg<_Float16>(cvh + (tid >> 6) * 256 + (tid & 63) * 4 + 3);
         }
         if (tid < 32) {
-            reinterpret_cast<uint4*>(S.dvh)[tid] = reinterpret_cast<const uint4*>(a.dv)[tid];
+            reinterpret_cast<uint4*>(S.dvh)[tid] = ldg<uint4>(reinterpret_cast<const uint4*>(a.dv) + tid);
         } else if (tid >= 448) {
             // lanes (u, lg) with u < 8 of the last wavefront: RoPE table
             const int l = tid - 448, u = l & 15, g = l >> 4;
@@ -944,7 +997,7 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
 #endif
 
     // ---- output: wavefront wv handles query heads 3 (wv / 4) .. + 2 of KV head h
-    const float* ep = reinterpret_cast<const float*>(S.o[h]);
+    const float* ep = S.o[h];
     float rv[16];
 #pragma unroll
     for (int t = 0; t < 16; t++) rv[t] = (float)S.rotv[lane * 16 + t];
@@ -972,12 +1025,10 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
         const float L = S.ml[h][hd][1];
         const bool empty = (M == -INFINITY);
 #pragma unroll
-        for (int c = 0; c < 4; c++)
-            out[lane * 4 + c] =
-                empty ? 0.0f : u[c] * rdv[c];
+        for (int c = 0; c < 4; c++) stg<float>(&out[lane * 4 + c], empty ? 0.0f : u[c] * rdv[c]);
         if (lane == 0) {
-            out[256] = empty ? -1e20f : M;
-            out[257] = empty ? 0.0f : L;
+            stg<float>(&out[256], empty ? -1e20f : M);
+            stg<float>(&out[257], empty ? 0.0f : L);
         }
     }
     PHASE(15);
@@ -1002,7 +1053,7 @@ __global__ __launch_bounds__(NTHR, 1) void attn_ws_batched_kernel(const AttnArgs
                                                                   const int2* __restrict__ map,
                                                                   int tiles_per_chunk) {
     const int2 m = map[blockIdx.x];
-    const AttnArgs a = args[m.x];
+    const AttnArgs& a = args[m.x];  // read in place (a private copy would go to scratch)
     ws_block(a, m.y, tiles_per_chunk, a.n_parts);
 }
 

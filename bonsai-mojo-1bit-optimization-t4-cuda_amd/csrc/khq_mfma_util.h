@@ -98,6 +98,12 @@ __device__ __forceinline__ float mix_hi(uint32_t hp, float m, float x) {
 __device__ __forceinline__ uint32_t pk_rtz(float x, float y) {
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x, y));
 }
+// Packed fp16 (x, y), round to nearest even (gfx950 v_cvt_pk_f16_f32).
+__device__ __forceinline__ uint32_t pk_rne(float x, float y) {
+    uint32_t d;
+    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(d) : "v"(x), "v"(y));
+    return d;
+}
 // Packed fp16 hi (truncated) and lo (remainder) parts of (x, y).
 __device__ __forceinline__ void split_pk(float x, float y, uint32_t& hi, uint32_t& lo) {
     hi = pk_rtz(x, y);
