@@ -26,9 +26,9 @@
 // the nibbles and signs of outlier ordinals q .. q + 7 (q = outliers before
 // these dims) at their dims.  The B operand splits into
 //   b1 = sgn * cb (outliers take their stored sign), exact fp16;
-//   b2 = sgn * nib / 1024 at outliers, 0 elsewhere, exact fp16;
+//   b2 = sgn * nib * 2^-14 at outliers, 0 elsewhere, exact fp16;
 // both go through the same A operands and b2's products are scaled by
-// 1024 rs / mult afterwards, per token.
+// 2^14 rs / mult afterwards, per token.
 // V is accumulated in the rotated domain; lane (patch 16 g + li, tokens
 // 4 lg .. 4 lg + 3) decodes straight into the B operand of 16x16x16 MFMAs:
 //   dims (p, k<3): codebook value * (w * a_v * norm * energy)
@@ -86,7 +86,6 @@ struct __align__(16) Smem {
     _Float16 cbk[256];           // cents_k[2]
     float pw[2][4][6][TT];       // softmax weights, by tile parity
     float fac[2][4][8];          // rescale factors of the same tile
-    float vsc[4][3][TT];         // per token V scalings
     float rope[4][3][8];         // per lane group: freq, cos(16 f), sin(16 f)
     _Float16 rotv[64 * 16];      // rotor_v
     _Float16 dvh[256];           // d_v
@@ -382,12 +381,13 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
             }
             int qrun;
             {
-                int incl = cnt;
-                int up = __shfl_up(incl, 16, 64);
-                if (lg >= 1) incl += up;
-                up = __shfl_up(incl, 32, 64);
-                if (lg >= 2) incl += up;
-                qrun = incl - cnt;
+                // outliers of the quarters before this lane's, across the 4 lane
+                // rows of the token (row swaps, no LDS round trip)
+                const auto p16 = __builtin_amdgcn_permlane16_swap((uint32_t)cnt, (uint32_t)cnt, false, false);
+                const uint32_t c_even = p16[0], c_odd = p16[1];  // rows 2 k, 2 k + 1
+                const uint32_t pair = c_even + c_odd;
+                const auto p32 = __builtin_amdgcn_permlane32_swap(pair, pair, false, false);
+                qrun = (int)(((lg & 1) ? c_even : 0u) + ((lg >= 2) ? p32[0] : 0u));
             }
             const uint32_t sw10 = krow[10], sw11 = krow[11];
             const uint64_t sig = (uint64_t)(sw10 | (sw11 << 24)) |
@@ -425,13 +425,16 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
                     uint32_t b1w[4], b2w[4];
 #pragma unroll
                     for (int k = 0; k < 4; k++) {
-                        // xs = +-1 at outlier dims, x = +-(1 + nib / 1024)
-                        const uint32_t xs = __builtin_amdgcn_perm(sb.y, sb.x, ssv[k]);
-                        const uint32_t x = __builtin_amdgcn_perm(nh, nl, snv[k]) | xs;
-                        b2w[k] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, x) -
-                                                                  __builtin_bit_cast(h2, xs));
-                        b1w[k] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, sgw[k] | xs) *
-                                                                  __builtin_bit_cast(h2, cbv[k]));
+                        // at outlier dims: xs = +-1024, xn = nib * 2^-24 (an fp16
+                        // subnormal, exact), so b2 = xn * xs = +-nib * 2^-14 and
+                        // b1 = (sgn + xs / 1024) * cb; both products are exact
+                        const h2 xs = __builtin_bit_cast(h2, __builtin_amdgcn_perm(sb.y, sb.x, ssv[k]));
+                        const h2 xn = __builtin_bit_cast(h2, __builtin_amdgcn_perm(nh, nl, snv[k]));
+                        b2w[k] = __builtin_bit_cast(uint32_t, xn * xs);
+                        const h2 sgy = __builtin_elementwise_fma(
+                            xs, h2{(_Float16)0.0009765625f, (_Float16)0.0009765625f},
+                            __builtin_bit_cast(h2, sgw[k]));
+                        b1w[k] = __builtin_bit_cast(uint32_t, sgy * __builtin_bit_cast(h2, cbv[k]));
                     }
                     const h8 b1 = __builtin_bit_cast(h8, uint4{b1w[0], b1w[1], b1w[2], b1w[3]});
                     const h8 b2 = __builtin_bit_cast(h8, uint4{b2w[0], b2w[1], b2w[2], b2w[3]});
@@ -441,7 +444,7 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
                     zt[st >> 1] = mfma32(aw, b1, zt[st >> 1]);
                     zt2[st >> 1] = mfma32(aw, b2, zt2[st >> 1]);
                 }
-                const float rr1024 = rr * 1024.0f;
+                const float rr1024 = rr * 16384.0f;  // b2 carries nib * 2^-14
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
                     cs[c] = fmaf(rr1024, cs2[c], cs[c]);
@@ -590,7 +593,9 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
     uint32_t vo_vp[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) vo_vp[k] = (uint32_t)(vp_tok[k] * 4 + h) * 104 + vp_part[k] * 8;
-    const uint32_t vo_n = (uint32_t)(li * 4 + h);
+    // norms of token 4 lg + (li & 3): the lane quad holds this lane group's tokens
+    const int n_tok = 4 * lg + (li & 3);
+    const uint32_t vo_n = (uint32_t)(n_tok * 4 + h);
     u2v vp_nx[4];
     unsigned short vn_nx = 0, ve_nx = 0;
     uint32_t vm_nx = 0;
@@ -643,6 +648,13 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
         if (it >= 1) {
             const int t = it - 1;
             const int buf = t & 1;
+            // ---- the key side's weights and rescale factors of this tile
+            // (read first: their latency overlaps the staging below)
+            const float f0 = lg < 3 ? S.fac[buf][h][2 * lg] : 1.0f;
+            const float f1 = lg < 3 ? S.fac[buf][h][2 * lg + 1] : 1.0f;
+            const float fr = r_ok ? S.fac[buf][h][r_head] : 1.0f;
+            f4 pw4 = f4{0.f, 0.f, 0.f, 0.f};
+            if (r_ok) pw4 = *reinterpret_cast<const f4*>(&S.pw[buf][h][r_head][4 * lg]);
             // ---- take the staged tile, start loading the next one
             const int s0 = s_lo + t * TT;
 #pragma unroll
@@ -651,44 +663,44 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
                     *reinterpret_cast<u2v*>(&vpw[vp_tok[k] * VP_TS + vp_part[k] * 2]) =
                         s0 + vp_tok[k] < s_hi ? vp_nx[k] : u2v{0, 0};
             PHASE(10);
-            if (lg == 0) {
-                const bool ok = s0 + li < s_hi;
+            // V scalings of token n_tok, then of tokens 4 lg .. 4 lg + 3 from
+            // the lane quad (DPP broadcast)
+            float sv[3][4];
+            {
+                const bool ok = s0 + n_tok < s_hi;
                 const float nv = ok ? __half2float(__ushort_as_half(vn_nx)) : 0.0f;
                 const float en = ok ? __half2float(__ushort_as_half(ve_nx)) : 0.0f;
                 const float vm = ok ? __uint_as_float(vm_nx) : 0.0f;
-                S.vsc[h][0][li] = (av * nv) * en;
-                S.vsc[h][1][li] = av * nv;
-                S.vsc[h][2][li] = nv * vm / 7.0f;
+                const float own[3] = {(av * nv) * en, av * nv, nv * vm / 7.0f};
+#pragma unroll
+                for (int v = 0; v < 3; v++) {
+                    sv[v][0] = dpp<0x00>(own[v]);
+                    sv[v][1] = dpp<0x55>(own[v]);
+                    sv[v][2] = dpp<0xAA>(own[v]);
+                    sv[v][3] = dpp<0xFF>(own[v]);
+                }
             }
             if (t + 1 < n_tiles) prefetch(s_lo + (t + 1) * TT);
             wave_sync();
 
             // ---- rescale for a raised maximum (rows 4 lg + c: head 2 lg + c / 2)
-            {
-                const float f0 = lg < 3 ? S.fac[buf][h][2 * lg] : 1.0f;
-                const float f1 = lg < 3 ? S.fac[buf][h][2 * lg + 1] : 1.0f;
-                const float fr = r_ok ? S.fac[buf][h][r_head] : 1.0f;
-                if (__ballot(f0 != 1.0f || f1 != 1.0f || fr != 1.0f) != 0ull) {
+            if (__ballot(f0 != 1.0f || f1 != 1.0f || fr != 1.0f) != 0ull) {
 #pragma unroll
-                    for (int n = 0; n < 20; n++) {
-                        pv[n][0] *= f0;
-                        pv[n][1] *= f0;
-                        pv[n][2] *= f1;
-                        pv[n][3] *= f1;
-                    }
-                    s3p *= fr;
+                for (int n = 0; n < 20; n++) {
+                    pv[n][0] *= f0;
+                    pv[n][1] *= f0;
+                    pv[n][2] *= f1;
+                    pv[n][3] *= f1;
                 }
+                s3p *= fr;
             }
 
             // ---- weights x V scalings -> A operands (rows head hi/lo, K = tokens 4 lg..)
             h4 Ap[3];
             {
-                f4 pw4 = f4{0.f, 0.f, 0.f, 0.f};
-                if (r_ok) pw4 = *reinterpret_cast<const f4*>(&S.pw[buf][h][r_head][4 * lg]);
 #pragma unroll
                 for (int v = 0; v < 3; v++) {
-                    const f4 sv = *reinterpret_cast<const f4*>(&S.vsc[h][v][4 * lg]);
-                    const f4 w = pw4 * sv;
+                    const f4 w = pw4 * f4{sv[v][0], sv[v][1], sv[v][2], sv[v][3]};
                     if (v == 2 && !r_lo) s3p += (w[0] + w[1]) + (w[2] + w[3]);
                     const uint2 pk = uint2{part_pk(w[0], w[1], m_lo), part_pk(w[2], w[3], m_lo)};
                     Ap[v] = __builtin_bit_cast(h4, pk);
@@ -951,12 +963,12 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
             }
             S.seln[tid] = uint4{sn[0], sn[1], sn[2], sn[3]};
             S.sels[tid] = uint4{ss[0], ss[1], ss[2], ss[3]};
-            // sign bits tid (bit r: ordinal r positive) -> high bytes of +-1.0
+            // sign bits tid (bit r: ordinal r positive) -> high bytes of +-1024
             uint32_t ev = 0, od = 0;
 #pragma unroll
             for (int m = 0; m < 4; m++) {
-                ev |= (((tid >> (2 * m)) & 1) ? 0x3Cu : 0xBCu) << (8 * m);
-                od |= (((tid >> (2 * m + 1)) & 1) ? 0x3Cu : 0xBCu) << (8 * m);
+                ev |= (((tid >> (2 * m)) & 1) ? 0x64u : 0xE4u) << (8 * m);
+                od |= (((tid >> (2 * m + 1)) & 1) ? 0x64u : 0xE4u) << (8 * m);
             }
             S.sgnb[tid] = uint2{ev, od};
         } else if (tid < 256 + 128) {
@@ -1034,7 +1046,7 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
     PHASE(15);
 #ifdef KHQ_PHASE_TIMING
     if (blockIdx.x == 0 && (threadIdx.x & 0xFF) == 0)
-        for (int k = 0; k < 16; k++) phase_cycles[k] += ph_acc[k];
+        for (int k = 0; k < 16; k++) atomicAdd(&phase_cycles[k], (unsigned long long)ph_acc[k]);
     if (threadIdx.x == 0 && blockIdx.x < 1024) {
         block_times[blockIdx.x][0] = rt0;
         block_times[blockIdx.x][1] = __builtin_amdgcn_s_memrealtime();
