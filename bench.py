@@ -57,6 +57,10 @@ def parse():
     ap.add_argument("--config", choices=["c3", "c4"], default="c3",
                     help="c3: the headline 32K-context step (default); c4: 32 ragged "
                          "sequences per layer-step in one batched call")
+    ap.add_argument("--counters-run", action="store_true",
+                    help="profiling aid for rocprofv3 --pmc: a 256 MiB device copy (the "
+                         "calibration kernel of known size), then the compressed-region kernel "
+                         "on 4 C3 layers, 3 times; prints no JSON")
     ap.add_argument("--sweep", action="store_true",
                     help="also time the reference entry points at splits 1/8/32/64")
     return ap.parse_args()
@@ -74,6 +78,8 @@ def main():
     _lib.call("khq_select_kernel", ["auto", "portable", "mfma-single"].index(args.kernel))
     if args.config == "c4":
         return bench_c4(args)
+    if args.counters_run:
+        return counters_run(args)
     from khq.centroids import synthetic_layer
 
     dev = "cuda"
@@ -233,6 +239,37 @@ def main():
         result["cpu_baseline"] = cpu_baseline(layers[0], c_len, win_len, win_start, scale,
                                               args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+def counters_run(args):
+    """Fixed dispatch sequence for hardware-counter passes: one 256 MiB copy
+    (read 256 MiB, write 256 MiB: the scale of FETCH_SIZE / WRITE_SIZE), then
+    khq_attn_partials_fp16 on 4 distinct C3 layers, 3 rounds (12 dispatches)."""
+    import torch
+
+    from khq import ops, synth
+    from khq.centroids import synthetic_layer
+
+    dev = "cuda"
+    c_len = args.ctx - args.win
+    x = torch.empty(64 << 20, device=dev)
+    y = torch.empty_like(x)
+    x.fill_(1.0)
+    torch.cuda.synchronize()
+    y.copy_(x)
+    layers = []
+    for l in range(4):
+        lc = synthetic_layer(l, seed=1234)
+        pay = ops.Payload(c_len * H_KV, dev)
+        for k, v in synth.random_rows(c_len * H_KV, seed=1000 + l, device=dev).items():
+            getattr(pay, k).copy_(v)
+        layers.append((pay, ops.Centroids(lc, dev), synth.q_gate(H_Q, seed=7000 + l, device=dev)))
+    torch.cuda.synchronize()
+    for _ in range(3):
+        for pay, cents, q in layers:
+            ops.attn_partials(q, pay, cents, H_q=H_Q, H_kv=H_KV, c_len=c_len, scale=1.0 / 16.0)
+    torch.cuda.synchronize()
+    print("counters run done", file=sys.stderr)
 
 
 def bench_c4(args):

@@ -58,10 +58,17 @@ __device__ unsigned long long block_times[1024][2];
         ph_acc[k] += (unsigned)(now_ - ph_t);                                 \
         ph_t = now_;                                                          \
     } while (0)
+// wait for the outstanding global loads, then close phase k
+#define PHASE_VM(k)                                                           \
+    do {                                                                      \
+        __builtin_amdgcn_s_waitcnt(0x0F70);                                   \
+        PHASE(k);                                                             \
+    } while (0)
 #define PH_PARAMS , unsigned long long ph_t, unsigned (&ph_acc)[16]
 #define PH_ARGS , ph_t, ph_acc
 #else
 #define PHASE(k) do { } while (0)
+#define PHASE_VM(k) do { } while (0)
 #define PH_PARAMS
 #define PH_ARGS
 #endif
@@ -340,6 +347,7 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
 
     for (int it = 0; it <= n_tiles; it++) {
         if (it < n_tiles) {
+            PHASE_VM(7);
             const int t = it;
             const int s0 = s_lo + t * TT;
             // ---- take the staged tile, start loading the next one
@@ -561,7 +569,7 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
     }
     __syncthreads();  // (3) maxima / sums / dump sums published
     __syncthreads();  // (4) V sums in place
-    PHASE(7);
+    PHASE(15);
 }
 
 // -------------------------------------------------------------- value role
@@ -646,6 +654,7 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
 
     for (int it = 0; it <= n_tiles; it++) {
         if (it >= 1) {
+            PHASE_VM(14);
             const int t = it - 1;
             const int buf = t & 1;
             // ---- the key side's weights and rescale factors of this tile
@@ -765,7 +774,7 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
         }
     }
     __syncthreads();  // (4)
-    PHASE(14);
+    PHASE(15);
 }
 
 // ------------------------------------------------------------ window block
