@@ -416,6 +416,80 @@ int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_
                                           static_cast<__half*>(out), H_q, np, 1e-8f, stream));
 }
 
+int khq_decompress_fp16(const void* k_payload, const void* v_payload, const void* v_shared_meta,
+                        const void* k_mask, const void* k_norms, const void* k_r_norms,
+                        const void* v_norms, const void* v_r_norms, const void* centroids_k,
+                        const void* centroids_v, const void* vq_centroids, const void* k_rotor,
+                        const void* v_rotor, const void* d_vec_k, const void* d_vec_v, int H_kv,
+                        int tok0, int n_tok, int start_pos, float alpha_k, float alpha_v,
+                        float rope_base, void* out_k, int key0, void* out_vt, int ld_vt,
+                        hipStream_t stream) {
+    if (H_kv <= 0 || tok0 < 0 || n_tok < 0 || key0 < 0 || !out_k || !out_vt) return -100;
+    if (ld_vt % 8 != 0 || ld_vt < key0 + (n_tok + 63) / 64 * 64) return -100;
+    khq::DecompArgs a{};
+    a.kpay = static_cast<const uint8_t*>(k_payload);
+    a.vpay = static_cast<const uint8_t*>(v_payload);
+    a.vsm = static_cast<const uint8_t*>(v_shared_meta);
+    a.kmask = static_cast<const uint32_t*>(k_mask);
+    a.knorm = static_cast<const __half*>(k_norms);
+    a.krn = static_cast<const __half*>(k_r_norms);
+    a.vnorm = static_cast<const __half*>(v_norms);
+    a.vrn = static_cast<const __half*>(v_r_norms);
+    a.cents_k = static_cast<const __half*>(centroids_k);
+    a.cents_v = static_cast<const __half*>(centroids_v);
+    a.vq = static_cast<const __half*>(vq_centroids);
+    a.rotor_k = static_cast<const __half*>(k_rotor);
+    a.rotor_v = static_cast<const __half*>(v_rotor);
+    a.dk = static_cast<const __half*>(d_vec_k);
+    a.dv = static_cast<const __half*>(d_vec_v);
+    a.out_k = static_cast<__half*>(out_k);
+    a.out_vt = static_cast<__half*>(out_vt);
+    a.h_kv = H_kv;
+    a.tok0 = tok0;
+    a.n_tok = n_tok;
+    a.start_pos = start_pos;
+    a.key0 = key0;
+    a.ld_vt = ld_vt;
+    a.a_k = alpha_k;
+    a.a_v = alpha_v;
+    a.rope_base = rope_base;
+    return rc_of(khq::launch_decompress(a, stream));
+}
+
+int khq_prefill_attn_fp16(const void* q_gate, const void* k, const void* vt, int ld_vt, int n_k,
+                          int n_q, int vis0, int H_q, int H_kv, float scale, void* out,
+                          hipStream_t stream) {
+    if (!q_gate || !k || !vt || !out || n_k <= 0 || n_q <= 0 || vis0 < 1) return -100;
+    if (H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || ld_vt % 8 != 0 ||
+        ld_vt < (n_k + 15) / 16 * 16)
+        return -100;
+    const int n_rep = H_q / H_kv;
+    int per = 0;
+    const int ns = khq::prefill_splits(n_q, n_rep, H_kv, n_k, &per);
+    float* ws = nullptr;
+    hipError_t e = workspace((size_t)n_q * H_q * ns * 258 * sizeof(float), &ws);
+    if (e != hipSuccess) return rc_of(e);
+    khq::PrefillArgs a{};
+    a.q = static_cast<const __half*>(q_gate);
+    a.k = static_cast<const __half*>(k);
+    a.vt = static_cast<const __half*>(vt);
+    a.part = ws;
+    a.ld_vt = ld_vt;
+    a.n_k = n_k;
+    a.n_q = n_q;
+    a.vis0 = vis0;
+    a.h_kv = H_kv;
+    a.n_rep = n_rep;
+    a.n_split = ns;
+    a.keys_per_split = per;
+    a.sc = scale;
+    e = khq::launch_prefill_attn(a, stream);
+    if (e != hipSuccess) return rc_of(e);
+    return rc_of(khq::launch_combine_gate(ws, static_cast<const __half*>(q_gate),
+                                          static_cast<__half*>(out), n_q * H_q, ns, 1e-8f,
+                                          stream));
+}
+
 int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centroids_k,
                                const void* centroids_v, const void* vq_centroids,
                                const void* k_rotor, const void* v_rotor, const void* d_vec_k,

@@ -101,4 +101,57 @@ hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks,
 hipError_t launch_attn_ws_batched(const AttnArgs* args, const int2* map, int n_blocks,
                                   int tiles_per_chunk, hipStream_t st);
 
+// ---- chunked prefill (khq_prefill.hip)
+// Compressed rows [tok0, tok0 + n_tok) of every KV head -> dense fp16 roped K
+// rows out_k[(key0 + t) * h_kv + h][256] and V^T out_vt[h][256][ld_vt]
+// columns key0 + t (ld_vt >= key0 + n_tok rounded up to 64, multiple of 8).
+struct DecompArgs {
+    const uint8_t* kpay;
+    const uint8_t* vpay;
+    const uint8_t* vsm;
+    const uint32_t* kmask;
+    const __half* knorm;
+    const __half* krn;
+    const __half* vnorm;
+    const __half* vrn;
+    const __half* cents_k;
+    const __half* cents_v;
+    const __half* vq;
+    const __half* rotor_k;
+    const __half* rotor_v;
+    const __half* dk;
+    const __half* dv;
+    __half* out_k;
+    __half* out_vt;
+    int h_kv, tok0, n_tok, start_pos, key0, ld_vt;
+    float a_k, a_v, rope_base;
+};
+// Ring slots (win_start + t) % ring_cap, t < n -> the same key layout at key0 + t.
+struct GatherArgs {
+    const __half* ring_k;
+    const __half* ring_v;
+    __half* out_k;
+    __half* out_vt;
+    int h_kv, win_start, n, ring_cap, key0, ld_vt;
+};
+// n_q queries (q_gate rows [n_q][H_q][512]) over dense keys [0, n_k); query j
+// sees keys [0, min(n_k, vis0 + j)).  Partial triple of (query j, head hq,
+// split s) at part[((j * H_q + hq) * n_split + s) * 258].
+struct PrefillArgs {
+    const __half* q;
+    const __half* k;
+    const __half* vt;
+    float* part;
+    int ld_vt, n_k, n_q, vis0, h_kv, n_rep, n_split, keys_per_split;
+    float sc;
+};
+hipError_t launch_decompress(const DecompArgs& a, hipStream_t st);
+hipError_t launch_ring_gather(const GatherArgs& a, hipStream_t st);
+int prefill_splits(int n_q, int n_rep, int h_kv, int n_k, int* keys_per_split);
+hipError_t launch_prefill_attn(const PrefillArgs& a, hipStream_t st);
+// n consecutive tokens (kv halves each) into ring slots (slot0 + i) % ring_cap.
+hipError_t launch_ring_write_n(__half* rk, __half* rv, __half* ru, const __half* k,
+                               const __half* v, const __half* ku, int kv, int slot0, int n,
+                               int ring_cap, hipStream_t st);
+
 }  // namespace khq

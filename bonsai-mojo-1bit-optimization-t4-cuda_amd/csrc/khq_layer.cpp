@@ -16,6 +16,7 @@
 #include <new>
 
 #include "khq.h"
+#include "khq_internal.h"
 
 namespace {
 
@@ -39,13 +40,17 @@ struct khq_layer {
     __half *knorm = nullptr, *krn = nullptr, *vnorm = nullptr, *vrn = nullptr;
     float *ac = nullptr, *aw = nullptr, *ap = nullptr;
     int boundary = 0, write_pos = 0, n_events = 0;
+    // chunked prefill: dense fp16 keys [key][H_kv][256] and V^T [H_kv][256][ld]
+    // (key = token position), compressed tokens [0, dec_hi) already decoded
+    __half *dk = nullptr, *dvt = nullptr;
+    int d_keys = 0, d_ld = 0, dec_hi = 0;
 };
 
 namespace {
 
 void release(khq_layer* L) {
     void* ptrs[] = {L->ring_k, L->ring_v, L->ring_u, L->kmask, L->kpay, L->vpay, L->vsm,
-                    L->knorm, L->krn, L->vnorm, L->vrn, L->ac, L->aw, L->ap};
+                    L->knorm, L->krn, L->vnorm, L->vrn, L->ac, L->aw, L->ap, L->dk, L->dvt};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
 }
@@ -57,6 +62,32 @@ bool alloc_zero(T** p, size_t bytes) {
         return false;
     }
     return hipMemset(*p, 0, bytes) == hipSuccess;
+}
+
+// Compression event: ring slots [boundary % 256, + 128) -> payload rows of
+// tokens [boundary, boundary + 128) (ref runtime.mojo:494-552).
+int compress_event(khq_layer* L, hipStream_t stream) {
+    const int kv = L->H_kv * kD;
+    const int s0 = L->boundary % kRing;
+    const size_t r0 = (size_t)L->boundary * L->H_kv;
+    const int n = kChunk * L->H_kv;
+    int rc = launch_khq_compress_fp16(L->ring_u + (size_t)s0 * kv, L->d_k, L->rotor_k, L->cents_k,
+                                      L->cents_k, L->kmask + r0 * 16, L->knorm + r0, L->krn + r0,
+                                      L->kpay + r0 * 40, L->vsm + r0 * 4, n, kD, L->ts_k,
+                                      L->alpha_k, 0, stream);
+    if (rc) return rc;
+    rc = launch_khq_compress_fp16(L->ring_v + (size_t)s0 * kv, L->d_v, L->rotor_v, L->cents_v,
+                                  L->vq, L->kmask + r0 * 16, L->vnorm + r0, L->vrn + r0,
+                                  L->vpay + r0 * 104, L->vsm + r0 * 4, n, kD, L->ts_v,
+                                  L->alpha_v, 1, stream);
+    if (rc) return rc;
+    L->boundary += kChunk;
+    L->n_events += 1;
+    return 0;
+}
+
+bool event_due(const khq_layer* L, int write_pos) {  // ref runtime.mojo:494-497
+    return write_pos - L->boundary >= kWatermark && L->boundary + kChunk <= L->cap;
 }
 
 int split_count(int c_len, int splits) {  // ref runtime.mojo:211-222
@@ -126,6 +157,7 @@ int khq_layer_reset(khq_layer* L) {
     L->boundary = 0;
     L->write_pos = 0;
     L->n_events = 0;
+    L->dec_hi = 0;
     return 0;
 }
 
@@ -161,23 +193,9 @@ int khq_layer_step(khq_layer* L, const void* q_gate, const void* k_roped, const 
                                         k_roped, v, k_unroped, slot, kv, stream);
     if (rc) return rc;
     L->write_pos += 1;
-    if (L->write_pos - L->boundary >= kWatermark && L->boundary + kChunk <= L->cap) {
-        // compression event: ring slots [boundary % 256, + 128) -> payload rows
-        const int s0 = L->boundary % kRing;
-        const size_t r0 = (size_t)L->boundary * L->H_kv;
-        const int n = kChunk * L->H_kv;
-        rc = launch_khq_compress_fp16(L->ring_u + (size_t)s0 * kv, L->d_k, L->rotor_k, L->cents_k,
-                                      L->cents_k, L->kmask + r0 * 16, L->knorm + r0, L->krn + r0,
-                                      L->kpay + r0 * 40, L->vsm + r0 * 4, n, kD, L->ts_k,
-                                      L->alpha_k, 0, stream);
+    if (event_due(L, L->write_pos)) {
+        rc = compress_event(L, stream);
         if (rc) return rc;
-        rc = launch_khq_compress_fp16(L->ring_v + (size_t)s0 * kv, L->d_v, L->rotor_v, L->cents_v,
-                                      L->vq, L->kmask + r0 * 16, L->vnorm + r0, L->vrn + r0,
-                                      L->vpay + r0 * 104, L->vsm + r0 * 4, n, kD, L->ts_v,
-                                      L->alpha_v, 1, stream);
-        if (rc) return rc;
-        L->boundary += kChunk;
-        L->n_events += 1;
     }
     const int c_len = L->boundary;
     const int win_len = L->write_pos - c_len;
@@ -214,6 +232,88 @@ int khq_layer_step(khq_layer* L, const void* q_gate, const void* k_roped, const 
     rc = launch_khq_merge_gate_fp16(has_c ? L->ac : L->aw, L->aw, q_gate, out, L->H_q, kD,
                                     has_c && has_w, stream);
     return rc ? rc : 1;
+}
+
+int khq_layer_prefill(khq_layer* L, const void* q_gate, const void* k_roped, const void* v,
+                      const void* k_unroped, void* out, int n, float scale, hipStream_t stream) {
+    if (!L || !q_gate || !k_roped || !v || !k_unroped || !out || n <= 0) return -100;
+    const int kv = L->H_kv * kD;
+    if (!L->dk) {  // dense key space for up to cap + 256 positions
+        L->d_keys = L->cap + kRing + 64;
+        L->d_ld = (L->d_keys + 63) / 64 * 64;
+        const size_t kb = (size_t)L->d_keys * kv * sizeof(__half);
+        const size_t vb = (size_t)L->H_kv * kD * L->d_ld * sizeof(__half);
+        if (hipMalloc(reinterpret_cast<void**>(&L->dk), kb) != hipSuccess ||
+            hipMalloc(reinterpret_cast<void**>(&L->dvt), vb) != hipSuccess) {
+            if (L->dk) (void)hipFree(L->dk);
+            L->dk = nullptr;
+            L->dvt = nullptr;
+            return -100;
+        }
+        L->dec_hi = 0;
+    }
+    const __half* qg = static_cast<const __half*>(q_gate);
+    const __half* kr = static_cast<const __half*>(k_roped);
+    const __half* vv = static_cast<const __half*>(v);
+    const __half* ku = static_cast<const __half*>(k_unroped);
+    __half* o = static_cast<__half*>(out);
+    int done = 0;
+    while (done < n) {
+        // Sub-chunk whose ring writes overwrite no slot that any of its
+        // queries or compression events still reads.
+        const int m = std::min(n - done, kRing - (L->write_pos - L->boundary));
+        if (m <= 0) return -102;
+        const int w0 = L->write_pos;
+        hipError_t e = khq::launch_ring_write_n(L->ring_k, L->ring_v, L->ring_u, kr + (size_t)done * kv,
+                                                vv + (size_t)done * kv, ku + (size_t)done * kv, kv,
+                                                w0 % kRing, m, kRing, stream);
+        if (e != hipSuccess) return (int)e;
+        int j = 0;
+        while (j < m) {
+            // query j appends position w0 + j; an event fires before its attention
+            if (event_due(L, w0 + j + 1)) {
+                const int rc = compress_event(L, stream);
+                if (rc) return rc;
+            }
+            int je = j + 1;
+            while (je < m && !event_due(L, w0 + je + 1)) je++;
+            // queries j .. je - 1 share c_len = boundary
+            const int c_len = L->boundary;
+            const int n_k = w0 + je;
+            if (n_k - c_len > kRing) return -102;
+            if (L->dec_hi < c_len) {
+                const int rc = khq_decompress_fp16(
+                    L->kpay, L->vpay, L->vsm, L->kmask, L->knorm, L->krn, L->vnorm, L->vrn,
+                    L->cents_k, L->cents_v, L->vq, L->rotor_k, L->rotor_v, L->d_k, L->d_v, L->H_kv,
+                    L->dec_hi, c_len - L->dec_hi, 0, L->alpha_k, L->alpha_v, L->rope_base, L->dk,
+                    L->dec_hi, L->dvt, L->d_ld, stream);
+                if (rc) return rc;
+                L->dec_hi = c_len;
+            }
+            khq::GatherArgs g{};
+            g.ring_k = L->ring_k;
+            g.ring_v = L->ring_v;
+            g.out_k = L->dk;
+            g.out_vt = L->dvt;
+            g.h_kv = L->H_kv;
+            g.win_start = c_len % kRing;
+            g.n = n_k - c_len;
+            g.ring_cap = kRing;
+            g.key0 = c_len;
+            g.ld_vt = L->d_ld;
+            e = khq::launch_ring_gather(g, stream);
+            if (e != hipSuccess) return (int)e;
+            const int rc = khq_prefill_attn_fp16(qg + (size_t)(done + j) * L->H_q * 2 * kD, L->dk,
+                                                 L->dvt, L->d_ld, n_k, je - j, w0 + j + 1, L->H_q,
+                                                 L->H_kv, scale,
+                                                 o + (size_t)(done + j) * L->H_q * kD, stream);
+            if (rc) return rc;
+            j = je;
+        }
+        L->write_pos = w0 + m;
+        done += m;
+    }
+    return n;
 }
 
 }  // extern "C"

@@ -1,0 +1,397 @@
+// khq_prefill.hip -- chunked prefill on matrix cores: many query tokens of one
+// layer attend to the compressed prefix and the raw ring window at once.
+//
+// Three kernels build one dense fp16 key space (key index = token position)
+// and attend over it causally:
+//   decompress_kernel   compressed rows -> roped K rows [key][H_kv][256] and
+//                       V^T [H_kv][256][ld] (the decode of the compressed-
+//                       region attention kernel, ref:src/csrc/
+//                       qmv_sm75_kernel.cu:1608-1699 for K and :1739-1762,
+//                       1776-1826 for V, applied per token instead of being
+//                       folded into the running sums);
+//   ring_gather_kernel  raw ring slots -> the same K rows / V^T columns;
+//   prefill_attn_kernel S^T = K Q^T and O^T = V^T P^T on MFMA (fp16 in, fp32
+//                       accumulate), online softmax, one split of the keys per
+//                       block, partial triples merged and gated by
+//                       combine_gate_kernel.
+// Query j of a launch sees keys [0, vis0 + j): the sequential step semantics
+// (its own position included) when keys are positions.
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "khq_internal.h"
+#include "khq_mfma_util.h"
+
+namespace khq {
+namespace pf {
+
+using namespace mu;
+
+constexpr int TOK_BLK = 64;   // tokens per decompress / gather block
+constexpr int VT_PAD = 8;     // halves of padding per LDS V^T row
+
+__device__ __forceinline__ uint32_t rd32(const uint8_t* p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+// Writes the block's LDS V^T tile sv[256][TOK_BLK + VT_PAD] to vt columns
+// key0 .. key0 + TOK_BLK - 1 of KV head h (all 64 columns: the caller's
+// buffer is padded to a multiple of 64 keys).
+__device__ __forceinline__ void store_vt(const _Float16 (*sv)[TOK_BLK + VT_PAD], __half* vt, int ld,
+                                         int h, int key0) {
+    for (int i = threadIdx.x; i < 256 * (TOK_BLK / 8); i += blockDim.x) {
+        const int d = i >> 3, part = i & 7;
+        const uint4 v = *reinterpret_cast<const uint4*>(&sv[d][part * 8]);
+        *reinterpret_cast<uint4*>(vt + ((size_t)h * 256 + d) * ld + key0 + part * 8) = v;
+    }
+}
+
+// ------------------------------------------------------------- decompress
+// Block (64 tokens, KV head h), 4 wavefronts of 16 tokens each; lane p owns
+// patch p = dims 4 p .. 4 p + 3.
+__global__ __launch_bounds__(256) void decompress_kernel(DecompArgs a) {
+    __shared__ __align__(16) _Float16 sv[256][TOK_BLK + VT_PAD];
+    const int h = blockIdx.y;
+    const int wv = threadIdx.x >> 6, p = threadIdx.x & 63;
+    const int t_blk = blockIdx.x * TOK_BLK;
+    // per-lane constants
+    float cbk[4], ldk[4], ldv[4], rk[16], rv[16];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        cbk[c] = __half2float(a.cents_k[512 + 4 * p + c]);
+        ldk[c] = (1.0f / 256.0f) / (__half2float(a.dk[4 * p + c]) + 1e-8f);
+        ldv[c] = (1.0f / 16.0f) / (__half2float(a.dv[4 * p + c]) + 1e-8f);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        rk[i] = __half2float(a.rotor_k[p * 16 + i]);
+        rv[i] = __half2float(a.rotor_v[p * 16 + i]);
+    }
+    const float cv0 = __half2float(a.cents_v[4 * p + 3]) * a.a_v;
+    const float cv1 = __half2float(a.cents_v[256 + 4 * p + 3]) * a.a_v;
+    // RoPE frequencies of dims 4 (p & 7) + c (lanes 0..15 rotate dims 0..63)
+    float fr[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) fr[c] = powf(a.rope_base, -2.0f * (float)(4 * (p & 7) + c) / 64.0f);
+    const uint64_t below = (p == 0) ? 0ull : (~0ull >> (64 - p));
+
+    for (int i = 0; i < 16; i++) {
+        const int tl = wv * 16 + i;  // token within the block
+        const int tok = t_blk + tl;
+        if (tok >= a.n_tok) {        // uniform per wavefront
+#pragma unroll
+            for (int c = 0; c < 4; c++) sv[4 * p + c][tl] = (_Float16)0.0f;
+            continue;
+        }
+        const size_t g = (size_t)(a.tok0 + tok) * a.h_kv + h;
+        // ---- K: codes, outlier ordinals (ballot prefix), values
+        const uint32_t mw = a.kmask[g * 16 + (p >> 2)];
+        const uint8_t* kb = a.kpay + g * 40;
+        const float nk = __half2float(a.knorm[g]);
+        const float rs = __half2float(a.krn[g]);
+        float mult = (float)rd32(kb) / 1000.0f;
+        if (mult < 0.1f || mult > 10.0f || isnan(mult)) mult = 1.0f;
+        uint32_t code[4];
+        int own = 0, ord = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            code[k] = (mw >> (2 * (4 * (p & 3) + k))) & 3u;
+            const uint64_t b = __ballot(code[k] == 3u);
+            ord += __popcll(b & below);
+        }
+        float kf[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float cbase = cbk[k] * mult;
+            float kv = 0.0f;
+            if (code[k] == 3u) {
+                const int jo = ord + own;
+                const float sign = (jo < 50 && ((kb[29 + jo / 8] >> (jo % 8)) & 1)) ? 1.0f : -1.0f;
+                const float r4 = (jo < 50) ? (float)((kb[4 + jo / 2] >> ((jo % 2) * 4)) & 0xF) : 0.0f;
+                kv = sign * fmaf(r4, rs, cbase);
+                own++;
+            } else if (code[k] == 2u) {
+                kv = cbase;
+            } else if (code[k] == 1u) {
+                kv = -cbase;
+            }
+            kf[k] = kv * a.a_k * nk;
+        }
+        float y[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float s = kf[0] * rk[c * 4 + 0];
+            s = fmaf(kf[1], rk[c * 4 + 1], s);
+            s = fmaf(kf[2], rk[c * 4 + 2], s);
+            s = fmaf(kf[3], rk[c * 4 + 3], s);
+            y[c] = s;
+        }
+        fwht256(y, p);
+#pragma unroll
+        for (int c = 0; c < 4; c++) y[c] *= ldk[c];
+        // RoPE on dims 0..63: lane p < 8 holds dim i, lane p + 8 dim i + 32
+        {
+            float xo[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) xo[c] = __shfl_xor(y[c], 8, 64);
+            if (p < 16) {
+                const float pos = (float)(a.start_pos + a.tok0 + tok);
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    float cs, sn;
+                    sincos_rev(pos * fr[c], cs, sn);
+                    y[c] = p < 8 ? fmaf(y[c], cs, -(xo[c] * sn)) : fmaf(xo[c], sn, y[c] * cs);
+                }
+            }
+        }
+        *reinterpret_cast<uint2*>(a.out_k + ((size_t)(a.key0 + tok) * a.h_kv + h) * 256 + 4 * p) =
+            uint2{pk_rne(y[0], y[1]), pk_rne(y[2], y[3])};
+        // ---- V: patch fields, codebook, dim 3, inverse rotor, FWHT
+        const uint8_t* vp = a.vpay + g * 104;
+        const float nv = __half2float(a.vnorm[g]);
+        const float ec = __half2float(a.vrn[g]);
+        const float smv = __uint_as_float(rd32(a.vsm + g * 4));
+        const uint32_t grp = (uint32_t)p / 8, sub = (uint32_t)p % 8;
+        const uint64_t w0 = rd32(vp + (grp * 3 + 0) * 4), w1 = rd32(vp + (grp * 3 + 1) * 4),
+                       w2 = rd32(vp + (grp * 3 + 2) * 4);
+        const uint64_t low64 = (w1 << 32) | w0, high64 = (w2 << 32) | w1;
+        const uint32_t pvl = (sub < 4) ? (uint32_t)((low64 >> (sub * 12)) & 0xFFF)
+                                       : (uint32_t)((high64 >> ((sub - 4) * 12 + 16)) & 0xFFF);
+        const uint32_t hb = (p < 32) ? ((rd32(vp + 96) >> p) & 1u) : ((rd32(vp + 100) >> (p - 32)) & 1u);
+        const uint32_t vc = (pvl & 0x7Fu) | (hb << 7);
+        const float pre_v = (a.a_v * nv) * ec;
+        const float pre_r = smv * nv;
+        float vv[4];
+#pragma unroll
+        for (int k = 0; k < 3; k++) vv[k] = __half2float(a.vq[(size_t)p * 768 + vc * 3 + k]) * pre_v;
+        vv[3] = fmaf(((float)((pvl >> 8) & 0xFu) - 8.0f) / 7.0f, pre_r, (((pvl >> 7) & 1u) ? cv1 : cv0) * nv);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float s = vv[0] * rv[c * 4 + 0];
+            s = fmaf(vv[1], rv[c * 4 + 1], s);
+            s = fmaf(vv[2], rv[c * 4 + 2], s);
+            s = fmaf(vv[3], rv[c * 4 + 3], s);
+            y[c] = s;
+        }
+        fwht256(y, p);
+#pragma unroll
+        for (int c = 0; c < 4; c++) sv[4 * p + c][tl] = (_Float16)(y[c] * ldv[c]);
+    }
+    __syncthreads();
+    store_vt(sv, a.out_vt, a.ld_vt, h, a.key0 + t_blk);
+}
+
+// ------------------------------------------------------------ ring gather
+// Block (64 keys, KV head h): K rows copied, V rows transposed through LDS.
+__global__ __launch_bounds__(256) void ring_gather_kernel(GatherArgs a) {
+    __shared__ __align__(16) _Float16 sv[256][TOK_BLK + VT_PAD];
+    const int h = blockIdx.y;
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t_blk = blockIdx.x * TOK_BLK;
+    for (int i = 0; i < 16; i++) {
+        const int tl = wv * 16 + i;
+        const int t = t_blk + tl;
+        if (t >= a.n) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) sv[4 * lane + c][tl] = (_Float16)0.0f;
+            continue;
+        }
+        int slot = a.win_start + t;
+        slot = slot >= a.ring_cap ? slot - a.ring_cap : slot;
+        const size_t src = ((size_t)slot * a.h_kv + h) * 256 + 4 * lane;
+        *reinterpret_cast<uint2*>(a.out_k + ((size_t)(a.key0 + t) * a.h_kv + h) * 256 + 4 * lane) =
+            *reinterpret_cast<const uint2*>(a.ring_k + src);
+        const h4 v = __builtin_bit_cast(h4, *reinterpret_cast<const uint2*>(a.ring_v + src));
+#pragma unroll
+        for (int c = 0; c < 4; c++) sv[4 * lane + c][tl] = v[c];
+    }
+    __syncthreads();
+    store_vt(sv, a.out_vt, a.ld_vt, h, a.key0 + t_blk);
+}
+
+// ----------------------------------------------------------- attention
+// Block = 4 wavefronts = 4 tiles of 16 query rows of one KV head, one key
+// split.  Row r of KV head h is (query j = r / n_rep, head h n_rep + r % n_rep).
+// Per 16-key tile and wavefront: S^T (16 keys x 16 rows) = 8 MFMA 16x16x32
+// with A = K rows, B = Q^T (registers); P^T stays in the C layout, which is
+// the B layout of O^T (256 dims x 16 rows) = 16 MFMA 16x16x16 with A = V^T.
+__global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
+    const int h = blockIdx.y;
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int li = lane & 15, lg = lane >> 4;
+    const int n_rows = a.n_q * a.n_rep;
+    const int row0 = (blockIdx.x * 4 + wv) * 16;
+    const int split = blockIdx.z;
+    const int k_lo = split * a.keys_per_split;
+    const int k_hi = min(a.n_k, k_lo + a.keys_per_split);
+    const int H_q = a.h_kv * a.n_rep;
+    // this lane's row (li) and its visible key count
+    const int r = row0 + li;
+    const bool r_ok = r < n_rows;
+    const int jq = r_ok ? r / a.n_rep : 0;
+    const int hq = h * a.n_rep + (r_ok ? r % a.n_rep : 0);
+    const int vis = r_ok ? min(a.n_k, a.vis0 + jq) : 0;
+    // wavefront's last visible key (rows are ordered by query)
+    const int r_last = min(row0 + 15, n_rows - 1);
+    const int vis_last = (row0 < n_rows) ? min(a.n_k, a.vis0 + r_last / a.n_rep) : 0;
+    const int kt_hi = min(k_hi, vis_last);
+
+    // Q^T B operands: lane (row li, lg) holds dims 32 st + 8 lg .. + 7
+    h8 qb[8];
+    {
+        const __half* qrow = a.q + ((size_t)jq * H_q + hq) * 512;
+#pragma unroll
+        for (int st = 0; st < 8; st++) {
+            const uint4 v = *reinterpret_cast<const uint4*>(qrow + 32 * st + 8 * lg);
+            qb[st] = __builtin_bit_cast(h8, r_ok ? v : uint4{0u, 0u, 0u, 0u});
+        }
+    }
+    f4 acc[16];
+#pragma unroll
+    for (int m = 0; m < 16; m++) acc[m] = f4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    const __half* kbase = a.k + (size_t)h * 256 + 32 * 0 + 8 * lg;
+    const __half* vtb = a.vt + (size_t)h * 256 * a.ld_vt;
+    auto load_tile = [&](int k0, uint4 (&kr)[8], uint2 (&vr)[16]) {
+        const int key = min(k0 + li, a.n_k - 1);
+        const __half* krow = kbase + (size_t)key * a.h_kv * 256;
+#pragma unroll
+        for (int st = 0; st < 8; st++) kr[st] = *reinterpret_cast<const uint4*>(krow + 32 * st);
+#pragma unroll
+        for (int mt = 0; mt < 16; mt++)
+            vr[mt] = *reinterpret_cast<const uint2*>(vtb + (size_t)(16 * mt + li) * a.ld_vt + k0 + 4 * lg);
+    };
+    auto compute_tile = [&](int k0, const uint4 (&kr)[8], const uint2 (&vr)[16]) {
+        f4 s = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < 8; st++) s = mfma32(__builtin_bit_cast(h8, kr[st]), qb[st], s);
+        // s[c] = score of key k0 + 4 lg + c for row li
+        float sc[4];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int key = k0 + 4 * lg + c;
+            sc[c] = key < vis ? s[c] * a.sc : -INFINITY;
+            tmax = fmaxf(tmax, sc[c]);
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float m_new = fmaxf(m_run, tmax);
+        const float fac = (m_new == -INFINITY) ? 1.0f : __expf(m_run - m_new);
+        float pv[4], psum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            pv[c] = (sc[c] == -INFINITY) ? 0.0f : __expf(sc[c] - m_new);
+            psum += pv[c];
+        }
+        psum += __shfl_xor(psum, 16, 64);
+        psum += __shfl_xor(psum, 32, 64);
+        l_run = fmaf(l_run, fac, psum);
+        m_run = m_new;
+        if (__ballot(fac != 1.0f) != 0ull) {
+#pragma unroll
+            for (int m = 0; m < 16; m++) acc[m] *= fac;
+        }
+        const h4 pb = __builtin_bit_cast(h4, uint2{pk_rne(pv[0], pv[1]), pk_rne(pv[2], pv[3])});
+        // keys past n_k: V^T columns are padding, zero them
+        const int kv_ok = a.n_k - (k0 + 4 * lg);  // valid keys among this lane's 4
+#pragma unroll
+        for (int mt = 0; mt < 16; mt++) {
+            uint2 v = vr[mt];
+            if (kv_ok < 4) {
+                v.x = kv_ok <= 0 ? 0u : (kv_ok == 1 ? (v.x & 0xFFFFu) : v.x);
+                v.y = kv_ok <= 2 ? 0u : (v.y & 0xFFFFu);
+            }
+            acc[mt] = mfma16(__builtin_bit_cast(h4, v), pb, acc[mt]);
+        }
+    };
+    if (k_lo < kt_hi) {
+        uint4 kA[8], kB[8];
+        uint2 vA[16], vB[16];
+        load_tile(k_lo, kA, vA);
+        for (int k0 = k_lo; k0 < kt_hi; k0 += 32) {
+            const bool has_b = k0 + 16 < kt_hi;
+            if (has_b) load_tile(k0 + 16, kB, vB);
+            compute_tile(k0, kA, vA);
+            if (k0 + 32 < kt_hi) load_tile(k0 + 32, kA, vA);
+            if (has_b) compute_tile(k0 + 16, kB, vB);
+        }
+    }
+    // ---- partial triple of row li (dims 16 mt + 4 lg + c)
+    if (r_ok) {
+        float* out = a.part + ((size_t)(jq * H_q + hq) * a.n_split + split) * 258;
+        const bool empty = (m_run == -INFINITY);
+#pragma unroll
+        for (int mt = 0; mt < 16; mt++)
+            *reinterpret_cast<f4*>(&out[16 * mt + 4 * lg]) = empty ? f4{0.f, 0.f, 0.f, 0.f} : acc[mt];
+        if (lg == 0) {
+            out[256] = empty ? -1e20f : m_run;
+            out[257] = empty ? 0.0f : l_run;
+        }
+    }
+}
+
+__global__ void ring_write_n_kernel(__half* __restrict__ rk, __half* __restrict__ rv,
+                                    __half* __restrict__ ru, const __half* __restrict__ k,
+                                    const __half* __restrict__ v, const __half* __restrict__ ku,
+                                    int kv, int slot0, int ring_cap) {
+    const int t = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= kv) return;
+    int slot = slot0 + t;
+    slot = slot % ring_cap;
+    const size_t src = (size_t)t * kv + i, dst = (size_t)slot * kv + i;
+    if (rk) rk[dst] = k[src];
+    if (rv) rv[dst] = v[src];
+    if (ru) ru[dst] = ku[src];
+}
+
+}  // namespace pf
+
+hipError_t launch_ring_write_n(__half* rk, __half* rv, __half* ru, const __half* k,
+                               const __half* v, const __half* ku, int kv, int slot0, int n,
+                               int ring_cap, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(pf::ring_write_n_kernel, dim3((kv + 255) / 256, n), dim3(256), 0, st, rk, rv,
+                       ru, k, v, ku, kv, slot0, ring_cap);
+    return hipGetLastError();
+}
+
+hipError_t launch_decompress(const DecompArgs& a, hipStream_t st) {
+    if (a.n_tok <= 0) return hipSuccess;
+    hipLaunchKernelGGL(pf::decompress_kernel, dim3((a.n_tok + pf::TOK_BLK - 1) / pf::TOK_BLK, a.h_kv),
+                       dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_ring_gather(const GatherArgs& a, hipStream_t st) {
+    if (a.n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(pf::ring_gather_kernel, dim3((a.n + pf::TOK_BLK - 1) / pf::TOK_BLK, a.h_kv),
+                       dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+int prefill_splits(int n_q, int n_rep, int h_kv, int n_k, int* keys_per_split) {
+    const int mtiles = (n_q * n_rep + 15) / 16;
+    const int blocks = (mtiles + 3) / 4 * h_kv;
+    int ns = (1024 + blocks - 1) / blocks;  // ~4 wavefronts per SIMD of the chip
+    ns = std::max(1, std::min(ns, 64));
+    int per = (n_k + ns - 1) / ns;
+    per = (per + 31) / 32 * 32;
+    ns = (n_k + per - 1) / per;
+    *keys_per_split = per;
+    return std::max(ns, 1);
+}
+
+hipError_t launch_prefill_attn(const PrefillArgs& a, hipStream_t st) {
+    const int mtiles = (a.n_q * a.n_rep + 15) / 16;
+    hipLaunchKernelGGL(pf::prefill_attn_kernel, dim3((mtiles + 3) / 4, a.h_kv, a.n_split), dim3(256),
+                       0, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace khq

@@ -32,6 +32,8 @@ SIGNATURES = {
     "launch_khq_gqa_attn_fp16": [P] * 4 + [I, I, I, I, F, P],
     "khq_attn_step_fp16": [P] * 19 + [I, I, I, I, I, I, F, F, F, F, P],
     "khq_attn_step_batched_fp16": [P, I] + [P] * 7 + [I, I, F, F, F, F, P],
+    "khq_decompress_fp16": [P] * 15 + [I, I, I, I, F, F, F, P, I, P, I, P],
+    "khq_prefill_attn_fp16": [P, P, P, I, I, I, I, I, I, F, P, P],
     "khq_attn_partials_fp16": [P] * 16 + [I, I, I, F, F, F, F, P],
     "khq_attn_parts": [I],
     "khq_select_kernel": [I],
@@ -44,6 +46,7 @@ SIGNATURES = {
     "khq_layer_payload": [P, P],
     "khq_layer_capture_unroped": [P, P, P],
     "khq_layer_step": [P] * 6 + [F, P],
+    "khq_layer_prefill": [P] * 6 + [I, F, P],
 }
 # return types other than int
 RESTYPES = {"khq_layer_create": ctypes.c_void_p, "khq_layer_destroy": None}

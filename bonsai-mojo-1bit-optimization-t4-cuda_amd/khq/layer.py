@@ -299,6 +299,26 @@ class NativeKhqLayer:
             raise KhqError("khq_layer_step", rc)
         return rc == 1
 
+    def prefill(self, q_gate, k_roped, v, k_unroped, out, scale: float) -> int:
+        """khq_layer_prefill: n tokens at once (q_gate f16 [n][H_q][512], k_roped /
+        v / k_unroped f16 [n][H_kv][256], out f16 [n][H_q][256]), the results of
+        n steps."""
+        from ._lib import KhqError, stream_handle
+
+        n = q_gate.shape[0]
+        ops._need(q_gate, torch.float16, n * self.H_q * 2 * D, "q_gate")
+        for name, t in (("k_roped", k_roped), ("v", v), ("k_unroped", k_unroped)):
+            ops._need(t, torch.float16, n * self.H_kv * D, name)
+        ops._need(out, torch.float16, n * self.H_q * D, "out")
+        rc = self._lib.khq_layer_prefill(self.handle, ops.ptr(q_gate), ops.ptr(k_roped),
+                                         ops.ptr(v), ops.ptr(k_unroped), ops.ptr(out), n, scale,
+                                         stream_handle())
+        if rc == -102:
+            raise RuntimeError("KHQ prefill: raw window would exceed the 256-slot ring")
+        if rc != n:
+            raise KhqError("khq_layer_prefill", rc)
+        return rc
+
 
 class KhqRuntime:
     """khq_activate / khq_init: loads a KHQK v2 file and creates the layers

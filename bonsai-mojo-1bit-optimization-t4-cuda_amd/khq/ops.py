@@ -211,6 +211,40 @@ def attn_step_batched(seqs, cents: Centroids, *, H_q: int, H_kv: int, scale: flo
                 rope_base, stream_handle(stream), check=check)
 
 
+def vt_ld(n_keys: int) -> int:
+    """Leading dimension of a V^T buffer for keys [0, n_keys) (padded to 64)."""
+    return (n_keys + 63) // 64 * 64
+
+
+def decompress(pay: Payload, cents: Centroids, out_k, out_vt, *, H_kv: int, tok0: int,
+               n_tok: int, key0: int, ld_vt: int, start_pos: int = 0, rope_base: float = 1e7,
+               check: bool = True, stream=None) -> int:
+    """khq_decompress_fp16: tokens [tok0, tok0 + n_tok) -> roped K rows
+    out_k f16 [keys][H_kv][256] at key0.. and V^T out_vt f16 [H_kv][256][ld_vt]."""
+    if (tok0 + n_tok) * H_kv > pay.rows:
+        raise ValueError("tokens exceed payload rows")
+    _need(out_k, torch.float16, (key0 + n_tok) * H_kv * D, "out_k")
+    _need(out_vt, torch.float16, H_kv * D * ld_vt, "out_vt")
+    return call("khq_decompress_fp16", ptr(pay.kpay), ptr(pay.vpay), ptr(pay.vsm), ptr(pay.kmask),
+                ptr(pay.knorm), ptr(pay.krn), ptr(pay.vnorm), ptr(pay.vrn), ptr(cents.cents_k),
+                ptr(cents.cents_v), ptr(cents.vq), ptr(cents.rotor_k), ptr(cents.rotor_v),
+                ptr(cents.d_k), ptr(cents.d_v), H_kv, tok0, n_tok, start_pos, cents.alpha_k,
+                cents.alpha_v, rope_base, ptr(out_k), key0, ptr(out_vt), ld_vt,
+                stream_handle(stream), check=check)
+
+
+def prefill_attn(q_gate, k, vt, out, *, ld_vt: int, n_k: int, n_q: int, vis0: int, H_q: int,
+                 H_kv: int, scale: float, check: bool = True, stream=None) -> int:
+    """khq_prefill_attn_fp16: n_q queries (q_gate f16 [n_q][H_q][512]) over
+    dense keys; query j sees keys [0, vis0 + j); out f16 [n_q][H_q][256] gated."""
+    _need(q_gate, torch.float16, n_q * H_q * 2 * D, "q_gate")
+    _need(k, torch.float16, n_k * H_kv * D, "k")
+    _need(vt, torch.float16, H_kv * D * ld_vt, "vt")
+    _need(out, torch.float16, n_q * H_q * D, "out")
+    return call("khq_prefill_attn_fp16", ptr(q_gate), ptr(k), ptr(vt), ld_vt, n_k, n_q, vis0,
+                H_q, H_kv, scale, ptr(out), stream_handle(stream), check=check)
+
+
 def attn_partials(q_gate, pay: Payload, cents: Centroids, *, H_q: int, H_kv: int, c_len: int,
                   scale: float, rope_base: float = 1e7, stream=None) -> int:
     """khq_attn_partials_fp16: the compressed-region kernel alone (profiling)."""

@@ -147,6 +147,31 @@ typedef struct khq_seq {
     void* out;           /* f16 [H_q][256] */
     int c_len, win_start, win_len, ring_cap;
 } khq_seq;
+/* Decode of compressed rows to dense fp16 (counterpart of the reference's
+ * calibration decoders cal_decompress_k / cal_decompress_v,
+ * ref:src/csrc/qmv_sm75_kernel.cu:2722-3024, with the attention kernel's
+ * decode and RoPE, :1608-1699, :1739-1762, :1776-1826): tokens [tok0, tok0 +
+ * n_tok) of every KV head -> out_k f16 [key0 + t][H_kv][256] (roped at
+ * position start_pos + tok0 + t) and out_vt f16 [H_kv][256][ld_vt] columns
+ * key0 + t.  ld_vt: multiple of 8, >= key0 + n_tok rounded up to 64. */
+int khq_decompress_fp16(const void* k_payload, const void* v_payload, const void* v_shared_meta,
+                        const void* k_mask, const void* k_norms, const void* k_r_norms,
+                        const void* v_norms, const void* v_r_norms, const void* centroids_k,
+                        const void* centroids_v, const void* vq_centroids, const void* k_rotor,
+                        const void* v_rotor, const void* d_vec_k, const void* d_vec_v, int H_kv,
+                        int tok0, int n_tok, int start_pos, float alpha_k, float alpha_v,
+                        float rope_base, void* out_k, int key0, void* out_vt, int ld_vt,
+                        hipStream_t stream);
+/* Causal attention of n_q query tokens over dense fp16 keys (no reference
+ * counterpart; the multi-query form of khq_attn_step_fp16's two regions):
+ * k f16 [n_k][H_kv][256], vt f16 [H_kv][256][ld_vt]; query j (q_gate row j,
+ * f16 [n_q][H_q][512]) sees keys [0, min(n_k, vis0 + j)).  out f16
+ * [n_q][H_q][256] = softmax-weighted V / (den + 1e-8) * sigmoid(gate), the
+ * merge_gate convention. */
+int khq_prefill_attn_fp16(const void* q_gate, const void* k, const void* vt, int ld_vt, int n_k,
+                          int n_q, int vis0, int H_q, int H_kv, float scale, void* out,
+                          hipStream_t stream);
+
 int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centroids_k,
                                const void* centroids_v, const void* vq_centroids,
                                const void* k_rotor, const void* v_rotor, const void* d_vec_k,
@@ -216,6 +241,16 @@ int khq_layer_capture_unroped(khq_layer* layer, const void* k_unroped, hipStream
  * raw window would exceed the ring (capacity reached), else an error code. */
 int khq_layer_step(khq_layer* layer, const void* q_gate, const void* k_roped, const void* v,
                    const void* k_unroped, void* out, float scale, hipStream_t stream);
+/* Chunked prefill of n tokens (no reference counterpart: the reference
+ * prefills through n calls of khq_step, ref runtime.mojo:454-613, and this
+ * reproduces those steps' results).  q_gate f16 [n][H_q][512], k_roped / v /
+ * k_unroped f16 [n][H_kv][256], out f16 [n][H_q][256].  Token i is appended,
+ * any compression event fires, and query i attends to the compressed prefix
+ * and its raw window, as in step i; queries between events share one launch
+ * (dense fp16 keys decoded from the compressed rows, MFMA attention).
+ * Returns n, -100 on bad arguments, -102 at capacity, else an error code. */
+int khq_layer_prefill(khq_layer* layer, const void* q_gate, const void* k_roped, const void* v,
+                      const void* k_unroped, void* out, int n, float scale, hipStream_t stream);
 
 #ifdef __cplusplus
 }
