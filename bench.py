@@ -54,9 +54,10 @@ def parse():
                     help="payload: seeded uniform-random packed codes with outlier counts "
                          "~U[0,50] (the config's data, default) or the library's compression "
                          "of N(0,1) K/V rows")
-    ap.add_argument("--config", choices=["c3", "c4"], default="c3",
+    ap.add_argument("--config", choices=["c3", "c4", "c5"], default="c3",
                     help="c3: the headline 32K-context step (default); c4: 32 ragged "
-                         "sequences per layer-step in one batched call")
+                         "sequences per layer-step in one batched call; c5: a 128-token "
+                         "chunked-prefill step after 8,192 tokens")
     ap.add_argument("--counters-run", action="store_true",
                     help="profiling aid for rocprofv3 --pmc: a 256 MiB device copy (the "
                          "calibration kernel of known size), then the compressed-region kernel "
@@ -78,6 +79,8 @@ def main():
     _lib.call("khq_select_kernel", ["auto", "portable", "mfma-single"].index(args.kernel))
     if args.config == "c4":
         return bench_c4(args)
+    if args.config == "c5":
+        return bench_c5(args)
     if args.counters_run:
         return counters_run(args)
     from khq.centroids import synthetic_layer
@@ -270,6 +273,125 @@ def counters_run(args):
             ops.attn_partials(q, pay, cents, H_q=H_Q, H_kv=H_KV, c_len=c_len, scale=1.0 / 16.0)
     torch.cuda.synchronize()
     print("counters run done", file=sys.stderr)
+
+
+def bench_c5(args):
+    """Config 5: per layer, 8,192 tokens already appended (boundary 8,064),
+    then one chunk of 128 tokens at positions 8,192..8,319 through
+    khq_layer_prefill: ring writes, the compression event at the 128th append,
+    decode of the newly compressed rows, MFMA attention of 127 queries over
+    8,064 compressed + 129..255 raw tokens and of the last query over 8,192 +
+    128.  Each timed step runs the chunk on 16 fresh layer states (one per
+    layer); the dense attention kernel is also timed alone (MFMA roofline)."""
+    import numpy as np
+    import torch
+
+    from khq import layer as KL
+    from khq import ops, synth
+    from khq.centroids import synthetic_layer
+
+    dev = "cuda"
+    n0, chunk, scale = 8192, 128, 1.0 / 16.0
+    n_layers = args.layers
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+
+    def toks(n):
+        k = torch.randn((n, H_KV, D), generator=g, device=dev).half()
+        pos = torch.arange(n, device=dev)
+        return k, synth.rope_halfsplit(k.float(), pos).half(), \
+            torch.randn((n, H_KV, D), generator=g, device=dev).half(), \
+            torch.randn((n, H_Q, 2 * D), generator=g, device=dev).half()
+
+    k, kr, v, q = toks(n0 + chunk)
+    k_c, kr_c, v_c, q_c = (x[n0:].contiguous() for x in (k, kr, v, q))
+    opt = KL.KhqOptions(splits=16, fused=True)
+    scratch = torch.empty((chunk, H_Q, D), device=dev, dtype=torch.float16)
+
+    def fresh_layers(n):
+        out = []
+        for l in range(n):
+            L = KL.NativeKhqLayer(synthetic_layer(l % 16, seed=1234), H_q=H_Q, H_kv=H_KV,
+                                  cap=n0 + 256, device=dev, options=opt)
+            for i in range(0, n0, chunk):
+                L.prefill(q[i:i + chunk], kr[i:i + chunk], v[i:i + chunk], k[i:i + chunk],
+                          scratch, scale)
+            out.append(L)
+        torch.cuda.synchronize()
+        return out
+
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    out = torch.empty((chunk, H_Q, D), device=dev, dtype=torch.float16)
+    for _ in range(args.warmup):
+        for L in fresh_layers(n_layers):
+            L.prefill(q_c, kr_c, v_c, k_c, out, scale)
+    ms = []
+    n_steps = min(args.steps, 5)  # each step needs 16 freshly prefilled layer states
+    for _ in range(n_steps):
+        layers = fresh_layers(n_layers)
+        e0.record(stream)
+        for L in layers:
+            L.prefill(q_c, kr_c, v_c, k_c, out, scale)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1))
+        del layers
+    ms_step = float(np.mean(ms))
+    us_layer = ms_step * 1000.0 / n_layers
+    attended = sum((8064 + 129 + j) if j < 127 else 8192 + 128 for j in range(chunk))
+    flops = 2 * 2 * H_Q * D * attended
+    # the dense attention kernel alone: 127 queries over 8,064 + 255 keys
+    n_k, n_q = 8064 + 255, 127
+    ld = ops.vt_ld(n_k)
+    kd = torch.randn((n_k, H_KV, D), generator=g, device=dev).half()
+    vt = torch.randn((H_KV, D, ld), generator=g, device=dev).half()
+    qd = q_c[:n_q].contiguous()
+    od = torch.empty((n_q, H_Q, D), device=dev, dtype=torch.float16)
+    run = lambda: ops.prefill_attn(qd, kd, vt, od, ld_vt=ld, n_k=n_k, n_q=n_q, vis0=8064 + 129,
+                                   H_q=H_Q, H_kv=H_KV, scale=scale)
+    run()
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(20):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    attn_us = e0.elapsed_time(e1) * 1000.0 / 20
+    attn_flops = 2 * 2 * H_Q * D * sum(8064 + 129 + j for j in range(n_q))
+    result = {
+        "metric": "KHQ chunked-prefill us/layer-step (128 queries, 8K context) + MFMA TFLOP/s",
+        "value": round(us_layer, 3),
+        "unit": "us/layer-step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16-in/f32-acc",
+        "timed_steps": n_steps,
+        "data": "synthetic: N(0,1) fp16 tokens, compressed by the library",
+        "config": {
+            "workload": f"C5: {n_layers} layers x one 128-token chunk at positions 8192..8319 "
+                        "(compression event at the last append)",
+            "layers": n_layers, "chunk": chunk, "context": n0, "parallelism": "1 GPU",
+        },
+        "tflops_layer_step": round(flops / (us_layer * 1e-6) / 1e12, 2),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "prefill_attn_kernel (127 queries x 24 heads over 8,319 keys) + combine",
+            "achieved": round(attn_flops / (attn_us * 1e-6) / 1e12, 2),
+            "peak": 2500.0,
+            "unit": "TFLOP/s",
+            "frac": round(attn_flops / (attn_us * 1e-6) / 1e12 / 2500.0, 4),
+            "traffic": None,
+            "avg_kernel_us": round(attn_us, 3),
+            "flops_per_launch": attn_flops,
+        },
+    }
+    print(json.dumps(result), flush=True)
 
 
 def bench_c4(args):

@@ -215,12 +215,25 @@ __global__ __launch_bounds__(256) void ring_gather_kernel(GatherArgs a) {
 // ----------------------------------------------------------- attention
 // Block = 4 wavefronts = 4 tiles of 16 query rows of one KV head, one key
 // split.  Row r of KV head h is (query j = r / n_rep, head h n_rep + r % n_rep).
-// Per 16-key tile and wavefront: S^T (16 keys x 16 rows) = 8 MFMA 16x16x32
-// with A = K rows, B = Q^T (registers); P^T stays in the C layout, which is
-// the B layout of O^T (256 dims x 16 rows) = 16 MFMA 16x16x16 with A = V^T.
+// Per 16-key tile the block stages K (16 x 256) and V^T (256 x 16) in LDS
+// (double-buffered, one barrier per tile; the next tile's global loads are in
+// flight while this one is computed), then each wavefront computes
+//   S^T (16 keys x 16 rows) = 8 MFMA 16x16x32, A = K rows, B = Q^T (registers);
+//   O^T (256 dims x 16 rows) += 16 MFMA 16x16x16, A = V^T, B = P^T, which is
+//   the C layout of S^T (lane: row li, keys 4 lg .. 4 lg + 3).
+// Softmax: a per-row reference maximum shared by the row's 4 lanes, raised
+// (with a cross-lane reduction and a rescale) only when a score exceeds it by
+// more than 8, so weights stay <= e^8; row sums are per lane until the end.
+constexpr int KT = 16;            // keys per tile
+constexpr int KS_LD = 256 + 8;    // halves per LDS K row
+constexpr float GAP = 8.0f;
+
 __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
+    __shared__ __align__(16) _Float16 ks[2][KT][KS_LD];
+    __shared__ __align__(16) _Float16 vs[2][256][KT];
     const int h = blockIdx.y;
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int tid = threadIdx.x;
+    const int wv = tid >> 6, lane = tid & 63;
     const int li = lane & 15, lg = lane >> 4;
     const int n_rows = a.n_q * a.n_rep;
     const int row0 = (blockIdx.x * 4 + wv) * 16;
@@ -228,18 +241,15 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
     const int k_lo = split * a.keys_per_split;
     const int k_hi = min(a.n_k, k_lo + a.keys_per_split);
     const int H_q = a.h_kv * a.n_rep;
-    // this lane's row (li) and its visible key count
     const int r = row0 + li;
     const bool r_ok = r < n_rows;
     const int jq = r_ok ? r / a.n_rep : 0;
     const int hq = h * a.n_rep + (r_ok ? r % a.n_rep : 0);
     const int vis = r_ok ? min(a.n_k, a.vis0 + jq) : 0;
-    // wavefront's last visible key (rows are ordered by query)
-    const int r_last = min(row0 + 15, n_rows - 1);
-    const int vis_last = (row0 < n_rows) ? min(a.n_k, a.vis0 + r_last / a.n_rep) : 0;
-    const int kt_hi = min(k_hi, vis_last);
+    // the block's last visible key (rows are ordered by query)
+    const int b_last = min((int)blockIdx.x * 64 + 63, n_rows - 1);
+    const int kt_hi = min(k_hi, min(a.n_k, a.vis0 + b_last / a.n_rep));
 
-    // Q^T B operands: lane (row li, lg) holds dims 32 st + 8 lg .. + 7
     h8 qb[8];
     {
         const __half* qrow = a.q + ((size_t)jq * H_q + hq) * 512;
@@ -252,85 +262,109 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
     f4 acc[16];
 #pragma unroll
     for (int m = 0; m < 16; m++) acc[m] = f4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.0f;
+    float m_ref = -INFINITY, l_part = 0.0f;
 
-    const __half* kbase = a.k + (size_t)h * 256 + 32 * 0 + 8 * lg;
-    const __half* vtb = a.vt + (size_t)h * 256 * a.ld_vt;
-    auto load_tile = [&](int k0, uint4 (&kr)[8], uint2 (&vr)[16]) {
-        const int key = min(k0 + li, a.n_k - 1);
-        const __half* krow = kbase + (size_t)key * a.h_kv * 256;
-#pragma unroll
-        for (int st = 0; st < 8; st++) kr[st] = *reinterpret_cast<const uint4*>(krow + 32 * st);
-#pragma unroll
-        for (int mt = 0; mt < 16; mt++)
-            vr[mt] = *reinterpret_cast<const uint2*>(vtb + (size_t)(16 * mt + li) * a.ld_vt + k0 + 4 * lg);
+    // cooperative tile loads: thread t -> K key t / 16, 32 B at (t % 16) * 16
+    // halves; V^T dim t, the tile's 16 keys (32 B)
+    const int ld_key = tid >> 4, ld_off = (tid & 15) * 16;
+    const __half* kg = a.k + (size_t)h * 256 + ld_off;
+    const __half* vg = a.vt + ((size_t)h * 256 + tid) * a.ld_vt;
+    uint4 pk0 = uint4{0u, 0u, 0u, 0u}, pk1 = pk0, pv0 = pk0, pv1 = pk0;
+    auto gload = [&](int k0) {
+        const int key = min(k0 + ld_key, a.n_k - 1);
+        const uint4* ksrc = reinterpret_cast<const uint4*>(kg + (size_t)key * a.h_kv * 256);
+        pk0 = ksrc[0];
+        pk1 = ksrc[1];
+        const uint4* vsrc = reinterpret_cast<const uint4*>(vg + k0);
+        pv0 = vsrc[0];
+        pv1 = vsrc[1];
     };
-    auto compute_tile = [&](int k0, const uint4 (&kr)[8], const uint2 (&vr)[16]) {
+    // V^T word i of a tile row holds keys 2 i, 2 i + 1; columns past n_k are
+    // padding and become zero
+    auto vmask = [](uint32_t w, int i, int nv) {
+        return 2 * i + 1 < nv ? w : (2 * i < nv ? (w & 0xFFFFu) : 0u);
+    };
+    auto lstore = [&](int buf, int k0) {
+        *reinterpret_cast<uint4*>(&ks[buf][ld_key][ld_off]) = pk0;
+        *reinterpret_cast<uint4*>(&ks[buf][ld_key][ld_off + 8]) = pk1;
+        const int nv = a.n_k - k0;
+        uint4 v0 = pv0, v1 = pv1;
+        if (nv < KT) {
+            v0 = uint4{vmask(v0.x, 0, nv), vmask(v0.y, 1, nv), vmask(v0.z, 2, nv), vmask(v0.w, 3, nv)};
+            v1 = uint4{vmask(v1.x, 4, nv), vmask(v1.y, 5, nv), vmask(v1.z, 6, nv), vmask(v1.w, 7, nv)};
+        }
+        *reinterpret_cast<uint4*>(&vs[buf][tid][0]) = v0;
+        *reinterpret_cast<uint4*>(&vs[buf][tid][8]) = v1;
+    };
+
+    const int n_tiles = k_lo < kt_hi ? (kt_hi - k_lo + KT - 1) / KT : 0;
+    if (n_tiles > 0) {
+        gload(k_lo);
+        lstore(0, k_lo);
+        if (n_tiles > 1) gload(k_lo + KT);
+    }
+    __syncthreads();
+    for (int t = 0; t < n_tiles; t++) {
+        const int buf = t & 1;
+        const int k0 = k_lo + t * KT;
+        // ---- S^T from LDS
         f4 s = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int st = 0; st < 8; st++) s = mfma32(__builtin_bit_cast(h8, kr[st]), qb[st], s);
-        // s[c] = score of key k0 + 4 lg + c for row li
-        float sc[4];
-        float tmax = -INFINITY;
+        for (int st = 0; st < 8; st++) {
+            const h8 kop = *reinterpret_cast<const h8*>(&ks[buf][li][32 * st + 8 * lg]);
+            s = mfma32(kop, qb[st], s);
+        }
+        float sc[4], lmax = -INFINITY;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const int key = k0 + 4 * lg + c;
-            sc[c] = key < vis ? s[c] * a.sc : -INFINITY;
-            tmax = fmaxf(tmax, sc[c]);
+            sc[c] = (k0 + 4 * lg + c < vis) ? s[c] * a.sc : -INFINITY;
+            lmax = fmaxf(lmax, sc[c]);
         }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float m_new = fmaxf(m_run, tmax);
-        const float fac = (m_new == -INFINITY) ? 1.0f : __expf(m_run - m_new);
-        float pv[4], psum = 0.0f;
+        // ---- raise the row's reference maximum only when needed
+        if (__ballot(lmax > m_ref + GAP) != 0ull) {
+            float rmax = fmaxf(lmax, __shfl_xor(lmax, 16, 64));
+            rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+            const float m_new = fmaxf(m_ref, rmax);
+            if (m_new > m_ref) {
+                const float fac = __expf(m_ref - m_new);  // 0 when m_ref = -inf
+#pragma unroll
+                for (int m = 0; m < 16; m++) acc[m] *= fac;
+                l_part *= fac;
+                m_ref = m_new;
+            }
+        }
+        float p[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            pv[c] = (sc[c] == -INFINITY) ? 0.0f : __expf(sc[c] - m_new);
-            psum += pv[c];
+            p[c] = sc[c] == -INFINITY ? 0.0f : __expf(sc[c] - m_ref);
+            l_part += p[c];
         }
-        psum += __shfl_xor(psum, 16, 64);
-        psum += __shfl_xor(psum, 32, 64);
-        l_run = fmaf(l_run, fac, psum);
-        m_run = m_new;
-        if (__ballot(fac != 1.0f) != 0ull) {
-#pragma unroll
-            for (int m = 0; m < 16; m++) acc[m] *= fac;
-        }
-        const h4 pb = __builtin_bit_cast(h4, uint2{pk_rne(pv[0], pv[1]), pk_rne(pv[2], pv[3])});
-        // keys past n_k: V^T columns are padding, zero them
-        const int kv_ok = a.n_k - (k0 + 4 * lg);  // valid keys among this lane's 4
+        const h4 pb = __builtin_bit_cast(h4, uint2{pk_rne(p[0], p[1]), pk_rne(p[2], p[3])});
+        // ---- O^T += V^T P^T
 #pragma unroll
         for (int mt = 0; mt < 16; mt++) {
-            uint2 v = vr[mt];
-            if (kv_ok < 4) {
-                v.x = kv_ok <= 0 ? 0u : (kv_ok == 1 ? (v.x & 0xFFFFu) : v.x);
-                v.y = kv_ok <= 2 ? 0u : (v.y & 0xFFFFu);
-            }
-            acc[mt] = mfma16(__builtin_bit_cast(h4, v), pb, acc[mt]);
+            const h4 vop = *reinterpret_cast<const h4*>(&vs[buf][16 * mt + li][4 * lg]);
+            acc[mt] = mfma16(vop, pb, acc[mt]);
         }
-    };
-    if (k_lo < kt_hi) {
-        uint4 kA[8], kB[8];
-        uint2 vA[16], vB[16];
-        load_tile(k_lo, kA, vA);
-        for (int k0 = k_lo; k0 < kt_hi; k0 += 32) {
-            const bool has_b = k0 + 16 < kt_hi;
-            if (has_b) load_tile(k0 + 16, kB, vB);
-            compute_tile(k0, kA, vA);
-            if (k0 + 32 < kt_hi) load_tile(k0 + 32, kA, vA);
-            if (has_b) compute_tile(k0 + 16, kB, vB);
+        // ---- stage the next tile, load the one after
+        if (t + 1 < n_tiles) {
+            lstore(buf ^ 1, k0 + KT);
+            if (t + 2 < n_tiles) gload(k0 + 2 * KT);
         }
+        __syncthreads();
     }
     // ---- partial triple of row li (dims 16 mt + 4 lg + c)
+    float l_row = l_part + __shfl_xor(l_part, 16, 64);
+    l_row += __shfl_xor(l_row, 32, 64);
     if (r_ok) {
         float* out = a.part + ((size_t)(jq * H_q + hq) * a.n_split + split) * 258;
-        const bool empty = (m_run == -INFINITY);
+        const bool empty = (m_ref == -INFINITY);
 #pragma unroll
         for (int mt = 0; mt < 16; mt++)
             *reinterpret_cast<f4*>(&out[16 * mt + 4 * lg]) = empty ? f4{0.f, 0.f, 0.f, 0.f} : acc[mt];
         if (lg == 0) {
-            out[256] = empty ? -1e20f : m_run;
-            out[257] = empty ? 0.0f : l_run;
+            out[256] = empty ? -1e20f : m_ref;
+            out[257] = empty ? 0.0f : l_row;
         }
     }
 }
