@@ -424,7 +424,8 @@ int khq_decompress_fp16(const void* k_payload, const void* v_payload, const void
                         int tok0, int n_tok, int start_pos, float alpha_k, float alpha_v,
                         float rope_base, void* out_k, int key0, void* out_vt, int ld_vt,
                         hipStream_t stream) {
-    if (H_kv <= 0 || tok0 < 0 || n_tok < 0 || key0 < 0 || !out_k || !out_vt) return -100;
+    if (H_kv <= 0 || tok0 < 0 || n_tok < 0 || key0 < 0 || key0 % 8 != 0 || !out_k || !out_vt)
+        return -100;
     if (ld_vt % 8 != 0 || ld_vt < key0 + (n_tok + 63) / 64 * 64) return -100;
     khq::DecompArgs a{};
     a.kpay = static_cast<const uint8_t*>(k_payload);
@@ -485,9 +486,9 @@ int khq_prefill_attn_fp16(const void* q_gate, const void* k, const void* vt, int
     a.sc = scale;
     e = khq::launch_prefill_attn(a, stream);
     if (e != hipSuccess) return rc_of(e);
-    return rc_of(khq::launch_combine_gate(ws, static_cast<const __half*>(q_gate),
-                                          static_cast<__half*>(out), n_q * H_q, ns, 1e-8f,
-                                          stream));
+    return rc_of(khq::launch_prefill_merge(ws, static_cast<const __half*>(q_gate),
+                                           static_cast<__half*>(out), n_q * H_q, ns, 1e-8f,
+                                           stream));
 }
 
 int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centroids_k,

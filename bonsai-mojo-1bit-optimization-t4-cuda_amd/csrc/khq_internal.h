@@ -149,6 +149,10 @@ hipError_t launch_decompress(const DecompArgs& a, hipStream_t st);
 hipError_t launch_ring_gather(const GatherArgs& a, hipStream_t st);
 int prefill_splits(int n_q, int n_rep, int h_kv, int n_k, int* keys_per_split);
 hipError_t launch_prefill_attn(const PrefillArgs& a, hipStream_t st);
+// Merge of n_split partial triples per row, / (den + eps), sigmoid gate from
+// q_gate row r (f16 [r][512], gate at 256..511): out f16 [r][256].
+hipError_t launch_prefill_merge(const float* part, const __half* q_gate, __half* out, int n_rows,
+                                int n_split, float eps, hipStream_t st);
 // n consecutive tokens (kv halves each) into ring slots (slot0 + i) % ring_cap.
 hipError_t launch_ring_write_n(__half* rk, __half* rv, __half* ru, const __half* k,
                                const __half* v, const __half* ku, int kv, int slot0, int n,

@@ -30,7 +30,8 @@ namespace pf {
 
 using namespace mu;
 
-constexpr int TOK_BLK = 64;   // tokens per decompress / gather block
+constexpr int TOK_BLK = 16;   // tokens per decompress / gather block: one per wavefront
+constexpr int BLK_THR = 64 * TOK_BLK;
 constexpr int VT_PAD = 8;     // halves of padding per LDS V^T row
 
 __device__ __forceinline__ uint32_t rd32(const uint8_t* p) {
@@ -38,21 +39,22 @@ __device__ __forceinline__ uint32_t rd32(const uint8_t* p) {
 }
 
 // Writes the block's LDS V^T tile sv[256][TOK_BLK + VT_PAD] to vt columns
-// key0 .. key0 + TOK_BLK - 1 of KV head h (all 64 columns: the caller's
+// key0 .. key0 + TOK_BLK - 1 of KV head h (all TOK_BLK columns: the caller's
 // buffer is padded to a multiple of 64 keys).
 __device__ __forceinline__ void store_vt(const _Float16 (*sv)[TOK_BLK + VT_PAD], __half* vt, int ld,
                                          int h, int key0) {
     for (int i = threadIdx.x; i < 256 * (TOK_BLK / 8); i += blockDim.x) {
-        const int d = i >> 3, part = i & 7;
+        const int d = i / (TOK_BLK / 8), part = i % (TOK_BLK / 8);
         const uint4 v = *reinterpret_cast<const uint4*>(&sv[d][part * 8]);
         *reinterpret_cast<uint4*>(vt + ((size_t)h * 256 + d) * ld + key0 + part * 8) = v;
     }
 }
 
 // ------------------------------------------------------------- decompress
-// Block (64 tokens, KV head h), 4 wavefronts of 16 tokens each; lane p owns
+// Block (16 tokens, KV head h), one wavefront per token (the decode of one
+// row is a chain of dependent loads: tokens in parallel hide it); lane p owns
 // patch p = dims 4 p .. 4 p + 3.
-__global__ __launch_bounds__(256) void decompress_kernel(DecompArgs a) {
+__global__ __launch_bounds__(BLK_THR) void decompress_kernel(DecompArgs a) {
     __shared__ __align__(16) _Float16 sv[256][TOK_BLK + VT_PAD];
     const int h = blockIdx.y;
     const int wv = threadIdx.x >> 6, p = threadIdx.x & 63;
@@ -78,13 +80,13 @@ __global__ __launch_bounds__(256) void decompress_kernel(DecompArgs a) {
     for (int c = 0; c < 4; c++) fr[c] = powf(a.rope_base, -2.0f * (float)(4 * (p & 7) + c) / 64.0f);
     const uint64_t below = (p == 0) ? 0ull : (~0ull >> (64 - p));
 
-    for (int i = 0; i < 16; i++) {
-        const int tl = wv * 16 + i;  // token within the block
+    {
+        const int tl = wv;           // token within the block
         const int tok = t_blk + tl;
         if (tok >= a.n_tok) {        // uniform per wavefront
 #pragma unroll
             for (int c = 0; c < 4; c++) sv[4 * p + c][tl] = (_Float16)0.0f;
-            continue;
+            goto staged;
         }
         const size_t g = (size_t)(a.tok0 + tok) * a.h_kv + h;
         // ---- K: codes, outlier ordinals (ballot prefix), values
@@ -180,24 +182,26 @@ __global__ __launch_bounds__(256) void decompress_kernel(DecompArgs a) {
 #pragma unroll
         for (int c = 0; c < 4; c++) sv[4 * p + c][tl] = (_Float16)(y[c] * ldv[c]);
     }
+staged:
     __syncthreads();
     store_vt(sv, a.out_vt, a.ld_vt, h, a.key0 + t_blk);
 }
 
 // ------------------------------------------------------------ ring gather
-// Block (64 keys, KV head h): K rows copied, V rows transposed through LDS.
-__global__ __launch_bounds__(256) void ring_gather_kernel(GatherArgs a) {
+// Block (16 keys, KV head h), one wavefront per key: K rows copied, V rows
+// transposed through LDS.
+__global__ __launch_bounds__(BLK_THR) void ring_gather_kernel(GatherArgs a) {
     __shared__ __align__(16) _Float16 sv[256][TOK_BLK + VT_PAD];
     const int h = blockIdx.y;
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t_blk = blockIdx.x * TOK_BLK;
-    for (int i = 0; i < 16; i++) {
-        const int tl = wv * 16 + i;
+    {
+        const int tl = wv;
         const int t = t_blk + tl;
         if (t >= a.n) {
 #pragma unroll
             for (int c = 0; c < 4; c++) sv[4 * lane + c][tl] = (_Float16)0.0f;
-            continue;
+            goto staged;
         }
         int slot = a.win_start + t;
         slot = slot >= a.ring_cap ? slot - a.ring_cap : slot;
@@ -208,6 +212,7 @@ __global__ __launch_bounds__(256) void ring_gather_kernel(GatherArgs a) {
 #pragma unroll
         for (int c = 0; c < 4; c++) sv[4 * lane + c][tl] = v[c];
     }
+staged:
     __syncthreads();
     store_vt(sv, a.out_vt, a.ld_vt, h, a.key0 + t_blk);
 }
@@ -384,7 +389,36 @@ __global__ void ring_write_n_kernel(__half* __restrict__ rk, __half* __restrict_
     if (ru) ru[dst] = ku[src];
 }
 
+// Merge of the key splits, normalisation and gate: one block per (query,
+// head) row, thread = dim; every thread walks the row's n_split (m, l) pairs
+// (the same addresses for the whole block) and its own acc column.
+__global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part,
+                                                            const __half* __restrict__ q_gate,
+                                                            __half* __restrict__ out, int n_split,
+                                                            float eps) {
+    const int row = blockIdx.x, d = threadIdx.x;
+    const float* base = part + (size_t)row * n_split * 258;
+    float M = -1e30f;
+    for (int s = 0; s < n_split; s++) M = fmaxf(M, base[(size_t)s * 258 + 256]);
+    float num = 0.0f, den = 0.0f;
+    for (int s = 0; s < n_split; s++) {
+        const float* ps = base + (size_t)s * 258;
+        const float w = __expf(ps[256] - M);
+        den = fmaf(ps[257], w, den);
+        num = fmaf(ps[d], w, num);
+    }
+    const float g = __half2float(q_gate[(size_t)row * 512 + 256 + d]);
+    out[(size_t)row * 256 + d] = __float2half(num / (den + eps) * (1.0f / (1.0f + expf(-g))));
+}
+
 }  // namespace pf
+
+hipError_t launch_prefill_merge(const float* part, const __half* q_gate, __half* out, int n_rows,
+                                int n_split, float eps, hipStream_t st) {
+    hipLaunchKernelGGL(pf::prefill_merge_kernel, dim3(n_rows), dim3(256), 0, st, part, q_gate, out,
+                       n_split, eps);
+    return hipGetLastError();
+}
 
 hipError_t launch_ring_write_n(__half* rk, __half* rv, __half* ru, const __half* k,
                                const __half* v, const __half* ku, int kv, int slot0, int n,
@@ -398,14 +432,14 @@ hipError_t launch_ring_write_n(__half* rk, __half* rv, __half* ru, const __half*
 hipError_t launch_decompress(const DecompArgs& a, hipStream_t st) {
     if (a.n_tok <= 0) return hipSuccess;
     hipLaunchKernelGGL(pf::decompress_kernel, dim3((a.n_tok + pf::TOK_BLK - 1) / pf::TOK_BLK, a.h_kv),
-                       dim3(256), 0, st, a);
+                       dim3(pf::BLK_THR), 0, st, a);
     return hipGetLastError();
 }
 
 hipError_t launch_ring_gather(const GatherArgs& a, hipStream_t st) {
     if (a.n <= 0) return hipSuccess;
     hipLaunchKernelGGL(pf::ring_gather_kernel, dim3((a.n + pf::TOK_BLK - 1) / pf::TOK_BLK, a.h_kv),
-                       dim3(256), 0, st, a);
+                       dim3(pf::BLK_THR), 0, st, a);
     return hipGetLastError();
 }
 

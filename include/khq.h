@@ -153,7 +153,8 @@ typedef struct khq_seq {
  * decode and RoPE, :1608-1699, :1739-1762, :1776-1826): tokens [tok0, tok0 +
  * n_tok) of every KV head -> out_k f16 [key0 + t][H_kv][256] (roped at
  * position start_pos + tok0 + t) and out_vt f16 [H_kv][256][ld_vt] columns
- * key0 + t.  ld_vt: multiple of 8, >= key0 + n_tok rounded up to 64. */
+ * key0 + t.  key0 and ld_vt: multiples of 8, ld_vt >= key0 + n_tok rounded up
+ * to 64. */
 int khq_decompress_fp16(const void* k_payload, const void* v_payload, const void* v_shared_meta,
                         const void* k_mask, const void* k_norms, const void* k_r_norms,
                         const void* v_norms, const void* v_r_norms, const void* centroids_k,

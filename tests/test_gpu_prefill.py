@@ -44,7 +44,7 @@ def test_decompress_matches_float64_decoders(device, data):
         rows = random_rows_np(384 * H_KV, seed=42)
         if data == "outlier-cap":  # every dim an outlier on some rows: ordinals >= 50
             rows["kmask"][5::7] = 0xFFFFFFFF
-    tok0, n_tok, key0 = 21, 301, 35
+    tok0, n_tok, key0 = 21, 301, 40
     pay = payload_from_rows(rows, rows["kmask"].shape[0])
     cents = ops.Centroids(lc, device)
     ld = ops.vt_ld(key0 + n_tok)
