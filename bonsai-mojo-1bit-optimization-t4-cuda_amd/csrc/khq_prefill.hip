@@ -220,22 +220,27 @@ staged:
 // ----------------------------------------------------------- attention
 // Block = 4 wavefronts = 4 tiles of 16 query rows of one KV head, one key
 // split.  Row r of KV head h is (query j = r / n_rep, head h n_rep + r % n_rep).
-// Per 16-key tile the block stages K (16 x 256) and V^T (256 x 16) in LDS
+// Per 32-key tile the block stages K (32 x 256) and V^T (256 x 32) in LDS
 // (double-buffered, one barrier per tile; the next tile's global loads are in
 // flight while this one is computed), then each wavefront computes
-//   S^T (16 keys x 16 rows) = 8 MFMA 16x16x32, A = K rows, B = Q^T (registers);
-//   O^T (256 dims x 16 rows) += 16 MFMA 16x16x16, A = V^T, B = P^T, which is
-//   the C layout of S^T (lane: row li, keys 4 lg .. 4 lg + 3).
+//   S^T (two 16-key halves x 16 rows) = 16 MFMA 16x16x32, A = K rows, B = Q^T
+//   (registers); lane (row li, lg) gets keys 4 lg .. 4 lg + 3 of each half;
+//   O^T (256 dims x 16 rows) += 16 MFMA 16x16x32 with K = the tile's 32 keys
+//   in the order (4 lg .. 4 lg + 3, 16 + 4 lg .. 16 + 4 lg + 3) per lane
+//   group, so P^T is the S^T C layout as is and A = V^T read in that order.
 // Softmax: a per-row reference maximum shared by the row's 4 lanes, raised
 // (with a cross-lane reduction and a rescale) only when a score exceeds it by
 // more than 8, so weights stay <= e^8; row sums are per lane until the end.
-constexpr int KT = 16;            // keys per tile
-constexpr int KS_LD = 256 + 8;    // halves per LDS K row
+constexpr int KT = 32;            // keys per tile
+constexpr int KS_LD = 256 + 16;   // halves per LDS K row (bank spread measured with
+                                  // SQ_LDS_BANK_CONFLICT)
+constexpr int VS_LD = KT + 4;     // halves per LDS V^T row (rows 8-byte aligned:
+                                  // stored and read in 8-byte pieces)
 constexpr float GAP = 8.0f;
 
 __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
     __shared__ __align__(16) _Float16 ks[2][KT][KS_LD];
-    __shared__ __align__(16) _Float16 vs[2][256][KT];
+    __shared__ __align__(16) _Float16 vs[2][256][VS_LD];
     const int h = blockIdx.y;
     const int tid = threadIdx.x;
     const int wv = tid >> 6, lane = tid & 63;
@@ -269,37 +274,41 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
     for (int m = 0; m < 16; m++) acc[m] = f4{0.f, 0.f, 0.f, 0.f};
     float m_ref = -INFINITY, l_part = 0.0f;
 
-    // cooperative tile loads: thread t -> K key t / 16, 32 B at (t % 16) * 16
-    // halves; V^T dim t, the tile's 16 keys (32 B)
-    const int ld_key = tid >> 4, ld_off = (tid & 15) * 16;
+    // cooperative tile loads: thread t -> K key t / 8, 64 B at (t % 8) * 32
+    // halves; V^T dim t, the tile's 32 keys (64 B)
+    const int ld_key = tid >> 3, ld_off = (tid & 7) * 32;
     const __half* kg = a.k + (size_t)h * 256 + ld_off;
     const __half* vg = a.vt + ((size_t)h * 256 + tid) * a.ld_vt;
-    uint4 pk0 = uint4{0u, 0u, 0u, 0u}, pk1 = pk0, pv0 = pk0, pv1 = pk0;
+    uint4 pk[4], pv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) pk[i] = pv[i] = uint4{0u, 0u, 0u, 0u};
     auto gload = [&](int k0) {
         const int key = min(k0 + ld_key, a.n_k - 1);
         const uint4* ksrc = reinterpret_cast<const uint4*>(kg + (size_t)key * a.h_kv * 256);
-        pk0 = ksrc[0];
-        pk1 = ksrc[1];
         const uint4* vsrc = reinterpret_cast<const uint4*>(vg + k0);
-        pv0 = vsrc[0];
-        pv1 = vsrc[1];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            pk[i] = ksrc[i];
+            pv[i] = vsrc[i];
+        }
     };
-    // V^T word i of a tile row holds keys 2 i, 2 i + 1; columns past n_k are
+    // V^T word w of a tile row holds keys 2 w, 2 w + 1; columns past n_k are
     // padding and become zero
     auto vmask = [](uint32_t w, int i, int nv) {
         return 2 * i + 1 < nv ? w : (2 * i < nv ? (w & 0xFFFFu) : 0u);
     };
     auto lstore = [&](int buf, int k0) {
-        *reinterpret_cast<uint4*>(&ks[buf][ld_key][ld_off]) = pk0;
-        *reinterpret_cast<uint4*>(&ks[buf][ld_key][ld_off + 8]) = pk1;
         const int nv = a.n_k - k0;
-        uint4 v0 = pv0, v1 = pv1;
-        if (nv < KT) {
-            v0 = uint4{vmask(v0.x, 0, nv), vmask(v0.y, 1, nv), vmask(v0.z, 2, nv), vmask(v0.w, 3, nv)};
-            v1 = uint4{vmask(v1.x, 4, nv), vmask(v1.y, 5, nv), vmask(v1.z, 6, nv), vmask(v1.w, 7, nv)};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            *reinterpret_cast<uint4*>(&ks[buf][ld_key][ld_off + 8 * i]) = pk[i];
+            uint4 v = pv[i];
+            if (nv < KT)
+                v = uint4{vmask(v.x, 4 * i, nv), vmask(v.y, 4 * i + 1, nv), vmask(v.z, 4 * i + 2, nv),
+                          vmask(v.w, 4 * i + 3, nv)};
+            *reinterpret_cast<uint2*>(&vs[buf][tid][8 * i]) = uint2{v.x, v.y};
+            *reinterpret_cast<uint2*>(&vs[buf][tid][8 * i + 4]) = uint2{v.z, v.w};
         }
-        *reinterpret_cast<uint4*>(&vs[buf][tid][0]) = v0;
-        *reinterpret_cast<uint4*>(&vs[buf][tid][8]) = v1;
     };
 
     const int n_tiles = k_lo < kt_hi ? (kt_hi - k_lo + KT - 1) / KT : 0;
@@ -312,19 +321,23 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
     for (int t = 0; t < n_tiles; t++) {
         const int buf = t & 1;
         const int k0 = k_lo + t * KT;
-        // ---- S^T from LDS
-        f4 s = f4{0.f, 0.f, 0.f, 0.f};
+        // ---- S^T of both 16-key halves from LDS
+        f4 s0 = f4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
 #pragma unroll
         for (int st = 0; st < 8; st++) {
-            const h8 kop = *reinterpret_cast<const h8*>(&ks[buf][li][32 * st + 8 * lg]);
-            s = mfma32(kop, qb[st], s);
+            const h8 ka = *reinterpret_cast<const h8*>(&ks[buf][li][32 * st + 8 * lg]);
+            const h8 kb = *reinterpret_cast<const h8*>(&ks[buf][16 + li][32 * st + 8 * lg]);
+            s0 = mfma32(ka, qb[st], s0);
+            s1 = mfma32(kb, qb[st], s1);
         }
-        float sc[4], lmax = -INFINITY;
+        float sc[8], lmax = -INFINITY;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            sc[c] = (k0 + 4 * lg + c < vis) ? s[c] * a.sc : -INFINITY;
-            lmax = fmaxf(lmax, sc[c]);
+            sc[c] = (k0 + 4 * lg + c < vis) ? s0[c] * a.sc : -INFINITY;
+            sc[4 + c] = (k0 + 16 + 4 * lg + c < vis) ? s1[c] * a.sc : -INFINITY;
         }
+#pragma unroll
+        for (int e = 0; e < 8; e++) lmax = fmaxf(lmax, sc[e]);
         // ---- raise the row's reference maximum only when needed
         if (__ballot(lmax > m_ref + GAP) != 0ull) {
             float rmax = fmaxf(lmax, __shfl_xor(lmax, 16, 64));
@@ -338,18 +351,27 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
                 m_ref = m_new;
             }
         }
-        float p[4];
+        float p[8];
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            p[c] = sc[c] == -INFINITY ? 0.0f : __expf(sc[c] - m_ref);
-            l_part += p[c];
+        for (int e = 0; e < 8; e++) {
+            p[e] = sc[e] == -INFINITY ? 0.0f : __expf(sc[e] - m_ref);
+            l_part += p[e];
         }
-        const h4 pb = __builtin_bit_cast(h4, uint2{pk_rne(p[0], p[1]), pk_rne(p[2], p[3])});
-        // ---- O^T += V^T P^T
+        const h8 pb = __builtin_bit_cast(
+            h8, uint4{pk_rne(p[0], p[1]), pk_rne(p[2], p[3]), pk_rne(p[4], p[5]), pk_rne(p[6], p[7])});
+        // ---- O^T += V^T P^T (K = the 32 keys in the lane order above)
 #pragma unroll
-        for (int mt = 0; mt < 16; mt++) {
-            const h4 vop = *reinterpret_cast<const h4*>(&vs[buf][16 * mt + li][4 * lg]);
-            acc[mt] = mfma16(vop, pb, acc[mt]);
+        for (int m4 = 0; m4 < 16; m4 += 4) {  // 4 operand reads in flight, then 4 MFMAs
+            h8 vop[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint2 va = *reinterpret_cast<const uint2*>(&vs[buf][16 * (m4 + i) + li][4 * lg]);
+                const uint2 vb = *reinterpret_cast<const uint2*>(&vs[buf][16 * (m4 + i) + li][16 + 4 * lg]);
+                vop[i] = __builtin_bit_cast(h8, uint4{va.x, va.y, vb.x, vb.y});
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep the 4 reads ahead of their MFMAs
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[m4 + i] = mfma32(vop[i], pb, acc[m4 + i]);
         }
         // ---- stage the next tile, load the one after
         if (t + 1 < n_tiles) {
@@ -396,16 +418,34 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
                                                             const __half* __restrict__ q_gate,
                                                             __half* __restrict__ out, int n_split,
                                                             float eps) {
+    __shared__ float s_w[64];  // split weights exp(m_s - M)
+    __shared__ float s_l[64];
     const int row = blockIdx.x, d = threadIdx.x;
     const float* base = part + (size_t)row * n_split * 258;
-    float M = -1e30f;
-    for (int s = 0; s < n_split; s++) M = fmaxf(M, base[(size_t)s * 258 + 256]);
+    // the row's (m, l) pairs once per block, its acc column per thread, all
+    // loads issued before any is used (n_split <= 64)
+    float acc[64];
+#pragma unroll
+    for (int s = 0; s < 64; s++) acc[s] = s < n_split ? base[(size_t)s * 258 + d] : 0.0f;
+    float m = -1e30f, l = 0.0f;
+    if (d < n_split) {
+        m = base[(size_t)d * 258 + 256];
+        l = base[(size_t)d * 258 + 257];
+    }
+    float M = d < 64 ? m : -1e30f;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    if (d < 64) {
+        const float w = d < n_split ? __expf(m - M) : 0.0f;
+        s_w[d] = w;
+        s_l[d] = l * w;
+    }
+    __syncthreads();
     float num = 0.0f, den = 0.0f;
-    for (int s = 0; s < n_split; s++) {
-        const float* ps = base + (size_t)s * 258;
-        const float w = __expf(ps[256] - M);
-        den = fmaf(ps[257], w, den);
-        num = fmaf(ps[d], w, num);
+#pragma unroll
+    for (int s = 0; s < 64; s++) {
+        num = fmaf(acc[s], s_w[s], num);
+        den += s_l[s];
     }
     const float g = __half2float(q_gate[(size_t)row * 512 + 256 + d]);
     out[(size_t)row * 256 + d] = __float2half(num / (den + eps) * (1.0f / (1.0f + expf(-g))));
@@ -449,7 +489,7 @@ int prefill_splits(int n_q, int n_rep, int h_kv, int n_k, int* keys_per_split) {
     int ns = (1024 + blocks - 1) / blocks;  // ~4 wavefronts per SIMD of the chip
     ns = std::max(1, std::min(ns, 64));
     int per = (n_k + ns - 1) / ns;
-    per = (per + 31) / 32 * 32;
+    per = (per + pf::KT - 1) / pf::KT * pf::KT;
     ns = (n_k + per - 1) / per;
     *keys_per_split = per;
     return std::max(ns, 1);
