@@ -191,19 +191,63 @@ __global__ __launch_bounds__(256) void step_finish_kernel(FinishArgs a) {
     finish_block(a, blockIdx.x, blockIdx.y);
 }
 
-// Batched form: blockIdx.x = sequence * H_q + query head.
+// Global-memory load through a pointer read from memory (keeps the access a
+// global load instead of a flat one).
+template <typename T>
+__device__ __forceinline__ T gload(const T* p) {
+    return *(const __attribute__((address_space(1))) T*)p;
+}
+
+// Batched form (window computed upstream, a few parts per sequence): one
+// block per (sequence, query head), thread = dim; each thread walks the
+// row's parts (the (m, l) pairs are the same addresses for the whole block),
+// 8 parts' loads in flight at a time.
 __global__ __launch_bounds__(256) void step_finish_batched_kernel(const FinishArgs* __restrict__ args,
                                                                   int H_q) {
-    const FinishArgs a = args[blockIdx.x / H_q];
-    finish_block(a, blockIdx.x % H_q, blockIdx.y);
+    const FinishArgs& a = args[blockIdx.x / H_q];
+    const int hq = blockIdx.x % H_q, d = threadIdx.x;
+    const float* base = a.part + (size_t)hq * a.part_stride * 258;
+    const int np = a.n_parts;
+    float M = -1e30f;
+    for (int p0 = 0; p0 < np; p0 += 8) {
+        float mv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) mv[i] = gload(base + (size_t)min(p0 + i, np - 1) * 258 + 256);
+#pragma unroll
+        for (int i = 0; i < 8; i++) M = fmaxf(M, mv[i]);
+    }
+    float num = 0.0f, den = 0.0f;
+    for (int p0 = 0; p0 < np; p0 += 8) {
+        float av[8], mv[8], lv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float* pp = base + (size_t)min(p0 + i, np - 1) * 258;
+            av[i] = gload(pp + d);
+            mv[i] = gload(pp + 256);
+            lv[i] = gload(pp + 257);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float w = p0 + i < np ? __expf(mv[i] - M) : 0.0f;
+            num = fmaf(av[i], w, num);
+            den = fmaf(lv[i], w, den);
+        }
+    }
+    const unsigned short gb =
+        gload(reinterpret_cast<const unsigned short*>(a.q) + (size_t)hq * 512 + 256 + d);
+    const float g = __half2float(__ushort_as_half(gb));
+    const float val = num / (den + a.eps) * (1.0f / (1.0f + expf(-g)));
+    *(__attribute__((address_space(1))) unsigned short*)(reinterpret_cast<unsigned short*>(a.out) +
+                                                          (size_t)hq * 256 + d) =
+        __half_as_ushort(__float2half(val));
 }
 
 }  // namespace fin
 
 hipError_t launch_step_finish_batched(const FinishArgs* args, int n_seq, int H_q,
                                       hipStream_t st) {
-    hipLaunchKernelGGL(fin::step_finish_batched_kernel, dim3(n_seq * H_q, 256 / fin::DS),
-                       dim3(256), 0, st, args, H_q);
+    hipLaunchKernelGGL(fin::step_finish_batched_kernel, dim3(n_seq * H_q), dim3(256), 0, st, args,
+                       H_q);
     return hipGetLastError();
 }
 

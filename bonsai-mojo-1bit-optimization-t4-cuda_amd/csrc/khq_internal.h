@@ -61,8 +61,8 @@ struct FinishArgs {
     __half* out;  // [H_q][256]
 };
 hipError_t launch_step_finish(const FinishArgs& a, int H_q, hipStream_t st);
-// n_seq sequences, args a device array (window computed upstream or not, per
-// sequence as in FinishArgs; parts <= 1024, win_len <= 256 each).
+// n_seq sequences, args a device array; the window must already be a part
+// (win_len = 0 in every FinishArgs).
 hipError_t launch_step_finish_batched(const FinishArgs* args, int n_seq, int H_q,
                                       hipStream_t st);
 
