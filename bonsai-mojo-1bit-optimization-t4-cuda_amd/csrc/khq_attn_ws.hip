@@ -40,6 +40,8 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
+#include <math.h>
+#include <string.h>
 
 #include "khq_internal.h"
 #include "khq_mfma_util.h"
@@ -50,7 +52,7 @@ namespace ws {
 using namespace mu;
 
 #ifdef KHQ_PHASE_TIMING
-__device__ unsigned long long phase_cycles[16];
+__device__ unsigned long long phase_cycles[24];
 __device__ unsigned long long block_times[1024][2];
 #define PHASE(k)                                                              \
     do {                                                                      \
@@ -64,7 +66,7 @@ __device__ unsigned long long block_times[1024][2];
         __builtin_amdgcn_s_waitcnt(0x0F70);                                   \
         PHASE(k);                                                             \
     } while (0)
-#define PH_PARAMS , unsigned long long ph_t, unsigned (&ph_acc)[16]
+#define PH_PARAMS , unsigned long long ph_t, unsigned (&ph_acc)[24]
 #define PH_ARGS , ph_t, ph_acc
 #else
 #define PHASE(k) do { } while (0)
@@ -148,6 +150,40 @@ __device__ __forceinline__ void load_setup(const AttnArgs& a, int h, int wv, int
     }
 }
 
+// Block-shared constants copied to LDS: loaded at kernel entry, stored
+// after the query transforms, so the load latency overlaps that work.
+struct TabIn {
+    unsigned short cbk, c3;  // cents_k[2][tid] (tid < 256), cents_v[c][4 p + 3] (tid < 128)
+    uint4 rot;               // rotor_k (tid 256..383) or rotor_v (tid 384..511), 16 B each
+    uint4 dv;                // d_v (tid < 32)
+    float rope;              // RoPE table entry tid - 416 (tid >= 416)
+};
+
+__device__ __forceinline__ void load_tables(const AttnArgs& a, int tid, TabIn& tb) {
+    // unconditional loads (clamped indices): a load under a branch makes the
+    // compiler wait for every outstanding load at the join
+    const uint4* rsrc = tid < 384 ? reinterpret_cast<const uint4*>(a.rotor_k) + (tid & 127)
+                                  : reinterpret_cast<const uint4*>(a.rotor_v) + (tid - 384);
+    tb.rot = ldg<uint4>(rsrc);
+    tb.cbk = ldg<unsigned short>(a.cents_k + 512 + (tid & 255));
+    tb.c3 = ldg<unsigned short>(a.cents_v + ((tid >> 6) & 1) * 256 + (tid & 63) * 4 + 3);
+    tb.dv = ldg<uint4>(reinterpret_cast<const uint4*>(a.dv) + (tid & 31));
+    tb.rope = ldg<float>(&a.rope_tab[(tid + 64) % 96]);  // entry tid - 416 for tid >= 416
+}
+
+__device__ __forceinline__ void store_tables(Smem& S, int tid, const TabIn& tb) {
+    if (tid < 256) {
+        S.cbk[tid] = __builtin_bit_cast(_Float16, tb.cbk);
+    } else if (tid < 384) {
+        reinterpret_cast<uint4*>(&S.vp[0][0])[tid - 256] = tb.rot;
+    } else {
+        reinterpret_cast<uint4*>(S.rotv)[tid - 384] = tb.rot;
+    }
+    if (tid < 128) S.c3v[tid >> 6][tid & 63] = __builtin_bit_cast(_Float16, tb.c3);
+    if (tid < 32) reinterpret_cast<uint4*>(S.dvh)[tid] = tb.dv;
+    if (tid >= 416) (&S.rope[0][0][0])[tid - 416] = tb.rope;
+}
+
 // Query side of the pass part for 3 query heads of KV head h (heads hd0 ..
 // hd0 + 2): tq_hd = R^T H (q_hd[64:] / (256 d)) into S.o[h] as floats [6][256].
 __device__ __forceinline__ void query_transform(const SetupIn& in, Smem& S, int h, int hd0,
@@ -157,16 +193,6 @@ __device__ __forceinline__ void query_transform(const SetupIn& in, Smem& S, int 
     float dks[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) dks[c] = (1.0f / 256.0f) / ((float)dk4[c] + 1e-8f);
-#pragma unroll
-    for (int hd = 0; hd < 3; hd++) {
-        const h4 qh = __builtin_bit_cast(h4, in.qr[hd]);
-        f4 v;
-#pragma unroll
-        for (int c = 0; c < 4; c++) v[c] = lane >= 16 ? (float)qh[c] * dks[c] : 0.0f;
-        *reinterpret_cast<f4*>(&tq[hd * 256 + lane * 4]) = v;
-    }
-    wave_sync();
-    fwht256_lds(tq, 3, lane);
     float rk[16];
     {
         const h8 r0 = __builtin_bit_cast(h8, in.rk[0]), r1 = __builtin_bit_cast(h8, in.rk[1]);
@@ -176,10 +202,14 @@ __device__ __forceinline__ void query_transform(const SetupIn& in, Smem& S, int 
             rk[8 + t] = (float)r1[t];
         }
     }
-    // per patch: t[4p + k] = sum_c u[4p + c] R_p[c][k]
 #pragma unroll
     for (int hd = 0; hd < 3; hd++) {
-        const f4 u = *reinterpret_cast<const f4*>(&tq[hd * 256 + lane * 4]);
+        const h4 qh = __builtin_bit_cast(h4, in.qr[hd]);
+        float u[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) u[c] = lane >= 16 ? (float)qh[c] * dks[c] : 0.0f;
+        fwht256(u, lane);
+        // per patch: t[4p + k] = sum_c u[4p + c] R_p[c][k]
         f4 t;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -194,8 +224,9 @@ __device__ __forceinline__ void query_transform(const SetupIn& in, Smem& S, int 
 }
 
 // ---------------------------------------------------------------- key role
-__device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const SetupIn& in, int h,
-                                         int lane, int s_lo, int s_hi, int n_tiles PH_PARAMS) {
+__device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const SetupIn& in,
+                                         const TabIn& tb, int h, int lane, int s_lo, int s_hi,
+                                         int n_tiles PH_PARAMS) {
     const int li = lane & 15, lg = lane >> 4;
     const float* tq = S.o[h];  // [6][256] query transforms
 
@@ -250,11 +281,14 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
         kp_nx0 = __builtin_amdgcn_raw_buffer_load_b64(rs_kp, vo_kp0, so * 40, 0);
         kp_nx1 = __builtin_amdgcn_raw_buffer_load_b64(rs_kp, vo_kp1, so * 40, 0);
     };
+    PHASE(16);
     if (n_tiles > 0) prefetch(s_lo);
     query_transform(in, S, h, 0, lane);
+    store_tables(S, threadIdx.x, tb);
+    PHASE(17);
 
     __syncthreads();  // (1) tables, staged rotors and query transforms in place
-    PHASE(1);
+    PHASE(18);
 
     const float m_lo = arow_lo ? -1.0f : 0.0f;  // part_pk: lo rows take the remainder
     h8 At[8];
@@ -569,12 +603,13 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
     }
     __syncthreads();  // (3) maxima / sums / dump sums published
     __syncthreads();  // (4) V sums in place
-    PHASE(15);
+    PHASE(21);
 }
 
 // -------------------------------------------------------------- value role
-__device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const SetupIn& in, int h,
-                                           int lane, int s_lo, int s_hi, int n_tiles PH_PARAMS) {
+__device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const SetupIn& in,
+                                           const TabIn& tb, int h, int lane, int s_lo, int s_hi,
+                                           int n_tiles PH_PARAMS) {
     const int li = lane & 15, lg = lane >> 4;
 
     const int r_head = li >> 1;       // A row li: head li / 2, hi (even) or lo (odd)
@@ -618,6 +653,8 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
     };
     if (n_tiles > 0) prefetch(s_lo);
     query_transform(in, S, h, 3, lane);
+    store_tables(S, threadIdx.x, tb);
+    PHASE(19);
     __syncthreads();  // (1)
     PHASE(8);
     // V codebook (96 KB), copied by these wavefronts alone while the key
@@ -636,6 +673,7 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
             for (int i = 0; i < 12; i++) cbdst[vt + 256 * (12 * b + i)] = cbt[i];
         }
     }
+    PHASE(20);
     // lane constants: patch p = 16 g + li for g = 0..3
     _Float16 c3a[4], c3b[4];
 #pragma unroll
@@ -774,7 +812,7 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
         }
     }
     __syncthreads();  // (4)
-    PHASE(15);
+    PHASE(21);
 }
 
 // ------------------------------------------------------------ window block
@@ -929,26 +967,41 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
 #ifdef KHQ_PHASE_TIMING
     unsigned long long ph_t = __builtin_amdgcn_s_memtime();
     const unsigned long long rt0 = __builtin_amdgcn_s_memrealtime();
-    unsigned ph_acc[16];
+    unsigned ph_acc[24];
 #pragma unroll
-    for (int k = 0; k < 16; k++) ph_acc[k] = 0;
+    for (int k = 0; k < 24; k++) ph_acc[k] = 0;
 #endif
 
-    // ---- shared tables: sign table, cents_k[2], rotors, d_v, RoPE (the value
-    // wavefronts copy the codebook themselves, after this point)
+    // ---- shared tables: the sign and outlier selector tables are computed
+    // here; cents_k[2], the rotors, d_v, cents_v[.][4 p + 3] and the RoPE
+    // table are loaded here and stored after the query transforms (the
+    // value wavefronts copy the codebook after the first block barrier)
     SetupIn in;
+    TabIn tb;
     {
         load_setup(a, h, wv, lane, in);
-        if (tid < 256) {
+        load_tables(a, tid, tb);
+        // key wavefronts: sign tables; value wavefronts: outlier selectors
+        // (a wavefront-uniform split)
+        const int t = tid & 255;
+        if (wv < 4) {
             h4 s;
 #pragma unroll
             for (int c = 0; c < 4; c++) {
-                const int code = (tid >> (2 * c)) & 3;
+                const int code = (t >> (2 * c)) & 3;
                 s[c] = code == 2 ? (_Float16)1.0f : (code == 1 ? (_Float16)-1.0f : (_Float16)0.0f);
             }
-            S.sgn[tid] = __builtin_bit_cast(uint2, s);
-            S.cbk[tid] = ldg<_Float16>(a.cents_k + 512 + tid);
-            // outlier pattern tid (bit i: dim i of 8 is an outlier): output
+            S.sgn[t] = __builtin_bit_cast(uint2, s);
+            // sign bits t (bit r: ordinal r positive) -> high bytes of +-1024
+            uint32_t ev = 0, od = 0;
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                ev |= (((t >> (2 * m)) & 1) ? 0x64u : 0xE4u) << (8 * m);
+                od |= (((t >> (2 * m + 1)) & 1) ? 0x64u : 0xE4u) << (8 * m);
+            }
+            S.sgnb[t] = uint2{ev, od};
+        } else {
+            // outlier pattern t (bit i: dim i of 8 is an outlier): output
             // word k holds dims 2k, 2k + 1 as fp16 halves; the nibble selector
             // puts the byte of ordinal rank(i) in the low byte of the half, the
             // sign selector in the high byte.  Bytes of even ordinals come
@@ -960,7 +1013,7 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
                 uint32_t n = 0x0C0C0C0Cu, g = 0x0C0C0C0Cu;
 #pragma unroll
                 for (int e = 0; e < 2; e++) {
-                    if ((tid >> (2 * k + e)) & 1) {
+                    if ((t >> (2 * k + e)) & 1) {
                         const uint32_t src = (r & 1) ? 4u + (uint32_t)(r >> 1) : (uint32_t)(r >> 1);
                         n = (n & ~(0xFFu << (16 * e))) | (src << (16 * e));
                         g = (g & ~(0xFFu << (16 * e + 8))) | (src << (16 * e + 8));
@@ -970,48 +1023,17 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
                 sn[k] = n;
                 ss[k] = g;
             }
-            S.seln[tid] = uint4{sn[0], sn[1], sn[2], sn[3]};
-            S.sels[tid] = uint4{ss[0], ss[1], ss[2], ss[3]};
-            // sign bits tid (bit r: ordinal r positive) -> high bytes of +-1024
-            uint32_t ev = 0, od = 0;
-#pragma unroll
-            for (int m = 0; m < 4; m++) {
-                ev |= (((tid >> (2 * m)) & 1) ? 0x64u : 0xE4u) << (8 * m);
-                od |= (((tid >> (2 * m + 1)) & 1) ? 0x64u : 0xE4u) << (8 * m);
-            }
-            S.sgnb[tid] = uint2{ev, od};
-        } else if (tid < 256 + 128) {
-            reinterpret_cast<uint4*>(&S.vp[0][0])[tid - 256] =
-                ldg<uint4>(reinterpret_cast<const uint4*>(a.rotor_k) + tid - 256);
-        } else {
-            reinterpret_cast<uint4*>(S.rotv)[tid - 384] =
-                ldg<uint4>(reinterpret_cast<const uint4*>(a.rotor_v) + tid - 384);
-        }
-        if (tid < 128) {
-            const __half* cvh = a.cents_v;
-            S.c3v[tid >> 6][tid & 63] = ldg<_Float16>(cvh + (tid >> 6) * 256 + (tid & 63) * 4 + 3);
-        }
-        if (tid < 32) {
-            reinterpret_cast<uint4*>(S.dvh)[tid] = ldg<uint4>(reinterpret_cast<const uint4*>(a.dv) + tid);
-        } else if (tid >= 448) {
-            // lanes (u, lg) with u < 8 of the last wavefront: RoPE table
-            const int l = tid - 448, u = l & 15, g = l >> 4;
-            if (u < 8) {
-                const int m = 16 * (u >> 2) + 4 * g + (u & 3);
-                const float f = powf(a.rope_base, -2.0f * (float)m / 64.0f);
-                S.rope[g][0][u] = f;
-                S.rope[g][1][u] = cosf(16.0f * f);
-                S.rope[g][2][u] = sinf(16.0f * f);
-            }
+            S.seln[t] = uint4{sn[0], sn[1], sn[2], sn[3]};
+            S.sels[t] = uint4{ss[0], ss[1], ss[2], ss[3]};
         }
     }
 
     PHASE(0);
 
     if (wv < 4) {
-        key_role(a, S, in, h, lane, s_lo, s_hi, n_tiles PH_ARGS);
+        key_role(a, S, in, tb, h, lane, s_lo, s_hi, n_tiles PH_ARGS);
     } else {
-        value_role(a, S, in, h, lane, s_lo, s_hi, n_tiles PH_ARGS);
+        value_role(a, S, in, tb, h, lane, s_lo, s_hi, n_tiles PH_ARGS);
     }
 #ifdef KHQ_PHASE_TIMING
     ph_t = __builtin_amdgcn_s_memtime();
@@ -1054,8 +1076,8 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
     }
     PHASE(15);
 #ifdef KHQ_PHASE_TIMING
-    if (blockIdx.x == 0 && (threadIdx.x & 0xFF) == 0)
-        for (int k = 0; k < 16; k++) atomicAdd(&phase_cycles[k], (unsigned long long)ph_acc[k]);
+    if ((threadIdx.x & 0xFF) == 0)
+        for (int k = 0; k < 24; k++) atomicAdd(&phase_cycles[k], (unsigned long long)ph_acc[k]);
     if (threadIdx.x == 0 && blockIdx.x < 1024) {
         block_times[blockIdx.x][0] = rt0;
         block_times[blockIdx.x][1] = __builtin_amdgcn_s_memrealtime();
@@ -1082,6 +1104,25 @@ __global__ __launch_bounds__(NTHR, 1) void attn_ws_batched_kernel(const AttnArgs
 
 size_t attn_ws_smem_bytes() { return sizeof(ws::Smem); }
 
+void fill_rope_table(AttnArgs& a) {
+    // freq = powf(base, -2 m / 64) as the oracle and the portable kernels
+    // compute it; the 16-token rotation in double, rounded once
+    thread_local float last_base = -1.0f;
+    thread_local float tab[96];
+    if (a.rope_base != last_base) {
+        for (int g = 0; g < 4; g++)
+            for (int u = 0; u < 8; u++) {
+                const int m = 16 * (u >> 2) + 4 * g + (u & 3);
+                const float f = powf(a.rope_base, -2.0f * (float)m / 64.0f);
+                tab[(g * 3 + 0) * 8 + u] = f;
+                tab[(g * 3 + 1) * 8 + u] = (float)cos(16.0 * (double)f);
+                tab[(g * 3 + 2) * 8 + u] = (float)sin(16.0 * (double)f);
+            }
+        last_base = a.rope_base;
+    }
+    memcpy(a.rope_tab, tab, sizeof(tab));
+}
+
 hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks, hipStream_t st) {
     static bool configured = false;
     const size_t smem = sizeof(ws::Smem);
@@ -1092,7 +1133,9 @@ hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks, 
         configured = true;
     }
     const int blocks = n_chunks + (a.win_len > 0 ? 1 : 0);
-    hipLaunchKernelGGL(ws::attn_ws_kernel, dim3(blocks), dim3(ws::NTHR), smem, st, a,
+    AttnArgs b = a;
+    fill_rope_table(b);
+    hipLaunchKernelGGL(ws::attn_ws_kernel, dim3(blocks), dim3(ws::NTHR), smem, st, b,
                        tiles_per_chunk, n_chunks);
     return hipGetLastError();
 }
@@ -1117,9 +1160,9 @@ hipError_t launch_attn_ws_batched(const AttnArgs* args, const int2* map, int n_b
 #ifdef KHQ_PHASE_TIMING
 extern "C" int khq_ws_phase_cycles(unsigned long long* out, int reset) {
     hipError_t e = hipMemcpyFromSymbol(out, HIP_SYMBOL(khq::ws::phase_cycles),
-                                       sizeof(unsigned long long) * 16);
+                                       sizeof(unsigned long long) * 24);
     if (e == hipSuccess && reset) {
-        unsigned long long z[16] = {0};
+        unsigned long long z[24] = {0};
         e = hipMemcpyToSymbol(HIP_SYMBOL(khq::ws::phase_cycles), z, sizeof(z));
     }
     return e == hipSuccess ? 0 : (int)e;

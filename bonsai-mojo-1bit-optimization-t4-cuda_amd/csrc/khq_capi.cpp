@@ -594,6 +594,7 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
         a.win_start = q.win_start % ring;
         a.win_len = q.win_len;
         a.ring_cap = ring;
+        khq::fill_rope_table(a);
         h_args[i] = a;
         for (int c = 0; c < np[i]; c++) h_map.push_back(int2{i, c});
         khq::FinishArgs f{};

@@ -36,6 +36,10 @@ struct AttnArgs {
     const __half* ring_k;
     const __half* ring_v;
     int win_start, win_len, ring_cap;
+    // RoPE table of the wavefront-specialised kernel, [lane group g][3][u]:
+    // freq of dim pair m = 16 (u / 4) + 4 g + u % 4, cos and sin of 16 freq
+    // (filled by the launchers from rope_base).
+    float rope_tab[96];
 };
 
 // fp16 ring-window work, same partial layout (query = head).
@@ -93,6 +97,8 @@ hipError_t launch_attn_mfma(const AttnArgs& a, int tiles_per_chunk, int n_chunks
                             hipStream_t st);
 // Wavefront-specialised variant of the same contract (512 threads per block).
 size_t attn_ws_smem_bytes();
+// Fills a.rope_tab from a.rope_base (host).
+void fill_rope_table(AttnArgs& a);
 hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks,
                           hipStream_t st);
 // Batched: args[seq] (device) with n_parts = that sequence's chunk count and

@@ -123,6 +123,23 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t n_bytes) {
 }
 
 // Unnormalised FWHT-256 across a wavefront holding 4 consecutive dims per lane.
+// Butterfly partner values: xor 1 / xor 2 by DPP quad_perm, xor 4 / 8 / 16
+// by ds_swizzle (bit mode inside 32 lanes), xor 32 by a lane permute.
+template <int M>
+__device__ __forceinline__ float xor_lane(float v) {
+    if constexpr (M == 1) return dpp<0xB1>(v);
+    else if constexpr (M == 2) return dpp<0x4E>(v);
+    else if constexpr (M == 4 || M == 8 || M == 16)
+        return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (M << 10)));
+    else return __shfl_xor(v, 32, 64);
+}
+template <int M>
+__device__ __forceinline__ void fwht_stage(float (&v)[4], int lane) {
+    // lower lane: v + partner; upper lane: partner - v (fma with +-1 is exact)
+    const float s = (lane & M) ? -1.0f : 1.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) v[c] = fmaf(s, v[c], xor_lane<M>(v[c]));
+}
 __device__ __forceinline__ void fwht256(float (&v)[4], int lane) {
     float a = v[0], b = v[1];
     v[0] = a + b; v[1] = a - b;
@@ -132,43 +149,12 @@ __device__ __forceinline__ void fwht256(float (&v)[4], int lane) {
     v[0] = a + b; v[2] = a - b;
     a = v[1]; b = v[3];
     v[1] = a + b; v[3] = a - b;
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        const bool lower = (lane & m) == 0;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const float p = __shfl_xor(v[c], m, 64);
-            v[c] = lower ? (v[c] + p) : (p - v[c]);
-        }
-    }
-}
-
-// Two 16-point FWHT passes in LDS over n_vec vectors of 256 floats
-// (dim = 16 hi + lo: first along lo, then along hi), by one wavefront.
-__device__ __forceinline__ void fwht256_lds(float* v, int n_vec, int lane) {
-#pragma unroll
-    for (int pass = 0; pass < 2; pass++) {
-        for (int item = lane; item < n_vec * 16; item += 64) {
-            const int h = item >> 4, r = item & 15;
-            const int base = h * 256 + (pass == 0 ? r * 16 : r);
-            const int step = pass == 0 ? 1 : 16;
-            float x[16];
-#pragma unroll
-            for (int i = 0; i < 16; i++) x[i] = v[base + i * step];
-#pragma unroll
-            for (int m = 1; m < 16; m <<= 1)
-#pragma unroll
-                for (int i = 0; i < 16; i++)
-                    if ((i & m) == 0) {
-                        const float p = x[i], q = x[i + m];
-                        x[i] = p + q;
-                        x[i + m] = p - q;
-                    }
-#pragma unroll
-            for (int i = 0; i < 16; i++) v[base + i * step] = x[i];
-        }
-        wave_sync();
-    }
+    fwht_stage<1>(v, lane);
+    fwht_stage<2>(v, lane);
+    fwht_stage<4>(v, lane);
+    fwht_stage<8>(v, lane);
+    fwht_stage<16>(v, lane);
+    fwht_stage<32>(v, lane);
 }
 
 }  // namespace mu
