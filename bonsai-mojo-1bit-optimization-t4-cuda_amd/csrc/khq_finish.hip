@@ -19,17 +19,34 @@ namespace fin {
 
 using namespace mu;
 
+typedef float f2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ f2 ldg_f2(const float* p) {
+    return *(const __attribute__((address_space(1))) f2*)p;
+}
+__device__ __forceinline__ f4 ldg_f4(const float* p) {
+    return *(const __attribute__((address_space(1))) f4*)p;
+}
+
 constexpr int DS = 32;         // dims per block
 constexpr int MAX_WIN = 256;   // ring capacity bound
 constexpr int MAX_PARTS = 1024;  // compressed partials (+ a window partial)
 
+// Wavefront max / sum: rows of 16 by DPP, then xor 16 (swizzle) and xor 32.
+__device__ __forceinline__ float wave_max(float v) {
+    v = row16_max(v);
+    v = fmaxf(v, xor_lane<16>(v));
+    return fmaxf(v, xor_lane<32>(v));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    v += xor_lane<16>(v);
+    return v + xor_lane<32>(v);
+}
+
 // Block-wide max of (x, y) in one pass; s_red holds 8 floats.
 __device__ __forceinline__ void block_max2(float& x, float& y, float* s_red) {
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        x = fmaxf(x, __shfl_xor(x, o, 64));
-        y = fmaxf(y, __shfl_xor(y, o, 64));
-    }
+    x = wave_max(x);
+    y = wave_max(y);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) {
         s_red[threadIdx.x >> 6] = x;
@@ -40,11 +57,8 @@ __device__ __forceinline__ void block_max2(float& x, float& y, float* s_red) {
     y = fmaxf(fmaxf(s_red[4], s_red[5]), fmaxf(s_red[6], s_red[7]));
 }
 __device__ __forceinline__ void block_sum2(float& x, float& y, float* s_red) {
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        x += __shfl_xor(x, o, 64);
-        y += __shfl_xor(y, o, 64);
-    }
+    x = wave_sum(x);
+    y = wave_sum(y);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) {
         s_red[threadIdx.x >> 6] = x;
@@ -242,6 +256,98 @@ __global__ __launch_bounds__(256) void step_finish_batched_kernel(const FinishAr
         __half_as_ushort(__float2half(val));
 }
 
+// Merge-only form (the window is already a part): every wavefront of a
+// 256-thread block works alone on 8 dims of one query head.  Lane l takes
+// parts l, l + 64, ...: their (max, sum) pairs give the wavefront the
+// head's maximum and denominator, their 8-dim rows its numerators; a
+// reduce-scatter over the 64 lanes then leaves dim j of the 8 in the lanes
+// whose bits 3..5 spell j.  No block barrier; for n_parts <= 256 every
+// load is issued before the first value is used.
+__device__ __forceinline__ f2 ld_ml(const float* pp) { return ldg_f2(pp + 256); }
+
+__global__ __launch_bounds__(256) void step_merge_kernel(FinishArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int hq = blockIdx.x;
+    const int d0 = blockIdx.y * 32 + (threadIdx.x >> 6) * 8;
+    const float* base = a.part + (size_t)hq * a.part_stride * 258;
+    const int np = a.n_parts, last = max(np - 1, 0);
+    float num[8], den = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) num[j] = 0.0f;
+    if (np <= 256) {
+        f2 ml[4];
+        f4 o[4][2];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float* pp = base + (size_t)min(lane + 64 * k, last) * 258;
+            ml[k] = ld_ml(pp);
+            o[k][0] = ldg_f4(pp + d0);
+            o[k][1] = ldg_f4(pp + d0 + 4);
+        }
+        float M = -3.0e38f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) M = fmaxf(M, ml[k].x);
+        M = wave_max(M);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float w = lane + 64 * k < np ? __expf(ml[k].x - M) : 0.0f;
+            den = fmaf(ml[k].y, w, den);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                num[j] = fmaf(o[k][0][j], w, num[j]);
+                num[4 + j] = fmaf(o[k][1][j], w, num[4 + j]);
+            }
+        }
+    } else {
+        float M = -3.0e38f;
+        for (int p = lane; p < np; p += 64) M = fmaxf(M, base[(size_t)p * 258 + 256]);
+        M = wave_max(M);
+        for (int p = lane; p < np; p += 64) {
+            const float* pp = base + (size_t)p * 258;
+            const f2 ml = ld_ml(pp);
+            const f4 o0 = ldg_f4(pp + d0), o1 = ldg_f4(pp + d0 + 4);
+            const float w = __expf(ml.x - M);
+            den = fmaf(ml.y, w, den);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                num[j] = fmaf(o0[j], w, num[j]);
+                num[4 + j] = fmaf(o1[j], w, num[4 + j]);
+            }
+        }
+    }
+    den = wave_sum(den);
+    // reduce-scatter: xor 32 keeps half (4 + 2 + 1 values), then sum the rest
+    const bool b5 = (lane & 32) != 0, b4 = (lane & 16) != 0, b3 = (lane & 8) != 0;
+    float k4[4], k2[2];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float keep = b5 ? num[4 + i] : num[i];
+        const float send = b5 ? num[i] : num[4 + i];
+        k4[i] = keep + xor_lane<32>(send);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const float keep = b4 ? k4[2 + i] : k4[i];
+        const float send = b4 ? k4[i] : k4[2 + i];
+        k2[i] = keep + xor_lane<16>(send);
+    }
+    float v;
+    {
+        const float keep = b3 ? k2[1] : k2[0];
+        const float send = b3 ? k2[0] : k2[1];
+        v = keep + xor_lane<8>(send);
+    }
+    v += xor_lane<1>(v);
+    v += xor_lane<2>(v);
+    v += xor_lane<4>(v);
+    if ((lane & 7) == 0) {
+        const int d = d0 + (lane >> 3);
+        const float g = __half2float(a.q[(size_t)hq * 512 + 256 + d]);
+        const float val = v / (den + a.eps) * (1.0f / (1.0f + expf(-g)));
+        a.out[(size_t)hq * 256 + d] = __float2half(val);
+    }
+}
+
 }  // namespace fin
 
 hipError_t launch_step_finish_batched(const FinishArgs* args, int n_seq, int H_q,
@@ -254,6 +360,10 @@ hipError_t launch_step_finish_batched(const FinishArgs* args, int n_seq, int H_q
 hipError_t launch_step_finish(const FinishArgs& a, int H_q, hipStream_t st) {
     if (a.n_parts > fin::MAX_PARTS || a.win_len > fin::MAX_WIN || a.n_rep <= 0)
         return hipErrorInvalidValue;
+    if (a.win_len == 0 && a.n_parts > 0) {
+        hipLaunchKernelGGL(fin::step_merge_kernel, dim3(H_q, 8), dim3(256), 0, st, a);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(fin::step_finish_kernel, dim3(H_q, 256 / fin::DS), dim3(256), 0, st, a);
     return hipGetLastError();
 }
