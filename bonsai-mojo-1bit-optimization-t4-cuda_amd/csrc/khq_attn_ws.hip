@@ -93,8 +93,7 @@ struct __align__(16) Smem {
     uint4 sels[256];             // outlier pattern -> sign byte selectors
     uint2 sgnb[256];             // 8 sign bits -> sign bytes (even, odd ordinals)
     _Float16 cbk[256];           // cents_k[2]
-    float pw[2][4][6][TT];       // softmax weights, by tile parity
-    float fac[2][4][8];          // rescale factors of the same tile
+    float pw[2][4][6][TT];       // scaled scores, by tile parity
     float rope[4][3][8];         // per lane group: freq, cos(16 f), sin(16 f)
     _Float16 rotv[64 * 16];      // rotor_v
     _Float16 dvh[256];           // d_v
@@ -352,8 +351,6 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
         bc[u] = 1.0f;
         bs[u] = 0.0f;
     }
-    float Mref[2] = {-INFINITY, -INFINITY};
-    float lsum[2] = {0.f, 0.f};
     const _Float16* cbq = &S.cbk[64 * lg];
     uint32_t* kpw = S.kp[h];
     // Staged kpay row of a token, in words: 0 c_base_mult, 1..7 nibbles 0..55
@@ -548,32 +545,11 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
                 sc2[1] = -INFINITY;
             }
 
-            // ---- softmax with a lazily raised reference maximum
-            float fac[2] = {1.0f, 1.0f};
-            float mx[2];
-#pragma unroll
-            for (int x = 0; x < 2; x++) mx[x] = row16_max(sc2[x]);
-            const bool need = (mx[0] > Mref[0] + RESCALE_GAP) || (mx[1] > Mref[1] + RESCALE_GAP);
-            if (__ballot(need) != 0ull) {
-#pragma unroll
-                for (int x = 0; x < 2; x++) {
-                    const bool upx = mx[x] > Mref[x] + RESCALE_GAP;
-                    const float nm = upx ? mx[x] : Mref[x];
-                    fac[x] = (nm == -INFINITY) ? 1.0f : fexp(Mref[x] - nm);
-                    Mref[x] = nm;
-                    lsum[x] *= fac[x];
-                }
-            }
+            // ---- raw scores to the value side (it keeps the softmax state)
             const int buf = t & 1;
-#pragma unroll
-            for (int x = 0; x < 2; x++) {
-                const float pr = (sc2[x] == -INFINITY) ? 0.0f : fexp(sc2[x] - Mref[x]);
-                lsum[x] += pr;
-                if (lg < 3) S.pw[buf][h][2 * lg + x][li] = pr;
-            }
-            if (li == 0 && lg < 3) {
-                S.fac[buf][h][2 * lg] = fac[0];
-                S.fac[buf][h][2 * lg + 1] = fac[1];
+            if (lg < 3) {
+                S.pw[buf][h][2 * lg][li] = sc2[0];
+                S.pw[buf][h][2 * lg + 1][li] = sc2[1];
             }
 
             // ---- advance the lane's RoPE angles by 16 tokens
@@ -591,16 +567,6 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
         PHASE(6);
     }
 
-    // ---- epilogue: (max, sum) per query head
-#pragma unroll
-    for (int x = 0; x < 2; x++) lsum[x] = row16_sum(lsum[x]);
-    if (li == 0 && lg < 3) {
-#pragma unroll
-        for (int x = 0; x < 2; x++) {
-            S.ml[h][2 * lg + x][0] = Mref[x];
-            S.ml[h][2 * lg + x][1] = lsum[x];
-        }
-    }
     __syncthreads();  // (3) maxima / sums / dump sums published
     __syncthreads();  // (4) V sums in place
     PHASE(21);
@@ -686,6 +652,7 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
 #pragma unroll
     for (int n = 0; n < 20; n++) pv[n] = f4{0.f, 0.f, 0.f, 0.f};
     float s3p = 0.0f;  // sum of w * norm * smeta / 7 over this lane's tokens (hi rows)
+    float Mref = -INFINITY, lsum = 0.0f;  // softmax state of head r_head
     const float av = a.a_v;
     uint32_t* vpw = S.vp[h];
     PHASE(9);
@@ -695,13 +662,10 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
             PHASE_VM(14);
             const int t = it - 1;
             const int buf = t & 1;
-            // ---- the key side's weights and rescale factors of this tile
-            // (read first: their latency overlaps the staging below)
-            const float f0 = lg < 3 ? S.fac[buf][h][2 * lg] : 1.0f;
-            const float f1 = lg < 3 ? S.fac[buf][h][2 * lg + 1] : 1.0f;
-            const float fr = r_ok ? S.fac[buf][h][r_head] : 1.0f;
-            f4 pw4 = f4{0.f, 0.f, 0.f, 0.f};
-            if (r_ok) pw4 = *reinterpret_cast<const f4*>(&S.pw[buf][h][r_head][4 * lg]);
+            // ---- the key side's scores of this tile: row head r_head, tokens
+            // 4 lg .. 4 lg + 3 (read first: their latency overlaps the staging)
+            f4 sc4 = f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+            if (r_ok) sc4 = *reinterpret_cast<const f4*>(&S.pw[buf][h][r_head][4 * lg]);
             // ---- take the staged tile, start loading the next one
             const int s0 = s_lo + t * TT;
 #pragma unroll
@@ -730,8 +694,22 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
             if (t + 1 < n_tiles) prefetch(s_lo + (t + 1) * TT);
             wave_sync();
 
-            // ---- rescale for a raised maximum (rows 4 lg + c: head 2 lg + c / 2)
-            if (__ballot(f0 != 1.0f || f1 != 1.0f || fr != 1.0f) != 0ull) {
+            // ---- softmax of head r_head with a lazily raised reference
+            // maximum (the same state in every lane of the head)
+            float mx = fmaxf(fmaxf(sc4[0], sc4[1]), fmaxf(sc4[2], sc4[3]));
+            mx = fmaxf(mx, xor_lane<16>(mx));
+            mx = fmaxf(mx, xor_lane<32>(mx));
+            const bool need = mx > Mref + RESCALE_GAP;
+            if (__ballot(need) != 0ull) {
+                const float nm = need ? mx : Mref;
+                const float fr = (nm == -INFINITY) ? 1.0f : fexp(Mref - nm);
+                Mref = nm;
+                lsum *= fr;
+                s3p *= fr;
+                // C rows 4 lg + c hold heads 2 lg + c / 2: factors from the
+                // lanes whose A rows are those heads (lane 16 lg + 4 lg + 2 x)
+                const float f0 = lg < 3 ? __shfl(fr, 20 * lg, 64) : 1.0f;
+                const float f1 = lg < 3 ? __shfl(fr, 20 * lg + 2, 64) : 1.0f;
 #pragma unroll
                 for (int n = 0; n < 20; n++) {
                     pv[n][0] *= f0;
@@ -739,8 +717,11 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
                     pv[n][2] *= f1;
                     pv[n][3] *= f1;
                 }
-                s3p *= fr;
             }
+            f4 pw4;
+#pragma unroll
+            for (int c = 0; c < 4; c++) pw4[c] = (sc4[c] == -INFINITY) ? 0.0f : fexp(sc4[c] - Mref);
+            lsum += (pw4[0] + pw4[1]) + (pw4[2] + pw4[3]);
 
             // ---- weights x V scalings -> A operands (rows head hi/lo, K = tokens 4 lg..)
             h4 Ap[3];
@@ -791,7 +772,13 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
     // ---- epilogue: dump sums per head (hi rows li = 2 hd, all lane groups)
     s3p += __shfl_xor(s3p, 16, 64);
     s3p += __shfl_xor(s3p, 32, 64);
-    if (lg == 0 && r_ok && !r_lo) S.s3[h][r_head] = s3p;
+    lsum += xor_lane<16>(lsum);
+    lsum += xor_lane<32>(lsum);
+    if (lg == 0 && r_ok && !r_lo) {
+        S.s3[h][r_head] = s3p;
+        S.ml[h][r_head][0] = Mref;
+        S.ml[h][r_head][1] = lsum;
+    }
     __syncthreads();  // (3)
     // rotated-domain sums [6][256] in the key strip area of this KV head
     float* ep = S.o[h];
