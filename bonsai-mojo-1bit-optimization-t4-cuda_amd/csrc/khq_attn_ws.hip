@@ -641,12 +641,12 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
     }
     PHASE(20);
     // lane constants: patch p = 16 g + li for g = 0..3
-    _Float16 c3a[4], c3b[4];
+    // (cents_v[0][4 p + 3], cents_v[1][4 p + 3]) as one packed pair
+    uint32_t c3w[4];
 #pragma unroll
-    for (int g = 0; g < 4; g++) {
-        c3a[g] = S.c3v[0][16 * g + li];
-        c3b[g] = S.c3v[1][16 * g + li];
-    }
+    for (int g = 0; g < 4; g++)
+        c3w[g] = (uint32_t)__builtin_bit_cast(unsigned short, S.c3v[0][16 * g + li]) |
+                 ((uint32_t)__builtin_bit_cast(unsigned short, S.c3v[1][16 * g + li]) << 16);
 
     f4 pv[20];
 #pragma unroll
@@ -744,19 +744,33 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
                 const int vw0 = (p >> 3) * 3 + (vbit >> 5);
                 const int vsh = vbit & 31;
                 const int vhw = 24 + (g >> 1), vhb = p & 31;
-                h4 b0, b1, b2, b3, b4;
+                h4 b0, b1, b2;
+                uint32_t fl[4];
 #pragma unroll
                 for (int tt = 0; tt < 4; tt++) {
                     const uint32_t* vr = &vpw[(4 * lg + tt) * VP_TS];
-                    const uint32_t fld = __builtin_amdgcn_alignbit(vr[vw0 + 1], vr[vw0], vsh) & 0xFFFu;
+                    const uint32_t fld = __builtin_amdgcn_alignbit(vr[vw0 + 1], vr[vw0], vsh);
+                    fl[tt] = fld;
                     const uint32_t code = (fld & 0x7Fu) | (__builtin_amdgcn_ubfe(vr[vhw], vhb, 1) << 7);
                     const _Float16* ce = &S.cb[p * CB_PS + code * 3];
                     b0[tt] = ce[0];
                     b1[tt] = ce[1];
                     b2[tt] = ce[2];
-                    b3[tt] = ((fld >> 7) & 1u) ? c3b[g] : c3a[g];
-                    b4[tt] = (_Float16)(unsigned short)((fld >> 8) & 0xFu);
                 }
+                // tokens in pairs: the low 16 bits of both fields in one word;
+                // bit 7 picks cents_v[bit][4 p + 3] (byte selectors of c3w),
+                // bits 8..11 are the nibble (1024 + nib as fp16, minus 1024)
+                uint32_t w3[2], w4[2];
+#pragma unroll
+                for (int pr = 0; pr < 2; pr++) {
+                    const uint32_t x = __builtin_amdgcn_perm(fl[2 * pr + 1], fl[2 * pr], 0x05040100u);
+                    const uint32_t sel = ((x >> 6) & 0x00020002u) * 0x0101u + 0x01000100u;
+                    w3[pr] = __builtin_amdgcn_perm(c3w[g], c3w[g], sel);
+                    const h2 n = __builtin_bit_cast(h2, ((x >> 8) & 0x000F000Fu) | 0x64006400u);
+                    w4[pr] = __builtin_bit_cast(uint32_t, n - h2{(_Float16)1024.0f, (_Float16)1024.0f});
+                }
+                const h4 b3 = __builtin_bit_cast(h4, uint2{w3[0], w3[1]});
+                const h4 b4 = __builtin_bit_cast(h4, uint2{w4[0], w4[1]});
                 pv[5 * g + 0] = mfma16(Ap[0], b0, pv[5 * g + 0]);
                 pv[5 * g + 1] = mfma16(Ap[0], b1, pv[5 * g + 1]);
                 pv[5 * g + 2] = mfma16(Ap[0], b2, pv[5 * g + 2]);
