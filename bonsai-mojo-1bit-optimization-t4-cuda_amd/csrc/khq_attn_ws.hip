@@ -100,7 +100,24 @@ struct __align__(16) Smem {
     _Float16 c3v[2][64];         // cents_v[c][4 p + 3]
     float ml[4][6][2];           // final (max, sum) per query head
     float s3[4][8];              // final dump-offset sums per query head
+    int kdone[4];                // tiles whose scores the key wavefront has published
+    int vread[4];                // tiles whose scores the value wavefront has read
 };
+
+// Hand-off between the key and value wavefronts of one KV head through LDS
+// counters (release / acquire at workgroup scope), so each pair runs at its
+// own pace instead of meeting the other pairs at a block barrier every tile.
+// The wait is bounded: a wavefront never spins for more than ~2^20 sleeps.
+__device__ __forceinline__ void wait_count(const int* f, int target) {
+    int n = 0;
+    while (__hip_atomic_load(f, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+        __builtin_amdgcn_s_sleep(1);
+        if (++n > (1 << 20)) break;
+    }
+}
+__device__ __forceinline__ void publish_count(int* f, int v) {
+    __hip_atomic_store(f, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
 
 // Loads / stores through global-memory pointers (the batched kernel reads its
 // pointers from memory, where the compiler cannot tell their address space
@@ -545,12 +562,15 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
                 sc2[1] = -INFINITY;
             }
 
-            // ---- raw scores to the value side (it keeps the softmax state)
+            // ---- raw scores to the value side (it keeps the softmax state);
+            // buffer t & 1 last held tile t - 2
             const int buf = t & 1;
+            wait_count(&S.vread[h], t - 1);
             if (lg < 3) {
                 S.pw[buf][h][2 * lg][li] = sc2[0];
                 S.pw[buf][h][2 * lg + 1][li] = sc2[1];
             }
+            publish_count(&S.kdone[h], t + 1);
 
             // ---- advance the lane's RoPE angles by 16 tokens
 #pragma unroll
@@ -563,7 +583,7 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
             }
         }
         PHASE(5);
-        __syncthreads();  // (2) tile hand-off
+        if (it == 0) __syncthreads();  // (2) the value side's codebook copy is complete
         PHASE(6);
     }
 
@@ -664,6 +684,7 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
             const int buf = t & 1;
             // ---- the key side's scores of this tile: row head r_head, tokens
             // 4 lg .. 4 lg + 3 (read first: their latency overlaps the staging)
+            wait_count(&S.kdone[h], t + 1);
             f4 sc4 = f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
             if (r_ok) sc4 = *reinterpret_cast<const f4*>(&S.pw[buf][h][r_head][4 * lg]);
             // ---- take the staged tile, start loading the next one
@@ -722,6 +743,7 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
 #pragma unroll
             for (int c = 0; c < 4; c++) pw4[c] = (sc4[c] == -INFINITY) ? 0.0f : fexp(sc4[c] - Mref);
             lsum += (pw4[0] + pw4[1]) + (pw4[2] + pw4[3]);
+            publish_count(&S.vread[h], t + 1);
 
             // ---- weights x V scalings -> A operands (rows head hi/lo, K = tokens 4 lg..)
             h4 Ap[3];
@@ -779,7 +801,7 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
             }
         }
         PHASE(12);
-        __syncthreads();  // (2) tile hand-off
+        if (it == 0) __syncthreads();  // (2) codebook copy complete
         PHASE(13);
     }
 
@@ -985,6 +1007,10 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
         // key wavefronts: sign tables; value wavefronts: outlier selectors
         // (a wavefront-uniform split)
         const int t = tid & 255;
+        if (tid < 4) {
+            S.kdone[tid] = 0;
+            S.vread[tid] = 0;
+        }
         if (wv < 4) {
             h4 s;
 #pragma unroll
