@@ -3,12 +3,14 @@
 //
 // Shape: H_kv = 4 KV heads, 6 query heads per KV head, D = 256, one query
 // token.  One 512-thread block per token chunk, tiles of 16 tokens:
-//   key wavefronts   0..3 (KV head w): outliers, scores, softmax of tile t;
-//   value wavefronts 4..7 (KV head w-4): V decode and P x V of tile t - 1.
+//   key wavefronts   0..3 (KV head w): outliers and scores of tile t;
+//   value wavefronts 4..7 (KV head w-4): softmax, V decode and P x V of
+//                    tile t - 1.
 // Each SIMD holds one key and one value wavefront, so one hides the other's
-// latency.  The two roles meet once per tile at a block barrier; the softmax
-// weights (and the rescale factors of a raised running maximum) pass through
-// a double-buffered LDS slot.
+// latency.  The two roles of a KV head hand over through LDS counters (no
+// block barrier per tile): the key side publishes a tile's raw scores in a
+// double-buffered LDS slot, the value side keeps the running maximum and
+// sum and reports when it has read the slot.
 //
 // The decoded key of row s is   k_s = a_k * norm_s * mult_s * M b_s   with
 //   b_s[i] = sgn_i * cb_i                    for codes 0..2 (sgn 0, -1, +1)
