@@ -720,8 +720,15 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
             // ---- softmax of head r_head with a lazily raised reference
             // maximum (the same state in every lane of the head)
             float mx = fmaxf(fmaxf(sc4[0], sc4[1]), fmaxf(sc4[2], sc4[3]));
-            mx = fmaxf(mx, xor_lane<16>(mx));
-            mx = fmaxf(mx, xor_lane<32>(mx));
+            {
+                // across the four lane rows: row-pair and half swaps (VALU)
+                const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                                  false, false);
+                mx = fmaxf(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
+                const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                                  false, false);
+                mx = fmaxf(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
+            }
             const bool need = mx > Mref + RESCALE_GAP;
             if (__ballot(need) != 0ull) {
                 const float nm = need ? mx : Mref;
