@@ -484,9 +484,22 @@ hipError_t launch_ring_gather(const GatherArgs& a, hipStream_t st) {
 }
 
 int prefill_splits(int n_q, int n_rep, int h_kv, int n_k, int* keys_per_split) {
+    // Blocks that run at once: 2 per CU (72 KB of LDS each).  The split
+    // count fills that many slots in one round: a few blocks past a round
+    // cost a whole extra round.
+    static int n_cu = 0;
+    if (n_cu == 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            n_cu = v;
+        else
+            n_cu = 256;
+    }
+    const int slots = 2 * n_cu;
     const int mtiles = (n_q * n_rep + 15) / 16;
     const int blocks = (mtiles + 3) / 4 * h_kv;
-    int ns = (1024 + blocks - 1) / blocks;  // ~4 wavefronts per SIMD of the chip
+    int ns = slots / blocks;
     ns = std::max(1, std::min(ns, 64));
     int per = (n_k + ns - 1) / ns;
     per = (per + pf::KT - 1) / pf::KT * pf::KT;
