@@ -220,12 +220,29 @@ __global__ __launch_bounds__(256) void compress_kernel(
     const __half* cb = vq + (size_t)lane * 768;
     float best_d = 1e20f;
     unsigned best = 0;
-    for (unsigned i = 0; i < 256; i++) {
-        const float d0 = fmaf(-h2f(cb[i * 3 + 0]), alpha, v0);
-        const float d1 = fmaf(-h2f(cb[i * 3 + 1]), alpha, v1);
-        const float d2 = fmaf(-h2f(cb[i * 3 + 2]), alpha, v2);
-        const float dist = fmaf(d2, d2, fmaf(d1, d1, d0 * d0));
-        if (dist < best_d) { best_d = dist; best = i; }
+    // the lane's 768 codebook halves in chunks of 32 codes (12 x 16 B), the
+    // next chunk's loads in flight while this one is searched; codes in
+    // increasing order with a strict < (first minimum wins)
+    const uint4* cb4 = reinterpret_cast<const uint4*>(cb);
+    uint4 cur[12], nxt[12];
+#pragma unroll
+    for (int k = 0; k < 12; k++) cur[k] = cb4[k];
+    for (int ch = 0; ch < 8; ch++) {
+        if (ch + 1 < 8) {
+#pragma unroll
+            for (int k = 0; k < 12; k++) nxt[k] = cb4[12 * (ch + 1) + k];
+        }
+        const __half* hv = reinterpret_cast<const __half*>(cur);
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            const float d0 = fmaf(-h2f(hv[3 * j + 0]), alpha, v0);
+            const float d1 = fmaf(-h2f(hv[3 * j + 1]), alpha, v1);
+            const float d2 = fmaf(-h2f(hv[3 * j + 2]), alpha, v2);
+            const float dist = fmaf(d2, d2, fmaf(d1, d1, d0 * d0));
+            if (dist < best_d) { best_d = dist; best = 32u * ch + j; }
+        }
+#pragma unroll
+        for (int k = 0; k < 12; k++) cur[k] = nxt[k];
     }
     const float c0 = h2f(cb[best * 3 + 0]) * alpha;
     const float c1 = h2f(cb[best * 3 + 1]) * alpha;
