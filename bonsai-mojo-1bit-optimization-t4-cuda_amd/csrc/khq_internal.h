@@ -139,6 +139,15 @@ struct GatherArgs {
     __half* out_k;
     __half* out_vt;
     int h_kv, win_start, n, ring_cap, key0, ld_vt;
+    // Chunk mode (src_k != null): token t comes from src_k / src_v / src_u
+    // rows [t][h_kv][256] instead of the ring, and is also written to ring
+    // slot (win_start + t) % ring_cap of wr_k / wr_v / wr_u (wr_u optional).
+    const __half* src_k;
+    const __half* src_v;
+    const __half* src_u;
+    __half* wr_k;
+    __half* wr_v;
+    __half* wr_u;
 };
 // n_q queries (q_gate rows [n_q][H_q][512]) over dense keys [0, n_k); query j
 // sees keys [0, min(n_k, vis0 + j)).  Partial triple of (query j, head hq,
@@ -159,9 +168,5 @@ hipError_t launch_prefill_attn(const PrefillArgs& a, hipStream_t st);
 // q_gate row r (f16 [r][512], gate at 256..511): out f16 [r][256].
 hipError_t launch_prefill_merge(const float* part, const __half* q_gate, __half* out, int n_rows,
                                 int n_split, float eps, hipStream_t st);
-// n consecutive tokens (kv halves each) into ring slots (slot0 + i) % ring_cap.
-hipError_t launch_ring_write_n(__half* rk, __half* rv, __half* ru, const __half* k,
-                               const __half* v, const __half* ku, int kv, int slot0, int n,
-                               int ring_cap, hipStream_t st);
 
 }  // namespace khq

@@ -41,9 +41,10 @@ struct khq_layer {
     float *ac = nullptr, *aw = nullptr, *ap = nullptr;
     int boundary = 0, write_pos = 0, n_events = 0;
     // chunked prefill: dense fp16 keys [key][H_kv][256] and V^T [H_kv][256][ld]
-    // (key = token position), compressed tokens [0, dec_hi) already decoded
+    // (key = token position), compressed tokens [0, dec_hi) already decoded,
+    // raw tokens [raw_lo, raw_hi) already copied (empty when raw_lo >= raw_hi)
     __half *dk = nullptr, *dvt = nullptr;
-    int d_keys = 0, d_ld = 0, dec_hi = 0;
+    int d_keys = 0, d_ld = 0, dec_hi = 0, raw_lo = 0, raw_hi = 0;
 };
 
 namespace {
@@ -158,6 +159,7 @@ int khq_layer_reset(khq_layer* L) {
     L->write_pos = 0;
     L->n_events = 0;
     L->dec_hi = 0;
+    L->raw_lo = L->raw_hi = 0;
     return 0;
 }
 
@@ -192,6 +194,7 @@ int khq_layer_step(khq_layer* L, const void* q_gate, const void* k_roped, const 
     int rc = launch_khq_ring_write_fp16(L->ring_k, L->ring_v, k_unroped ? L->ring_u : nullptr,
                                         k_roped, v, k_unroped, slot, kv, stream);
     if (rc) return rc;
+    L->raw_lo = L->raw_hi = 0;  // the dense key space does not get this token
     L->write_pos += 1;
     if (event_due(L, L->write_pos)) {
         rc = compress_event(L, stream);
@@ -264,10 +267,31 @@ int khq_layer_prefill(khq_layer* L, const void* q_gate, const void* k_roped, con
         const int m = std::min(n - done, kRing - (L->write_pos - L->boundary));
         if (m <= 0) return -102;
         const int w0 = L->write_pos;
-        hipError_t e = khq::launch_ring_write_n(L->ring_k, L->ring_v, L->ring_u, kr + (size_t)done * kv,
-                                                vv + (size_t)done * kv, ku + (size_t)done * kv, kv,
-                                                w0 % kRing, m, kRing, stream);
+        // the sub-chunk's tokens go to their ring slots and to the dense key
+        // space in one launch
+        khq::GatherArgs cw{};
+        cw.out_k = L->dk;
+        cw.out_vt = L->dvt;
+        cw.h_kv = L->H_kv;
+        cw.win_start = w0 % kRing;
+        cw.n = m;
+        cw.ring_cap = kRing;
+        cw.key0 = w0;
+        cw.ld_vt = L->d_ld;
+        cw.src_k = kr + (size_t)done * kv;
+        cw.src_v = vv + (size_t)done * kv;
+        cw.src_u = ku + (size_t)done * kv;
+        cw.wr_k = L->ring_k;
+        cw.wr_v = L->ring_v;
+        cw.wr_u = L->ring_u;
+        hipError_t e = khq::launch_ring_gather(cw, stream);
         if (e != hipSuccess) return (int)e;
+        if (L->raw_lo < L->raw_hi && L->raw_hi == w0)
+            L->raw_hi = w0 + m;
+        else {
+            L->raw_lo = w0;
+            L->raw_hi = w0 + m;
+        }
         int j = 0;
         while (j < m) {
             // query j appends position w0 + j; an event fires before its attention
@@ -282,27 +306,38 @@ int khq_layer_prefill(khq_layer* L, const void* q_gate, const void* k_roped, con
             const int n_k = w0 + je;
             if (n_k - c_len > kRing) return -102;
             if (L->dec_hi < c_len) {
+                const int d0 = L->dec_hi, nd = c_len - d0;
                 const int rc = khq_decompress_fp16(
                     L->kpay, L->vpay, L->vsm, L->kmask, L->knorm, L->krn, L->vnorm, L->vrn,
                     L->cents_k, L->cents_v, L->vq, L->rotor_k, L->rotor_v, L->d_k, L->d_v, L->H_kv,
-                    L->dec_hi, c_len - L->dec_hi, 0, L->alpha_k, L->alpha_v, L->rope_base, L->dk,
-                    L->dec_hi, L->dvt, L->d_ld, stream);
+                    d0, nd, 0, L->alpha_k, L->alpha_v, L->rope_base, L->dk, d0, L->dvt, L->d_ld,
+                    stream);
                 if (rc) return rc;
                 L->dec_hi = c_len;
+                // V^T columns up to the decode's last 16-column block are rewritten
+                L->raw_lo = std::max(L->raw_lo, d0 + (nd + 15) / 16 * 16);
             }
-            khq::GatherArgs g{};
-            g.ring_k = L->ring_k;
-            g.ring_v = L->ring_v;
-            g.out_k = L->dk;
-            g.out_vt = L->dvt;
-            g.h_kv = L->H_kv;
-            g.win_start = c_len % kRing;
-            g.n = n_k - c_len;
-            g.ring_cap = kRing;
-            g.key0 = c_len;
-            g.ld_vt = L->d_ld;
-            e = khq::launch_ring_gather(g, stream);
-            if (e != hipSuccess) return (int)e;
+            // raw tokens [c_len, n_k) in the dense key space: copied from the
+            // ring unless already there (with every raw token after them, so
+            // the copy's padded last block clobbers nothing still needed)
+            if (!(L->raw_lo <= c_len && L->raw_hi >= n_k && L->raw_lo < L->raw_hi)) {
+                const int g_hi = std::max(n_k, L->raw_lo < L->raw_hi && L->raw_lo <= n_k ? L->raw_hi : n_k);
+                khq::GatherArgs g{};
+                g.ring_k = L->ring_k;
+                g.ring_v = L->ring_v;
+                g.out_k = L->dk;
+                g.out_vt = L->dvt;
+                g.h_kv = L->H_kv;
+                g.win_start = c_len % kRing;
+                g.n = g_hi - c_len;
+                g.ring_cap = kRing;
+                g.key0 = c_len;
+                g.ld_vt = L->d_ld;
+                e = khq::launch_ring_gather(g, stream);
+                if (e != hipSuccess) return (int)e;
+                L->raw_lo = c_len;
+                L->raw_hi = g_hi;
+            }
             const int rc = khq_prefill_attn_fp16(qg + (size_t)(done + j) * L->H_q * 2 * kD, L->dk,
                                                  L->dvt, L->d_ld, n_k, je - j, w0 + j + 1, L->H_q,
                                                  L->H_kv, scale,

@@ -50,6 +50,16 @@ __device__ __forceinline__ void store_vt(const _Float16 (*sv)[TOK_BLK + VT_PAD],
     }
 }
 
+// Writes columns key0 .. key0 + nc - 1 only (any alignment), 2 bytes each.
+__device__ __forceinline__ void store_vt_cols(const _Float16 (*sv)[TOK_BLK + VT_PAD], __half* vt,
+                                              int ld, int h, int key0, int nc) {
+    for (int i = threadIdx.x; i < 256 * TOK_BLK; i += blockDim.x) {
+        const int d = i / TOK_BLK, c = i % TOK_BLK;
+        if (c < nc)
+            reinterpret_cast<_Float16*>(vt)[((size_t)h * 256 + d) * ld + key0 + c] = sv[d][c];
+    }
+}
+
 // ------------------------------------------------------------- decompress
 // Block (16 tokens, KV head h), one wavefront per token (the decode of one
 // row is a chain of dependent loads: tokens in parallel hide it); lane p owns
@@ -189,7 +199,9 @@ staged:
 
 // ------------------------------------------------------------ ring gather
 // Block (16 keys, KV head h), one wavefront per key: K rows copied, V rows
-// transposed through LDS.
+// transposed through LDS.  In chunk mode the keys come from the caller's new
+// tokens, which also go to their ring slots (one launch appends a chunk to
+// the ring and to the dense key space).
 __global__ __launch_bounds__(BLK_THR) void ring_gather_kernel(GatherArgs a) {
     __shared__ __align__(16) _Float16 sv[256][TOK_BLK + VT_PAD];
     const int h = blockIdx.y;
@@ -205,16 +217,30 @@ __global__ __launch_bounds__(BLK_THR) void ring_gather_kernel(GatherArgs a) {
         }
         int slot = a.win_start + t;
         slot = slot >= a.ring_cap ? slot - a.ring_cap : slot;
-        const size_t src = ((size_t)slot * a.h_kv + h) * 256 + 4 * lane;
-        *reinterpret_cast<uint2*>(a.out_k + ((size_t)(a.key0 + t) * a.h_kv + h) * 256 + 4 * lane) =
-            *reinterpret_cast<const uint2*>(a.ring_k + src);
-        const h4 v = __builtin_bit_cast(h4, *reinterpret_cast<const uint2*>(a.ring_v + src));
+        const size_t rs = ((size_t)slot * a.h_kv + h) * 256 + 4 * lane;
+        uint2 kw, vw;
+        if (a.src_k) {
+            const size_t cs = ((size_t)t * a.h_kv + h) * 256 + 4 * lane;
+            kw = *reinterpret_cast<const uint2*>(a.src_k + cs);
+            vw = *reinterpret_cast<const uint2*>(a.src_v + cs);
+            *reinterpret_cast<uint2*>(a.wr_k + rs) = kw;
+            *reinterpret_cast<uint2*>(a.wr_v + rs) = vw;
+            if (a.wr_u) *reinterpret_cast<uint2*>(a.wr_u + rs) = *reinterpret_cast<const uint2*>(a.src_u + cs);
+        } else {
+            kw = *reinterpret_cast<const uint2*>(a.ring_k + rs);
+            vw = *reinterpret_cast<const uint2*>(a.ring_v + rs);
+        }
+        *reinterpret_cast<uint2*>(a.out_k + ((size_t)(a.key0 + t) * a.h_kv + h) * 256 + 4 * lane) = kw;
+        const h4 v = __builtin_bit_cast(h4, vw);
 #pragma unroll
         for (int c = 0; c < 4; c++) sv[4 * lane + c][tl] = v[c];
     }
 staged:
     __syncthreads();
-    store_vt(sv, a.out_vt, a.ld_vt, h, a.key0 + t_blk);
+    if (a.src_k)  // chunk mode: exactly the chunk's columns (key0 is any position)
+        store_vt_cols(sv, a.out_vt, a.ld_vt, h, a.key0 + t_blk, min(TOK_BLK, a.n - t_blk));
+    else
+        store_vt(sv, a.out_vt, a.ld_vt, h, a.key0 + t_blk);
 }
 
 // ----------------------------------------------------------- attention
@@ -396,21 +422,6 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
     }
 }
 
-__global__ void ring_write_n_kernel(__half* __restrict__ rk, __half* __restrict__ rv,
-                                    __half* __restrict__ ru, const __half* __restrict__ k,
-                                    const __half* __restrict__ v, const __half* __restrict__ ku,
-                                    int kv, int slot0, int ring_cap) {
-    const int t = blockIdx.y;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= kv) return;
-    int slot = slot0 + t;
-    slot = slot % ring_cap;
-    const size_t src = (size_t)t * kv + i, dst = (size_t)slot * kv + i;
-    if (rk) rk[dst] = k[src];
-    if (rv) rv[dst] = v[src];
-    if (ru) ru[dst] = ku[src];
-}
-
 // Merge of the key splits, normalisation and gate: one block per (query,
 // head) row, thread = dim; every thread walks the row's n_split (m, l) pairs
 // (the same addresses for the whole block) and its own acc column.
@@ -457,15 +468,6 @@ hipError_t launch_prefill_merge(const float* part, const __half* q_gate, __half*
                                 int n_split, float eps, hipStream_t st) {
     hipLaunchKernelGGL(pf::prefill_merge_kernel, dim3(n_rows), dim3(256), 0, st, part, q_gate, out,
                        n_split, eps);
-    return hipGetLastError();
-}
-
-hipError_t launch_ring_write_n(__half* rk, __half* rv, __half* ru, const __half* k,
-                               const __half* v, const __half* ku, int kv, int slot0, int n,
-                               int ring_cap, hipStream_t st) {
-    if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(pf::ring_write_n_kernel, dim3((kv + 255) / 256, n), dim3(256), 0, st, rk, rv,
-                       ru, k, v, ku, kv, slot0, ring_cap);
     return hipGetLastError();
 }
 

@@ -196,3 +196,34 @@ def test_c5_chunk_vs_oracle(device):
                                    ring_cap=256, H_q=H_Q, H_kv=H_KV, scale=SCALE)
         _, want = oracle.merge_gate(ac, aw, qj, H_q=H_Q, has_w=True)
         close(got[j], want)
+
+
+def test_layer_prefill_mixed_with_steps(device):
+    """Prefill chunks and single steps interleaved on one layer (the dense key
+    space must not keep raw tokens the steps wrote only to the ring) against
+    the same tokens stepped one by one."""
+    lc, _ = layer_consts(layer_id=9)
+    opt = KL.KhqOptions(splits=8, fused=True)
+    st = KL.NativeKhqLayer(lc, H_q=H_Q, H_kv=H_KV, cap=1024, device=device, options=opt)
+    mx = KL.NativeKhqLayer(lc, H_q=H_Q, H_kv=H_KV, cap=1024, device=device, options=opt)
+    n = 420
+    k, kr, v, q = _tokens(n, seed=29)
+    o_step = torch.empty((n, H_Q, D), device=device, dtype=torch.float16)
+    for i in range(n):
+        assert st.step(t(q[i]), t(kr[i]), t(v[i]), o_step[i], SCALE, k_unroped=t(k[i]))
+    o_mx = torch.empty_like(o_step)
+    i = 0
+    for kind, m in (("p", 100), ("s", 3), ("p", 60), ("s", 1), ("p", 97), ("s", 30), ("p", 129)):
+        if kind == "p":
+            assert mx.prefill(t(q[i:i + m]), t(kr[i:i + m]), t(v[i:i + m]), t(k[i:i + m]),
+                              o_mx[i:i + m], SCALE) == m
+        else:
+            for j in range(i, i + m):
+                assert mx.step(t(q[j]), t(kr[j]), t(v[j]), o_mx[j], SCALE, k_unroped=t(k[j]))
+        i += m
+    assert i == n
+    torch.cuda.synchronize()
+    assert mx.state() == st.state()
+    got, want = o_mx.cpu().numpy(), o_step.cpu().numpy()
+    for j in list(range(0, n, 7)) + [99, 100, 102, 103, 162, 163, 164, 260, 290, 291, n - 1]:
+        close(got[j], want[j])
