@@ -81,12 +81,16 @@ __global__ __launch_bounds__(256) void compress_kernel(
     __shared__ uint32_t s_w[4][32];
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + wave;
-    const bool live = row < n;
+    // K: one row per wavefront.  V: one row per block, the four wavefronts
+    // search a quarter of the codebook each and all finish the row; wavefront
+    // 0 writes it.
+    const int row = is_v ? (int)blockIdx.x : (int)blockIdx.x * 4 + wave;
+    const bool valid = row < n;
+    const bool live = valid && (!is_v || wave == 0);
     const float f_s = 0.0625f;
 
     float xv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (live) {
+    if (valid) {
         const __half* xr = x + (size_t)row * 256 + lane * 4;
 #pragma unroll
         for (int c = 0; c < 4; c++) xv[c] = h2f(xr[c]);
@@ -220,15 +224,17 @@ __global__ __launch_bounds__(256) void compress_kernel(
     const __half* cb = vq + (size_t)lane * 768;
     float best_d = 1e20f;
     unsigned best = 0;
-    // the lane's 768 codebook halves in chunks of 32 codes (12 x 16 B), the
-    // next chunk's loads in flight while this one is searched; codes in
-    // increasing order with a strict < (first minimum wins)
+    // the lane's codebook quarter (codes 64 wave .. + 63) in two chunks of 32
+    // codes (12 x 16 B), the second chunk's loads in flight while the first
+    // is searched; codes in increasing order with a strict < (first minimum
+    // wins), then the quarters in order through LDS, so the result is the
+    // sequential search's
     const uint4* cb4 = reinterpret_cast<const uint4*>(cb);
     uint4 cur[12], nxt[12];
 #pragma unroll
-    for (int k = 0; k < 12; k++) cur[k] = cb4[k];
-    for (int ch = 0; ch < 8; ch++) {
-        if (ch + 1 < 8) {
+    for (int k = 0; k < 12; k++) cur[k] = cb4[12 * (2 * wave) + k];
+    for (int ch = 2 * wave; ch < 2 * wave + 2; ch++) {
+        if (ch + 1 < 2 * wave + 2) {
 #pragma unroll
             for (int k = 0; k < 12; k++) nxt[k] = cb4[12 * (ch + 1) + k];
         }
@@ -243,6 +249,21 @@ __global__ __launch_bounds__(256) void compress_kernel(
         }
 #pragma unroll
         for (int k = 0; k < 12; k++) cur[k] = nxt[k];
+    }
+    {
+        __shared__ float s_bd[4][64];
+        __shared__ unsigned s_bi[4][64];
+        s_bd[wave][lane] = best_d;
+        s_bi[wave][lane] = best;
+        __syncthreads();
+        best_d = s_bd[0][lane];
+        best = s_bi[0][lane];
+#pragma unroll
+        for (int w = 1; w < 4; w++)
+            if (s_bd[w][lane] < best_d) {
+                best_d = s_bd[w][lane];
+                best = s_bi[w][lane];
+            }
     }
     const float c0 = h2f(cb[best * 3 + 0]) * alpha;
     const float c1 = h2f(cb[best * 3 + 1]) * alpha;
@@ -816,7 +837,7 @@ hipError_t launch_compress(const __half* x, const __half* d_vec, const __half* r
                            __half* out_norms, __half* out_rn, uint8_t* out_pay,
                            uint8_t* out_sm, int n, float ts, float alpha, int is_v,
                            hipStream_t st) {
-    const int blocks = (n + 3) / 4;
+    const int blocks = is_v ? n : (n + 3) / 4;
     hipLaunchKernelGGL(compress_kernel, dim3(blocks), dim3(256), 0, st, x, d_vec, rotor, cents,
                        vq, out_mask, out_norms, out_rn, out_pay, out_sm, n, ts, alpha, is_v);
     return hipGetLastError();
