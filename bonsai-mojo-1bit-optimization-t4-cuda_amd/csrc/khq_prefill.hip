@@ -30,7 +30,8 @@ namespace pf {
 
 using namespace mu;
 
-constexpr int TOK_BLK = 16;   // tokens per decompress / gather block: one per wavefront
+constexpr int TOK_BLK = 4;    // tokens per decompress / gather block: one per wavefront
+                              // (small blocks spread a short chunk over many CUs)
 constexpr int BLK_THR = 64 * TOK_BLK;
 constexpr int VT_PAD = 8;     // halves of padding per LDS V^T row
 
@@ -40,13 +41,14 @@ __device__ __forceinline__ uint32_t rd32(const uint8_t* p) {
 
 // Writes the block's LDS V^T tile sv[256][TOK_BLK + VT_PAD] to vt columns
 // key0 .. key0 + TOK_BLK - 1 of KV head h (all TOK_BLK columns: the caller's
-// buffer is padded to a multiple of 64 keys).
+// buffer is padded to a multiple of 64 keys), in 8-byte pieces (key0 is a
+// multiple of 4).
 __device__ __forceinline__ void store_vt(const _Float16 (*sv)[TOK_BLK + VT_PAD], __half* vt, int ld,
                                          int h, int key0) {
-    for (int i = threadIdx.x; i < 256 * (TOK_BLK / 8); i += blockDim.x) {
-        const int d = i / (TOK_BLK / 8), part = i % (TOK_BLK / 8);
-        const uint4 v = *reinterpret_cast<const uint4*>(&sv[d][part * 8]);
-        *reinterpret_cast<uint4*>(vt + ((size_t)h * 256 + d) * ld + key0 + part * 8) = v;
+    for (int i = threadIdx.x; i < 256 * (TOK_BLK / 4); i += blockDim.x) {
+        const int d = i / (TOK_BLK / 4), part = i % (TOK_BLK / 4);
+        const uint2 v = *reinterpret_cast<const uint2*>(&sv[d][part * 4]);
+        *reinterpret_cast<uint2*>(vt + ((size_t)h * 256 + d) * ld + key0 + part * 4) = v;
     }
 }
 
