@@ -1082,7 +1082,8 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
     for (int t = 0; t < 16; t++) rv[t] = (float)S.rotv[lane * 16 + t];
     float rdv[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) rdv[c] = (1.0f / 16.0f) / ((float)S.dvh[lane * 4 + c] + 1e-8f);
+    for (int c = 0; c < 4; c++)  // hardware reciprocal: 1 ulp, far below the output bar
+        rdv[c] = 0.0625f * __builtin_amdgcn_rcpf((float)S.dvh[lane * 4 + c] + 1e-8f);
 #pragma unroll
     for (int hh = 0; hh < 3; hh++) {
         const int hd = 3 * (wv >> 2) + hh;
@@ -1103,12 +1104,11 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
         const float M = S.ml[h][hd][0];
         const float L = S.ml[h][hd][1];
         const bool empty = (M == -INFINITY);
-#pragma unroll
-        for (int c = 0; c < 4; c++) stg<float>(&out[lane * 4 + c], empty ? 0.0f : u[c] * rdv[c]);
-        if (lane == 0) {
-            stg<float>(&out[256], empty ? -1e20f : M);
-            stg<float>(&out[257], empty ? 0.0f : L);
-        }
+        // partial rows are 258 floats: 8-byte aligned, so 8-byte stores
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        stg<f2>(&out[lane * 4], empty ? f2{0.f, 0.f} : f2{u[0] * rdv[0], u[1] * rdv[1]});
+        stg<f2>(&out[lane * 4 + 2], empty ? f2{0.f, 0.f} : f2{u[2] * rdv[2], u[3] * rdv[3]});
+        if (lane == 0) stg<f2>(&out[256], empty ? f2{-1e20f, 0.f} : f2{M, L});
     }
     PHASE(15);
 #ifdef KHQ_PHASE_TIMING
