@@ -424,6 +424,199 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
     }
 }
 
+// 32-row form: each wavefront owns 32 query rows and uses 32x32x16 MFMAs, so
+// every K / V^T operand read from LDS feeds twice the arithmetic of the
+// 16-row form.  One block (4 wavefronts, 128 rows) per CU: the O^T
+// accumulators (32 rows x 256 dims) and Q^T (32 x 256 fp16) stay in
+// registers.  Per tile every LDS operand read of the tile (16 K, 32 V^T) is
+// issued first, then the S^T MFMAs (four accumulation chains), the softmax
+// and the P x V MFMAs.  32x32 layouts (lane l, n = l % 32, hh = l / 32):
+//   A[m][k]: lane m + 32 (k / 8) holds element k % 8;  B[k][n] likewise;
+//   C[m][n]: lane n + 32 hh, register r <-> m = 8 (r / 4) + 4 hh + r % 4.
+// S^T = K Q^T (keys x rows); its C registers 8 s' .. 8 s' + 7 are the B
+// operand of K-step s' of O^T += V^T P^T when that step's K order is
+// key 8 (2 s' + i / 4) + 4 hh + i % 4 for element i, which is how V^T is read.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ f32x16 mfma3232(h8 a, h8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+constexpr int KS2_LD = 256 + 8;   // halves per LDS K row
+constexpr int VS2_LD = KT + 4;    // halves per LDS V^T row
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void prefill_attn32_kernel(PrefillArgs a) {
+    __shared__ __align__(16) _Float16 ks[2][KT][KS2_LD];
+    __shared__ __align__(16) _Float16 vs[2][256][VS2_LD];
+    const int h = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int wv = tid >> 6, lane = tid & 63;
+    const int ln = lane & 31, hh = lane >> 5;
+    const int n_rows = a.n_q * a.n_rep;
+    const int row0 = (blockIdx.x * 4 + wv) * 32;
+    const int split = blockIdx.z;
+    const int k_lo = split * a.keys_per_split;
+    const int k_hi = min(a.n_k, k_lo + a.keys_per_split);
+    const int H_q = a.h_kv * a.n_rep;
+    const int r = row0 + ln;
+    const bool r_ok = r < n_rows;
+    const int jq = r_ok ? r / a.n_rep : 0;
+    const int hq = h * a.n_rep + (r_ok ? r % a.n_rep : 0);
+    const int vis = r_ok ? min(a.n_k, a.vis0 + jq) : 0;
+    // the block's last visible key (rows are ordered by query)
+    const int b_last = min((int)blockIdx.x * 128 + 127, n_rows - 1);
+    const int kt_hi = min(k_hi, min(a.n_k, a.vis0 + b_last / a.n_rep));
+
+    h8 qb[16];
+    {
+        const __half* qrow = a.q + ((size_t)jq * H_q + hq) * 512;
+#pragma unroll
+        for (int st = 0; st < 16; st++) {
+            const uint4 v = *reinterpret_cast<const uint4*>(qrow + 16 * st + 8 * hh);
+            qb[st] = __builtin_bit_cast(h8, r_ok ? v : uint4{0u, 0u, 0u, 0u});
+        }
+    }
+    f32x16 acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[t][e] = 0.0f;
+    float m_ref = -INFINITY, l_part = 0.0f;
+
+    // cooperative tile loads: thread t -> K key t / 8, 64 B at (t % 8) * 32
+    // halves; V^T dim t, the tile's 32 keys (64 B)
+    const int ld_key = tid >> 3, ld_off = (tid & 7) * 32;
+    const __half* kg = a.k + (size_t)h * 256 + ld_off;
+    const __half* vg = a.vt + ((size_t)h * 256 + tid) * a.ld_vt;
+    uint4 pk[4], pv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) pk[i] = pv[i] = uint4{0u, 0u, 0u, 0u};
+    auto gload = [&](int k0) {
+        const int key = min(k0 + ld_key, a.n_k - 1);
+        const uint4* ksrc = reinterpret_cast<const uint4*>(kg + (size_t)key * a.h_kv * 256);
+        const uint4* vsrc = reinterpret_cast<const uint4*>(vg + k0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            pk[i] = ksrc[i];
+            pv[i] = vsrc[i];
+        }
+    };
+    auto vmask = [](uint32_t w, int i, int nv) {
+        return 2 * i + 1 < nv ? w : (2 * i < nv ? (w & 0xFFFFu) : 0u);
+    };
+    auto lstore = [&](int buf, int k0) {
+        const int nv = a.n_k - k0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            *reinterpret_cast<uint4*>(&ks[buf][ld_key][ld_off + 8 * i]) = pk[i];
+            uint4 v = pv[i];
+            if (nv < KT)
+                v = uint4{vmask(v.x, 4 * i, nv), vmask(v.y, 4 * i + 1, nv), vmask(v.z, 4 * i + 2, nv),
+                          vmask(v.w, 4 * i + 3, nv)};
+            *reinterpret_cast<uint2*>(&vs[buf][tid][8 * i]) = uint2{v.x, v.y};
+            *reinterpret_cast<uint2*>(&vs[buf][tid][8 * i + 4]) = uint2{v.z, v.w};
+        }
+    };
+
+    const int n_tiles = k_lo < kt_hi ? (kt_hi - k_lo + KT - 1) / KT : 0;
+    if (n_tiles > 0) {
+        gload(k_lo);
+        lstore(0, k_lo);
+        if (n_tiles > 1) gload(k_lo + KT);
+    }
+    __syncthreads();
+    for (int t = 0; t < n_tiles; t++) {
+        const int buf = t & 1;
+        const int k0 = k_lo + t * KT;
+        // ---- the tile's K operand reads first, then S^T (32 keys x 32 rows)
+        // in four accumulation chains
+        f32x16 sc4[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) sc4[c][e] = 0.0f;
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            h8 kop[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                kop[i] = *reinterpret_cast<const h8*>(&ks[buf][ln][16 * (8 * half + i) + 8 * hh]);
+#pragma unroll
+            for (int i = 0; i < 8; i++) sc4[i & 3] = mfma3232(kop[i], qb[8 * half + i], sc4[i & 3]);
+        }
+        float sc[16], lmax = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int key = k0 + 8 * (e >> 2) + 4 * hh + (e & 3);
+            const float x = (sc4[0][e] + sc4[1][e]) + (sc4[2][e] + sc4[3][e]);
+            sc[e] = key < vis ? x * a.sc : -INFINITY;
+            lmax = fmaxf(lmax, sc[e]);
+        }
+        // ---- raise the row's reference maximum only when needed (the row's
+        // keys sit in lanes l and l ^ 32)
+        if (__ballot(lmax > m_ref + GAP) != 0ull) {
+            const float rmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
+            const float m_new = fmaxf(m_ref, rmax);
+            if (m_new > m_ref) {
+                const float fac = __expf(m_ref - m_new);  // 0 when m_ref = -inf
+#pragma unroll
+                for (int t2 = 0; t2 < 8; t2++) acc[t2] *= fac;
+                l_part *= fac;
+                m_ref = m_new;
+            }
+        }
+        h8 pb[2];
+#pragma unroll
+        for (int sp = 0; sp < 2; sp++) {
+            float p[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float x = sc[8 * sp + i];
+                p[i] = x == -INFINITY ? 0.0f : __expf(x - m_ref);
+                l_part += p[i];
+            }
+            pb[sp] = __builtin_bit_cast(h8, uint4{pk_rne(p[0], p[1]), pk_rne(p[2], p[3]),
+                                                  pk_rne(p[4], p[5]), pk_rne(p[6], p[7])});
+        }
+        // ---- O^T += V^T P^T: 8 tiles of 32 dims x 2 K-steps of 16 keys; each
+        // K-step's 8 operand reads issued before its MFMAs
+#pragma unroll
+        for (int sp = 0; sp < 2; sp++) {
+            h8 vop[8];
+#pragma unroll
+            for (int t2 = 0; t2 < 8; t2++) {
+                const uint2 va = *reinterpret_cast<const uint2*>(&vs[buf][32 * t2 + ln][16 * sp + 4 * hh]);
+                const uint2 vb = *reinterpret_cast<const uint2*>(&vs[buf][32 * t2 + ln][16 * sp + 8 + 4 * hh]);
+                vop[t2] = __builtin_bit_cast(h8, uint4{va.x, va.y, vb.x, vb.y});
+            }
+#pragma unroll
+            for (int t2 = 0; t2 < 8; t2++) acc[t2] = mfma3232(vop[t2], pb[sp], acc[t2]);
+        }
+        // ---- stage the next tile, load the one after
+        if (t + 1 < n_tiles) {
+            lstore(buf ^ 1, k0 + KT);
+            if (t + 2 < n_tiles) gload(k0 + 2 * KT);
+        }
+        __syncthreads();
+    }
+    // ---- partial triple of row ln (dims 32 t + 8 j + 4 hh + c)
+    const float l_row = l_part + __shfl_xor(l_part, 32, 64);
+    if (r_ok) {
+        float* out = a.part + ((size_t)(jq * H_q + hq) * a.n_split + split) * 258;
+        const bool empty = (m_ref == -INFINITY);
+#pragma unroll
+        for (int t2 = 0; t2 < 8; t2++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const f4 v = f4{acc[t2][4 * j], acc[t2][4 * j + 1], acc[t2][4 * j + 2], acc[t2][4 * j + 3]};
+                *reinterpret_cast<f4*>(&out[32 * t2 + 8 * j + 4 * hh]) = empty ? f4{0.f, 0.f, 0.f, 0.f} : v;
+            }
+        if (hh == 0) {
+            out[256] = empty ? -1e20f : m_ref;
+            out[257] = empty ? 0.0f : l_row;
+        }
+    }
+}
+
 // Merge of the key splits, normalisation and gate: one block per (query,
 // head) row, thread = dim; every thread walks the row's n_split (m, l) pairs
 // (the same addresses for the whole block) and its own acc column.
@@ -487,10 +680,17 @@ hipError_t launch_ring_gather(const GatherArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
+namespace {
+// Few query rows (a handful of queries, e.g. the one after a compression
+// event): the 16-row kernel, two blocks per CU (more, shorter splits); many:
+// the 32-row kernel (half the LDS operand traffic per flop).
+bool few_rows(int n_rows) { return n_rows <= 128; }
+}  // namespace
+
 int prefill_splits(int n_q, int n_rep, int h_kv, int n_k, int* keys_per_split) {
-    // Blocks that run at once: 2 per CU (72 KB of LDS each).  The split
-    // count fills that many slots in one round: a few blocks past a round
-    // cost a whole extra round.
+    // Blocks that run at once: 2 per CU for the 16-row kernel (72 KB of LDS
+    // each), 1 for the 32-row kernel (registers).  The split count fills that
+    // many slots in one round: a few blocks past a round cost a whole round.
     static int n_cu = 0;
     if (n_cu == 0) {
         int dev = 0, v = 0;
@@ -500,9 +700,10 @@ int prefill_splits(int n_q, int n_rep, int h_kv, int n_k, int* keys_per_split) {
         else
             n_cu = 256;
     }
-    const int slots = 2 * n_cu;
-    const int mtiles = (n_q * n_rep + 15) / 16;
-    const int blocks = (mtiles + 3) / 4 * h_kv;
+    const int n_rows = n_q * n_rep;
+    const bool few = few_rows(n_rows);
+    const int slots = few ? 2 * n_cu : n_cu;
+    const int blocks = (few ? ((n_rows + 15) / 16 + 3) / 4 : (n_rows + 127) / 128) * h_kv;
     int ns = slots / blocks;
     ns = std::max(1, std::min(ns, 64));
     int per = (n_k + ns - 1) / ns;
@@ -513,9 +714,15 @@ int prefill_splits(int n_q, int n_rep, int h_kv, int n_k, int* keys_per_split) {
 }
 
 hipError_t launch_prefill_attn(const PrefillArgs& a, hipStream_t st) {
-    const int mtiles = (a.n_q * a.n_rep + 15) / 16;
-    hipLaunchKernelGGL(pf::prefill_attn_kernel, dim3((mtiles + 3) / 4, a.h_kv, a.n_split), dim3(256),
-                       0, st, a);
+    const int n_rows = a.n_q * a.n_rep;
+    if (few_rows(n_rows)) {
+        const int mtiles = (n_rows + 15) / 16;
+        hipLaunchKernelGGL(pf::prefill_attn_kernel, dim3((mtiles + 3) / 4, a.h_kv, a.n_split),
+                           dim3(256), 0, st, a);
+    } else {
+        hipLaunchKernelGGL(pf::prefill_attn32_kernel, dim3((n_rows + 127) / 128, a.h_kv, a.n_split),
+                           dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 
