@@ -151,6 +151,20 @@ def main():
     kern_gbs = c_bytes / (kern_us * 1e-6) / 1e9
     step_gbs = step_bytes / (us_layer_step * 1e-6) / 1e9
 
+    # the box's own copy bandwidth (device-to-device, 1 GiB read + 1 GiB
+    # written per copy), reported beside the vendor peak
+    xa = torch.empty(1 << 28, device=dev, dtype=torch.float32)
+    xb = torch.empty_like(xa)
+    xb.copy_(xa)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(5):
+        xb.copy_(xa)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    copy_gbs = 5 * 2 * xa.numel() * 4 / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del xa, xb
+
     traffic = {}
     tname = {"auto": "attn_ws_c3_traffic.json", "mfma-single": "attn_mfma_c3_traffic.json"}
     tpath = os.path.join(ROOT, "profiles", tname.get(args.kernel, "none"))
@@ -193,6 +207,7 @@ def main():
             "traffic_fetch_factor": traffic.get("fetch_factor"),
             "avg_kernel_us": round(kern_us, 3),
             "bytes_per_launch": c_bytes,
+            "measured_copy_gbps": round(copy_gbs, 1),
         },
     }
 
