@@ -519,8 +519,10 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
         }
         return 0;
     }
-    // Chunk length: the smallest tile count per chunk whose blocks (compressed
-    // chunks plus one window block per sequence with a window) fit the CUs.
+    // Chunk length: the smallest tile count per chunk whose compressed chunks
+    // fit the CUs.  The window blocks (one per sequence with a window) are
+    // dispatched first and are short; the chunk blocks follow longest first,
+    // so the few that wait for a CU freed by a window block are the shortest.
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) == hipSuccess)
         (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
@@ -533,14 +535,14 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
         max_tiles = std::max(max_tiles, tiles[i]);
         n_win += seqs[i].win_len > 0 ? 1 : 0;
     }
-    const int budget = std::max(1, cus - n_win);
-    int per = std::max(1, (int)((total_tiles + budget - 1) / budget));
-    auto blocks_for = [&](int p) {
-        long b = n_win;
+    int per = std::max(1, (int)((total_tiles + cus - 1) / cus));
+    auto chunks_for = [&](int p) {
+        long b = 0;
         for (int i = 0; i < n_seq; i++) b += (tiles[i] + p - 1) / p;
         return b;
     };
-    while (per < max_tiles && blocks_for(per) > cus) per++;
+    while (per < max_tiles && chunks_for(per) > cus) per++;
+    auto blocks_for = [&](int p) { return chunks_for(p) + n_win; };
     // partial layout: sequence i owns H_q x np_i triples from float offset off_i
     static thread_local std::vector<khq::AttnArgs> h_args;
     static thread_local std::vector<khq::FinishArgs> h_fin;
@@ -596,7 +598,7 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
         a.ring_cap = ring;
         khq::fill_rope_table(a);
         h_args[i] = a;
-        for (int c = 0; c < np[i]; c++) h_map.push_back(int2{i, c});
+        if (np[i] > chunks[i]) h_map.push_back(int2{i, chunks[i]});  // window block
         khq::FinishArgs f{};
         f.part = ws + off[i];
         f.n_parts = np[i];
@@ -613,6 +615,18 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
         f.eps = 1e-8f;
         f.out = static_cast<__half*>(q.out);
         h_fin[i] = f;
+    }
+    {
+        // chunk blocks after the window blocks, longest first
+        std::vector<std::pair<int, int2>> cb;
+        for (int i = 0; i < n_seq; i++)
+            for (int c = 0; c < chunks[i]; c++)
+                cb.push_back({std::min(per, tiles[i] - c * per), int2{i, c}});
+        std::stable_sort(cb.begin(), cb.end(),
+                         [](const std::pair<int, int2>& x, const std::pair<int, int2>& y) {
+                             return x.first > y.first;
+                         });
+        for (const auto& x : cb) h_map.push_back(x.second);
     }
     e = hipMemcpyAsync(d_args, h_args.data(), n_seq * sizeof(khq::AttnArgs),
                        hipMemcpyHostToDevice, stream);
