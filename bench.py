@@ -54,8 +54,10 @@ def parse():
                     help="payload: seeded uniform-random packed codes with outlier counts "
                          "~U[0,50] (the config's data, default) or the library's compression "
                          "of N(0,1) K/V rows")
-    ap.add_argument("--config", choices=["c3", "c4", "c5"], default="c3",
-                    help="c3: the headline 32K-context step (default); c4: 32 ragged "
+    ap.add_argument("--config", choices=["c1", "c2", "c3", "c4", "c5"], default="c3",
+                    help="c1: the uncompressed fp16 GQA baseline over 512 positions; c2: "
+                         "the 512-token two-region step (384 compressed + 128 raw); "
+                         "c3: the headline 32K-context step (default); c4: 32 ragged "
                          "sequences per layer-step in one batched call; c5: a 128-token "
                          "chunked-prefill step after 8,192 tokens")
     ap.add_argument("--counters-run", action="store_true",
@@ -77,6 +79,8 @@ def main():
     from khq import _lib, ops, synth
 
     _lib.call("khq_select_kernel", ["auto", "portable", "mfma-single"].index(args.kernel))
+    if args.config in ("c1", "c2"):
+        return bench_small(args)
     if args.config == "c4":
         return bench_c4(args)
     if args.config == "c5":
@@ -407,6 +411,89 @@ def bench_c5(args):
         },
     }
     print(json.dumps(result), flush=True)
+
+
+def bench_small(args):
+    """Configs 1 and 2, small and launch-bound (reported in µs, with HBM GB/s
+    for the record).  C1: the uncompressed fp16 GQA decode baseline
+    (launch_khq_gqa_attn_fp16) over 512 cached positions per layer.  C2: the
+    fused two-region step with 384 compressed rows (seeded uniform-random
+    codes) and 128 raw ring tokens per layer."""
+    import torch
+
+    from khq import ops, synth
+    from khq.centroids import synthetic_layer
+
+    dev = "cuda"
+    scale = 1.0 / 16.0
+    layers = []
+    for l in range(args.layers):
+        g = torch.Generator(device=dev)
+        g.manual_seed(400000 + l)
+        q = synth.q_gate(H_Q, seed=500000 + l, device=dev)
+        out = torch.empty((H_Q, D), device=dev, dtype=torch.float16)
+        if args.config == "c1":
+            k = torch.randn((512, H_KV, D), generator=g, device=dev).half()
+            v = torch.randn((512, H_KV, D), generator=g, device=dev).half()
+            layers.append((q, k, v, out))
+        else:
+            cents = ops.Centroids(synthetic_layer(l, seed=1234), dev)
+            pay = ops.Payload(384 * H_KV, dev)
+            for kk, vv in synth.random_rows(384 * H_KV, seed=600000 + l, device=dev).items():
+                getattr(pay, kk).copy_(vv)
+            rk = torch.randn((RING, H_KV, D), generator=g, device=dev).half()
+            rv = torch.randn((RING, H_KV, D), generator=g, device=dev).half()
+            layers.append((q, pay, cents, rk, rv, out))
+
+    def step():
+        for L in layers:
+            if args.config == "c1":
+                q, k, v, out = L
+                ops.gqa_attn(q, k, v, out, seq_len=512, H_q=H_Q, H_kv=H_KV, scale=scale,
+                             check=False)
+            else:
+                q, pay, cents, rk, rv, out = L
+                ops.attn_step(q, pay, cents, rk, rv, out, H_q=H_Q, H_kv=H_KV, c_len=384,
+                              win_start=384 % RING, win_len=128, ring_cap=RING, scale=scale,
+                              check=False)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = e0.elapsed_time(e1) / args.steps
+    us_layer = ms_step * 1000.0 / args.layers
+    if args.config == "c1":
+        nbytes = 512 * H_KV * D * 2 * 2
+        workload = f"C1: {args.layers} layers x 512 fp16 cached positions, H_q 24 / H_kv 4, D 256"
+        metric = "uncompressed fp16 GQA decode baseline us/layer-step (512 ctx)"
+    else:
+        nbytes = 384 * H_KV * 220 + 128 * H_KV * D * 2 * 2
+        workload = (f"C2: {args.layers} layers x (384 compressed + 128 raw) tokens, "
+                    "fused two-region step")
+        metric = "KHQ decode attn us/layer-step @512 ctx"
+    gbs = nbytes / (us_layer * 1e-6) / 1e9
+    result = {
+        "metric": metric, "value": round(us_layer, 3), "unit": "us/layer-step", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16-in/f32-acc" if args.config == "c1" else "f32",
+        "data": "synthetic: N(0,1) fp16 K/V" if args.config == "c1" else
+                "synthetic: seeded uniform-random packed codes, N(0,1) fp16 ring",
+        "config": {"workload": workload, "layers": args.layers, "parallelism": "1 GPU"},
+        "bytes_per_layer_step": nbytes,
+        "roofline": {"bound": "hbm", "kernel": "whole layer-step (launch-bound)",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result))
 
 
 def bench_c4(args):

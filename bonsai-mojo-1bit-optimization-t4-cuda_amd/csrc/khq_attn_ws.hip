@@ -847,16 +847,167 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
     PHASE(21);
 }
 
-// ------------------------------------------------------------ window block
-// The raw ring window (fp16, K already roped) for all 24 query heads, in the
-// block after the last compressed chunk.  Wavefront w serves KV head w % 4
+// ------------------------------------------------------------ window blocks
+// The raw ring window (fp16, K already roped) of KV head hk, in one of four
+// blocks (one per KV head) after the last compressed chunk, used when the
+// launch has CUs to spare; the four write the rows of their 6 query heads
+// into the same partial.  Wavefront w takes window rows w hw .. + hw - 1
+// (hw = 16 or 32, win_len <= 256); every K and V load of its rows is issued
+// at entry, so the block waits for memory once:
+//   scores q.k on MFMA (A = the 6 query rows, B = K rows, exact fp16, fp32
+//   accumulate) into LDS;
+//   softmax per query head over the whole window (wavefront i < 6 takes head i);
+//   P x V on the vector ALUs, lane l holding dims 4 l .. 4 l + 3, then the 8
+//   wavefronts' numerators are summed through LDS.
+constexpr int NWIN = 4;  // window blocks per sequence
+__device__ __forceinline__ void window_block(const AttnArgs& a, Smem& S, int part_idx, int hk) {
+    constexpr int WMAX = 256;
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    const int li = lane & 15, lg = lane >> 4;
+    const int wl = a.win_len;
+    const int hw = wl > 128 ? 32 : 16;  // rows per wavefront
+    const int r_lo = wv * hw, r_hi = min(wl, r_lo + hw);
+    float* sp = reinterpret_cast<float*>(S.cb);  // [6][WMAX] scores, then weights
+    float* sml = sp + 6 * WMAX;                  // [6][2] max, sum
+    float* sacc = sml + 16;                      // [8][6][256] numerators per wavefront
+    auto slot_of = [&](int s) {
+        const int x = a.win_start + s;
+        return x >= a.ring_cap ? x - a.ring_cap : x;
+    };
+    // ---- all loads first: q rows, this wavefront's K rows and V rows
+    h8 Aqk[8];
+    {
+        const __half* qrow = a.q + (size_t)(hk * 6 + min(li, 5)) * 512;
+#pragma unroll
+        for (int st = 0; st < 8; st++) {
+            const uint4 v = ldg<uint4>(qrow + 32 * st + 8 * lg);
+            Aqk[st] = __builtin_bit_cast(h8, li < 6 ? v : uint4{0u, 0u, 0u, 0u});
+        }
+    }
+    const int last = max(wl - 1, 0);
+    // ring rows through buffer loads (32-bit offsets): K rows of both tiles and
+    // the V rows of the first 16 at entry, the other 16 V rows (32-row
+    // wavefronts) during the scores
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+    const uint32_t ring_bytes = (uint32_t)a.ring_cap * a.h_kv * 512;
+    const rsrc_t rsk = make_rsrc(a.ring_k, ring_bytes);
+    const rsrc_t rsv = make_rsrc(a.ring_v, ring_bytes);
+    auto row_off = [&](int s) { return ((uint32_t)slot_of(min(s, last)) * a.h_kv + hk) * 512; };
+    u4v kv[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const uint32_t o = row_off(r_lo + 16 * u + li) + 16 * lg;
+#pragma unroll
+        for (int st = 0; st < 8; st++)
+            kv[u][st] = (u == 0 || hw == 32) ? __builtin_amdgcn_raw_buffer_load_b128(rsk, o, 64 * st, 0)
+                                             : u4v{0u, 0u, 0u, 0u};
+    }
+    u2v vr[16];
+    auto load_v = [&](int base) {
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+            vr[u] = __builtin_amdgcn_raw_buffer_load_b64(rsv, row_off(base + u) + 8 * lane, 0, 0);
+    };
+    float acc[6][4];
+#pragma unroll
+    for (int i = 0; i < 6; i++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[i][c] = 0.0f;
+    load_v(r_lo);
+    // ---- scores of this wavefront's rows
+#pragma unroll
+    for (int u = 0; u < 2; u++) {  // the second tile only for 32-row wavefronts
+        const int s = r_lo + 16 * u + li;
+        f4 sacc4 = f4{0.f, 0.f, 0.f, 0.f};
+        if (u == 0 || hw == 32) {
+#pragma unroll
+            for (int st = 0; st < 8; st++)
+                sacc4 = mfma32(Aqk[st], __builtin_bit_cast(h8, kv[u][st]), sacc4);
+        }
+        // C rows 4 lg + c = query head, column li = row s
+        if (lg < 2) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int hd = 4 * lg + c;
+                if (hd < 6 && s < r_hi) sp[hd * WMAX + s] = sacc4[c] * a.sc;
+            }
+        }
+    }
+    __syncthreads();
+    // ---- softmax: wavefront i < 6 owns query head i
+    if (wv < 6) {
+        float* row = sp + wv * WMAX;
+        float m = -INFINITY;
+        for (int s = lane; s < wl; s += 64) m = fmaxf(m, row[s]);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        float l = 0.0f;
+        for (int s = lane; s < wl; s += 64) {
+            const float p = __expf(row[s] - m);
+            row[s] = p;
+            l += p;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
+        if (lane == 0) {
+            sml[wv * 2 + 0] = m;
+            sml[wv * 2 + 1] = l;
+        }
+    }
+    __syncthreads();
+    // ---- P x V over this wavefront's rows (rows past r_hi weigh 0)
+    auto pv16 = [&](int base) {
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const bool ok = base + u < r_hi;
+            const int su = min(base + u, WMAX - 1);
+            const h4 vh = __builtin_bit_cast(h4, vr[u]);
+#pragma unroll
+            for (int i = 0; i < 6; i++) {
+                const float p = ok ? sp[i * WMAX + su] : 0.0f;
+#pragma unroll
+                for (int c = 0; c < 4; c++) acc[i][c] = fmaf(p, (float)vh[c], acc[i][c]);
+            }
+        }
+    };
+    pv16(r_lo);
+    if (hw == 32) {
+        load_v(r_lo + 16);
+        pv16(r_lo + 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 6; i++)
+        *reinterpret_cast<f4*>(&sacc[(wv * 6 + i) * 256 + 4 * lane]) =
+            f4{acc[i][0], acc[i][1], acc[i][2], acc[i][3]};
+    __syncthreads();
+    // ---- sum the 8 wavefronts: thread t takes dims of (head, dim) pairs t, t + 512, t + 1024
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        const int e = tid + 512 * j;  // e = head * 256 + dim
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 8; w++) v += sacc[w * 6 * 256 + e];
+        const int i = e >> 8, d = e & 255;
+        float* out = a.part + ((size_t)(hk * 6 + i) * a.part_stride + part_idx) * 258;
+        stg<float>(&out[d], v);
+        if (d == 0) {
+            stg<float>(&out[256], sml[i * 2 + 0]);
+            stg<float>(&out[257], sml[i * 2 + 1]);
+        }
+    }
+}
+
+// The raw ring window (fp16, K already roped) for all 24 query heads in one
+// block (used when the chunks leave no CU for one block per KV head: the
+// chunks then take several tiles each and hide it).  Wavefront w serves KV head w % 4
 // and half w / 4 of the window rows (win_len <= 256):
 //   scores q.k on MFMA (A = the 6 query rows of the group, B = K rows, both
 //   exact fp16, fp32 accumulate) into LDS;
 //   softmax per query head over the whole window in LDS;
 //   P x V on the vector ALUs, lane l holding dims 4 l .. 4 l + 3;
 // then the two halves of each KV head are added into one partial triple.
-__device__ void window_block(const AttnArgs& a, Smem& S, int part_idx) {
+__device__ void window_block_all(const AttnArgs& a, Smem& S, int part_idx) {
     constexpr int WMAX = 256;
     const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
     const int li = lane & 15, lg = lane >> 4;
@@ -988,8 +1139,11 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
     const int wv = tid >> 6;
     const int h = wv & 3;
     const int lane = tid & 63;
-    if (chunk >= n_chunks) {  // the block after the compressed chunks
-        window_block(a, S, a.part_offset + n_chunks);
+    if (chunk >= n_chunks) {  // the window block(s) after the compressed chunks
+        if (a.win_blocks == NWIN)
+            window_block(a, S, a.part_offset + n_chunks, chunk - n_chunks);
+        else
+            window_block_all(a, S, a.part_offset + n_chunks);
         return;
     }
     const int c_len = a.c_len;
@@ -1168,8 +1322,18 @@ hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks, 
         if (e != hipSuccess) return e;
         configured = true;
     }
-    const int blocks = n_chunks + (a.win_len > 0 ? 1 : 0);
+    // four window blocks when they fit beside the chunks, else one (it is
+    // hidden behind chunks of several tiles then)
+    static int n_cu = 0;
+    if (n_cu == 0) {
+        int dev = 0, v = 0;
+        n_cu = (hipGetDevice(&dev) == hipSuccess &&
+                hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+                   ? v : 256;
+    }
     AttnArgs b = a;
+    b.win_blocks = n_chunks + ws::NWIN <= n_cu ? ws::NWIN : 1;
+    const int blocks = n_chunks + (a.win_len > 0 ? b.win_blocks : 0);
     fill_rope_table(b);
     hipLaunchKernelGGL(ws::attn_ws_kernel, dim3(blocks), dim3(ws::NTHR), smem, st, b,
                        tiles_per_chunk, n_chunks);

@@ -542,7 +542,7 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
         return b;
     };
     while (per < max_tiles && chunks_for(per) > cus) per++;
-    auto blocks_for = [&](int p) { return chunks_for(p) + n_win; };
+    auto blocks_for = [&](int p) { return chunks_for(p) + 4 * n_win; };
     // partial layout: sequence i owns H_q x np_i triples from float offset off_i
     static thread_local std::vector<khq::AttnArgs> h_args;
     static thread_local std::vector<khq::FinishArgs> h_fin;
@@ -596,9 +596,11 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
         a.win_start = q.win_start % ring;
         a.win_len = q.win_len;
         a.ring_cap = ring;
+        a.win_blocks = 4;
         khq::fill_rope_table(a);
         h_args[i] = a;
-        if (np[i] > chunks[i]) h_map.push_back(int2{i, chunks[i]});  // window block
+        if (np[i] > chunks[i])  // window blocks, one per KV head
+            for (int w = 0; w < 4; w++) h_map.push_back(int2{i, chunks[i] + w});
         khq::FinishArgs f{};
         f.part = ws + off[i];
         f.n_parts = np[i];

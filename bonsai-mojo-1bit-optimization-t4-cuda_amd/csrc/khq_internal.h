@@ -36,6 +36,7 @@ struct AttnArgs {
     const __half* ring_k;
     const __half* ring_v;
     int win_start, win_len, ring_cap;
+    int win_blocks;  // window blocks after the chunks: 4 (one per KV head) or 1 (all heads)
     // RoPE table of the wavefront-specialised kernel, [lane group g][3][u]:
     // freq of dim pair m = 16 (u / 4) + 4 g + u % 4, cos and sin of 16 freq
     // (filled by the launchers from rope_base).
