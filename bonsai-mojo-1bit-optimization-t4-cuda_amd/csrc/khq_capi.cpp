@@ -460,35 +460,10 @@ int khq_decompress_fp16(const void* k_payload, const void* v_payload, const void
 int khq_prefill_attn_fp16(const void* q_gate, const void* k, const void* vt, int ld_vt, int n_k,
                           int n_q, int vis0, int H_q, int H_kv, float scale, void* out,
                           hipStream_t stream) {
-    if (!q_gate || !k || !vt || !out || n_k <= 0 || n_q <= 0 || vis0 < 1) return -100;
-    if (H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || ld_vt % 8 != 0 ||
-        ld_vt < (n_k + 15) / 16 * 16)
-        return -100;
-    const int n_rep = H_q / H_kv;
-    int per = 0;
-    const int ns = khq::prefill_splits(n_q, n_rep, H_kv, n_k, &per);
-    float* ws = nullptr;
-    hipError_t e = workspace((size_t)n_q * H_q * ns * 258 * sizeof(float), &ws);
-    if (e != hipSuccess) return rc_of(e);
-    khq::PrefillArgs a{};
-    a.q = static_cast<const __half*>(q_gate);
-    a.k = static_cast<const __half*>(k);
-    a.vt = static_cast<const __half*>(vt);
-    a.part = ws;
-    a.ld_vt = ld_vt;
-    a.n_k = n_k;
-    a.n_q = n_q;
-    a.vis0 = vis0;
-    a.h_kv = H_kv;
-    a.n_rep = n_rep;
-    a.n_split = ns;
-    a.keys_per_split = per;
-    a.sc = scale;
-    e = khq::launch_prefill_attn(a, stream);
-    if (e != hipSuccess) return rc_of(e);
-    return rc_of(khq::launch_prefill_merge(ws, static_cast<const __half*>(q_gate),
-                                           static_cast<__half*>(out), n_q * H_q, ns, 1e-8f,
-                                           stream));
+    if (!q_gate || !k || !vt || !out) return -100;
+    return khq::prefill_attn_run(static_cast<const __half*>(q_gate), static_cast<const __half*>(k),
+                                 static_cast<const __half*>(vt), ld_vt, n_k, n_q, vis0, H_q, H_kv,
+                                 scale, static_cast<__half*>(out), stream, 0, 0, 0, 0, 0);
 }
 
 int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centroids_k,
@@ -645,3 +620,51 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
 }
 
 }  // extern "C"
+
+namespace khq {
+
+int prefill_attn_run(const __half* q_gate, const __half* k, const __half* vt, int ld_vt, int n_k,
+                     int n_q, int vis0, int H_q, int H_kv, float scale, __half* out,
+                     hipStream_t stream, int q_b, int hole_lo, int hole_hi, int ex_lo, int ex_hi) {
+    if (n_k <= 0 || n_q <= 0 || vis0 < 1) return -100;
+    if (q_b < 0 || q_b > n_q || hole_lo < 0 || hole_hi < hole_lo || hole_hi > n_k ||
+        ex_hi < ex_lo || (ex_hi > ex_lo && ex_lo < n_k) ||
+        (q_b > 0 && ex_hi - ex_lo != hole_hi - hole_lo))
+        return -100;
+    const int n_tot = std::max(n_k, ex_hi);
+    if (H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || ld_vt % 8 != 0 ||
+        ld_vt < (n_tot + 15) / 16 * 16)
+        return -100;
+    const int n_rep = H_q / H_kv;
+    int per = 0;
+    const int ns = prefill_splits(n_q, n_rep, H_kv, n_tot, &per);
+    float* ws = nullptr;
+    hipError_t e = workspace((size_t)n_q * H_q * ns * 258 * sizeof(float), &ws);
+    if (e != hipSuccess) return rc_of(e);
+    PrefillArgs a{};
+    a.q = q_gate;
+    a.k = k;
+    a.vt = vt;
+    a.part = ws;
+    a.ld_vt = ld_vt;
+    a.n_k = n_k;
+    a.n_q = n_q;
+    a.vis0 = vis0;
+    a.h_kv = H_kv;
+    a.n_rep = n_rep;
+    a.n_split = ns;
+    a.keys_per_split = per;
+    a.sc = scale;
+    a.n_tot = n_tot;
+    a.q_b = q_b;
+    a.hole_lo = hole_lo;
+    a.hole_hi = hole_hi;
+    a.ex_lo = ex_lo;
+    a.ex_hi = ex_hi;
+    e = launch_prefill_attn(a, stream);
+    if (e != hipSuccess) return rc_of(e);
+    return rc_of(launch_prefill_merge(ws, q_gate, out, n_q * H_q, ns, 1e-8f, stream));
+}
+
+}  // namespace khq
+

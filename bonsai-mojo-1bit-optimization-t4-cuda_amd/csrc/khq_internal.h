@@ -149,6 +149,10 @@ struct GatherArgs {
     __half* wr_k;
     __half* wr_v;
     __half* wr_u;
+    // Second job (grid z = 1, chunk mode only): side_n tokens whose first
+    // side_from_src come from ring slots (side_start + t) % ring_cap and the
+    // rest from src rows t - side_from_src, written to keys side_key0 + t.
+    int side_n, side_start, side_from_src, side_key0;
 };
 // n_q queries (q_gate rows [n_q][H_q][512]) over dense keys [0, n_k); query j
 // sees keys [0, min(n_k, vis0 + j)).  Partial triple of (query j, head hq,
@@ -160,11 +164,23 @@ struct PrefillArgs {
     float* part;
     int ld_vt, n_k, n_q, vis0, h_kv, n_rep, n_split, keys_per_split;
     float sc;
+    // Keys are indices [0, n_tot), n_tot >= n_k.  Queries j < q_b (the run
+    // before a compression event) lose [hole_lo, hole_hi) and see key
+    // ex_lo + i for position hole_lo + i (when that position is below their
+    // causal limit) instead: the raw copies of the compressed chunk, placed
+    // past n_k, while the main key space holds its decoded rows for the
+    // queries after the event.  q_b = 0: no such run.
+    int n_tot, q_b, hole_lo, hole_hi, ex_lo, ex_hi;
 };
 hipError_t launch_decompress(const DecompArgs& a, hipStream_t st);
 hipError_t launch_ring_gather(const GatherArgs& a, hipStream_t st);
 int prefill_splits(int n_q, int n_rep, int h_kv, int n_k, int* keys_per_split);
 hipError_t launch_prefill_attn(const PrefillArgs& a, hipStream_t st);
+// Prefill attention plus merge and gate through the shared workspace; the
+// hole / extra ranges as in PrefillArgs (all zero: plain causal prefill).
+int prefill_attn_run(const __half* q_gate, const __half* k, const __half* vt, int ld_vt, int n_k,
+                     int n_q, int vis0, int H_q, int H_kv, float scale, __half* out,
+                     hipStream_t stream, int q_b, int hole_lo, int hole_hi, int ex_lo, int ex_hi);
 // Merge of n_split partial triples per row, / (den + eps), sigmoid gate from
 // q_gate row r (f16 [r][512], gate at 256..511): out f16 [r][256].
 hipError_t launch_prefill_merge(const float* part, const __half* q_gate, __half* out, int n_rows,

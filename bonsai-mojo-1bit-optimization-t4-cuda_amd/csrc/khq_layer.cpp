@@ -242,7 +242,9 @@ int khq_layer_prefill(khq_layer* L, const void* q_gate, const void* k_roped, con
     if (!L || !q_gate || !k_roped || !v || !k_unroped || !out || n <= 0) return -100;
     const int kv = L->H_kv * kD;
     if (!L->dk) {  // dense key space for up to cap + 256 positions
-        L->d_keys = L->cap + kRing + 64;
+        // positions up to cap + ring, then the raw copy of one compressed
+        // chunk (the extra keys of a combined launch) past them
+        L->d_keys = L->cap + kRing + kChunk + 64;
         L->d_ld = (L->d_keys + 63) / 64 * 64;
         const size_t kb = (size_t)L->d_keys * kv * sizeof(__half);
         const size_t vb = (size_t)L->H_kv * kD * L->d_ld * sizeof(__half);
@@ -253,6 +255,10 @@ int khq_layer_prefill(khq_layer* L, const void* q_gate, const void* k_roped, con
             L->dvt = nullptr;
             return -100;
         }
+        // finite contents everywhere: padding keys of a launch get P = 0
+        if (hipMemsetAsync(L->dk, 0, kb, stream) != hipSuccess ||
+            hipMemsetAsync(L->dvt, 0, vb, stream) != hipSuccess)
+            return -100;
         L->dec_hi = 0;
     }
     const __half* qg = static_cast<const __half*>(q_gate);
@@ -267,8 +273,16 @@ int khq_layer_prefill(khq_layer* L, const void* q_gate, const void* k_roped, con
         const int m = std::min(n - done, kRing - (L->write_pos - L->boundary));
         if (m <= 0) return -102;
         const int w0 = L->write_pos;
+        // An event due at the sub-chunk's last query and at none before it
+        // (the usual case: the sub-chunk fills the ring to the watermark):
+        // the event runs first and one attention launch serves every query;
+        // the earlier queries read the chunk's raw rows from a copy past the
+        // sub-chunk's keys instead of its decoded rows.
+        const bool combine = m >= 2 && event_due(L, w0 + m) && !event_due(L, w0 + m - 1);
+        const int c_a = L->boundary;
+        const int side0 = (w0 + m + 15) / 16 * 16;
         // the sub-chunk's tokens go to their ring slots and to the dense key
-        // space in one launch
+        // space in one launch (with the raw copy as a second job)
         khq::GatherArgs cw{};
         cw.out_k = L->dk;
         cw.out_vt = L->dvt;
@@ -284,6 +298,12 @@ int khq_layer_prefill(khq_layer* L, const void* q_gate, const void* k_roped, con
         cw.wr_k = L->ring_k;
         cw.wr_v = L->ring_v;
         cw.wr_u = L->ring_u;
+        if (combine) {
+            cw.side_n = kChunk;
+            cw.side_start = c_a % kRing;
+            cw.side_from_src = std::min(w0 - c_a, kChunk);
+            cw.side_key0 = side0;
+        }
         hipError_t e = khq::launch_ring_gather(cw, stream);
         if (e != hipSuccess) return (int)e;
         if (L->raw_lo < L->raw_hi && L->raw_hi == w0)
@@ -292,19 +312,8 @@ int khq_layer_prefill(khq_layer* L, const void* q_gate, const void* k_roped, con
             L->raw_lo = w0;
             L->raw_hi = w0 + m;
         }
-        int j = 0;
-        while (j < m) {
-            // query j appends position w0 + j; an event fires before its attention
-            if (event_due(L, w0 + j + 1)) {
-                const int rc = compress_event(L, stream);
-                if (rc) return rc;
-            }
-            int je = j + 1;
-            while (je < m && !event_due(L, w0 + je + 1)) je++;
-            // queries j .. je - 1 share c_len = boundary
-            const int c_len = L->boundary;
-            const int n_k = w0 + je;
-            if (n_k - c_len > kRing) return -102;
+        // decoded rows up to c_len, raw rows [c_len, n_k) in the dense key space
+        auto prepare = [&](int c_len, int n_k) -> int {
             if (L->dec_hi < c_len) {
                 const int d0 = L->dec_hi, nd = c_len - d0;
                 const int rc = khq_decompress_fp16(
@@ -317,9 +326,9 @@ int khq_layer_prefill(khq_layer* L, const void* q_gate, const void* k_roped, con
                 // V^T columns up to the decode's last 16-column block are rewritten
                 L->raw_lo = std::max(L->raw_lo, d0 + (nd + 15) / 16 * 16);
             }
-            // raw tokens [c_len, n_k) in the dense key space: copied from the
-            // ring unless already there (with every raw token after them, so
-            // the copy's padded last block clobbers nothing still needed)
+            // raw tokens [c_len, n_k): copied from the ring unless already
+            // there (with every raw token after them, so the copy's padded
+            // last block clobbers nothing still needed)
             if (!(L->raw_lo <= c_len && L->raw_hi >= n_k && L->raw_lo < L->raw_hi)) {
                 const int g_hi = std::max(n_k, L->raw_lo < L->raw_hi && L->raw_lo <= n_k ? L->raw_hi : n_k);
                 khq::GatherArgs g{};
@@ -333,15 +342,44 @@ int khq_layer_prefill(khq_layer* L, const void* q_gate, const void* k_roped, con
                 g.ring_cap = kRing;
                 g.key0 = c_len;
                 g.ld_vt = L->d_ld;
-                e = khq::launch_ring_gather(g, stream);
-                if (e != hipSuccess) return (int)e;
+                const hipError_t ge = khq::launch_ring_gather(g, stream);
+                if (ge != hipSuccess) return (int)ge;
                 L->raw_lo = c_len;
                 L->raw_hi = g_hi;
             }
-            const int rc = khq_prefill_attn_fp16(qg + (size_t)(done + j) * L->H_q * 2 * kD, L->dk,
-                                                 L->dvt, L->d_ld, n_k, je - j, w0 + j + 1, L->H_q,
-                                                 L->H_kv, scale,
-                                                 o + (size_t)(done + j) * L->H_q * kD, stream);
+            return 0;
+        };
+        if (combine) {
+            int rc = compress_event(L, stream);
+            if (rc) return rc;
+            const int c_b = L->boundary;  // c_a + kChunk
+            const int n_k = w0 + m;
+            rc = prepare(c_b, n_k);
+            if (rc) return rc;
+            rc = khq::prefill_attn_run(qg + (size_t)done * L->H_q * 2 * kD, L->dk, L->dvt,
+                                       L->d_ld, n_k, m, w0 + 1, L->H_q, L->H_kv, scale,
+                                       o + (size_t)done * L->H_q * kD, stream, m - 1, c_a, c_b,
+                                       side0, side0 + (c_b - c_a));
+            if (rc) return rc;
+        }
+        int j = combine ? m : 0;
+        while (j < m) {
+            // query j appends position w0 + j; an event fires before its attention
+            if (event_due(L, w0 + j + 1)) {
+                const int rc = compress_event(L, stream);
+                if (rc) return rc;
+            }
+            int je = j + 1;
+            while (je < m && !event_due(L, w0 + je + 1)) je++;
+            // queries j .. je - 1 share c_len = boundary
+            const int c_len = L->boundary;
+            const int n_k = w0 + je;
+            if (n_k - c_len > kRing) return -102;
+            int rc = prepare(c_len, n_k);
+            if (rc) return rc;
+            rc = khq_prefill_attn_fp16(qg + (size_t)(done + j) * L->H_q * 2 * kD, L->dk, L->dvt,
+                                       L->d_ld, n_k, je - j, w0 + j + 1, L->H_q, L->H_kv, scale,
+                                       o + (size_t)(done + j) * L->H_q * kD, stream);
             if (rc) return rc;
             j = je;
         }

@@ -209,40 +209,93 @@ __global__ __launch_bounds__(BLK_THR) void ring_gather_kernel(GatherArgs a) {
     const int h = blockIdx.y;
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t_blk = blockIdx.x * TOK_BLK;
+    // job 0: the gather / chunk write; job 1: the side copy (block-uniform)
+    const bool side = blockIdx.z == 1;
+    const int n = side ? a.side_n : a.n;
+    const int key0 = side ? a.side_key0 : a.key0;
+    if (t_blk >= n) return;
     {
         const int tl = wv;
         const int t = t_blk + tl;
-        if (t >= a.n) {
+        if (t >= n) {
 #pragma unroll
             for (int c = 0; c < 4; c++) sv[4 * lane + c][tl] = (_Float16)0.0f;
             goto staged;
         }
-        int slot = a.win_start + t;
-        slot = slot >= a.ring_cap ? slot - a.ring_cap : slot;
-        const size_t rs = ((size_t)slot * a.h_kv + h) * 256 + 4 * lane;
         uint2 kw, vw;
-        if (a.src_k) {
-            const size_t cs = ((size_t)t * a.h_kv + h) * 256 + 4 * lane;
-            kw = *reinterpret_cast<const uint2*>(a.src_k + cs);
-            vw = *reinterpret_cast<const uint2*>(a.src_v + cs);
-            *reinterpret_cast<uint2*>(a.wr_k + rs) = kw;
-            *reinterpret_cast<uint2*>(a.wr_v + rs) = vw;
-            if (a.wr_u) *reinterpret_cast<uint2*>(a.wr_u + rs) = *reinterpret_cast<const uint2*>(a.src_u + cs);
+        if (side) {
+            if (t >= a.side_from_src) {
+                const size_t cs = ((size_t)(t - a.side_from_src) * a.h_kv + h) * 256 + 4 * lane;
+                kw = *reinterpret_cast<const uint2*>(a.src_k + cs);
+                vw = *reinterpret_cast<const uint2*>(a.src_v + cs);
+            } else {
+                int slot = a.side_start + t;
+                slot = slot >= a.ring_cap ? slot - a.ring_cap : slot;
+                const size_t rs = ((size_t)slot * a.h_kv + h) * 256 + 4 * lane;
+                kw = *reinterpret_cast<const uint2*>(a.wr_k + rs);
+                vw = *reinterpret_cast<const uint2*>(a.wr_v + rs);
+            }
         } else {
-            kw = *reinterpret_cast<const uint2*>(a.ring_k + rs);
-            vw = *reinterpret_cast<const uint2*>(a.ring_v + rs);
+            int slot = a.win_start + t;
+            slot = slot >= a.ring_cap ? slot - a.ring_cap : slot;
+            const size_t rs = ((size_t)slot * a.h_kv + h) * 256 + 4 * lane;
+            if (a.src_k) {
+                const size_t cs = ((size_t)t * a.h_kv + h) * 256 + 4 * lane;
+                kw = *reinterpret_cast<const uint2*>(a.src_k + cs);
+                vw = *reinterpret_cast<const uint2*>(a.src_v + cs);
+                *reinterpret_cast<uint2*>(a.wr_k + rs) = kw;
+                *reinterpret_cast<uint2*>(a.wr_v + rs) = vw;
+                if (a.wr_u) *reinterpret_cast<uint2*>(a.wr_u + rs) = *reinterpret_cast<const uint2*>(a.src_u + cs);
+            } else {
+                kw = *reinterpret_cast<const uint2*>(a.ring_k + rs);
+                vw = *reinterpret_cast<const uint2*>(a.ring_v + rs);
+            }
         }
-        *reinterpret_cast<uint2*>(a.out_k + ((size_t)(a.key0 + t) * a.h_kv + h) * 256 + 4 * lane) = kw;
+        *reinterpret_cast<uint2*>(a.out_k + ((size_t)(key0 + t) * a.h_kv + h) * 256 + 4 * lane) = kw;
         const h4 v = __builtin_bit_cast(h4, vw);
 #pragma unroll
         for (int c = 0; c < 4; c++) sv[4 * lane + c][tl] = v[c];
     }
 staged:
     __syncthreads();
-    if (a.src_k)  // chunk mode: exactly the chunk's columns (key0 is any position)
-        store_vt_cols(sv, a.out_vt, a.ld_vt, h, a.key0 + t_blk, min(TOK_BLK, a.n - t_blk));
+    if (a.src_k)  // chunk mode: exactly the written columns (key0 is any position)
+        store_vt_cols(sv, a.out_vt, a.ld_vt, h, key0 + t_blk, min(TOK_BLK, n - t_blk));
     else
-        store_vt(sv, a.out_vt, a.ld_vt, h, a.key0 + t_blk);
+        store_vt(sv, a.out_vt, a.ld_vt, h, key0 + t_blk);
+}
+
+// Visibility of the keys of one 32-key tile to one query row, as a bit mask
+// (bit i: key k0 + i): [0, vis) less the hole, plus the extra range (hole and
+// extra are empty for rows after a compression event).  Only vis and a lane
+// flag stay live; the hole and extra bounds are the launch's scalar arguments.
+__device__ __forceinline__ uint32_t bits_below(int n) {  // bits [0, n) of 32
+    return n >= 32 ? ~0u : (n <= 0 ? 0u : (1u << n) - 1u);
+}
+struct RowKeys {
+    const PrefillArgs& a;
+    int vis;
+    bool run_a;
+    __device__ __forceinline__ RowKeys(const PrefillArgs& a_, bool r_ok, int jq) : a(a_) {
+        // padding rows see every key: their scores are never written
+        vis = r_ok ? min(a.n_k, a.vis0 + jq) : a.n_tot;
+        run_a = r_ok && jq < a.q_b;
+    }
+    __device__ __forceinline__ uint32_t tile(int k0) const {
+        // selects, no branch: a divergent branch here costs the 32-row
+        // kernel about 45 registers (spilled to AGPRs)
+        const uint32_t hole = bits_below(a.hole_hi - k0) & ~bits_below(a.hole_lo - k0);
+        // extra key ex_lo + i stands for position hole_lo + i: visible below vis
+        const int ex_end = min(a.ex_hi, a.ex_lo + vis - a.hole_lo);
+        const uint32_t ex = bits_below(ex_end - k0) & ~bits_below(a.ex_lo - k0);
+        const uint32_t m = bits_below(vis - k0);
+        return run_a ? ((m & ~hole) | ex) : m;
+    }
+};
+// One past the last key any row of the block sees (rows are ordered by query).
+__device__ __forceinline__ int block_key_end(const PrefillArgs& a, int row_first, int row_last) {
+    int lim = min(a.n_k, a.vis0 + row_last / a.n_rep);
+    if (row_first / a.n_rep < a.q_b) lim = max(lim, a.ex_hi);
+    return lim;
 }
 
 // ----------------------------------------------------------- attention
@@ -277,16 +330,15 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
     const int row0 = (blockIdx.x * 4 + wv) * 16;
     const int split = blockIdx.z;
     const int k_lo = split * a.keys_per_split;
-    const int k_hi = min(a.n_k, k_lo + a.keys_per_split);
+    const int k_hi = min(a.n_tot, k_lo + a.keys_per_split);
     const int H_q = a.h_kv * a.n_rep;
     const int r = row0 + li;
     const bool r_ok = r < n_rows;
     const int jq = r_ok ? r / a.n_rep : 0;
     const int hq = h * a.n_rep + (r_ok ? r % a.n_rep : 0);
-    const int vis = r_ok ? min(a.n_k, a.vis0 + jq) : 0;
-    // the block's last visible key (rows are ordered by query)
+    const RowKeys vis(a, r_ok, jq);
     const int b_last = min((int)blockIdx.x * 64 + 63, n_rows - 1);
-    const int kt_hi = min(k_hi, min(a.n_k, a.vis0 + b_last / a.n_rep));
+    const int kt_hi = min(k_hi, block_key_end(a, blockIdx.x * 64, b_last));
 
     h8 qb[8];
     {
@@ -311,7 +363,7 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) pk[i] = pv[i] = uint4{0u, 0u, 0u, 0u};
     auto gload = [&](int k0) {
-        const int key = min(k0 + ld_key, a.n_k - 1);
+        const int key = min(k0 + ld_key, a.n_tot - 1);
         const uint4* ksrc = reinterpret_cast<const uint4*>(kg + (size_t)key * a.h_kv * 256);
         const uint4* vsrc = reinterpret_cast<const uint4*>(vg + k0);
 #pragma unroll
@@ -326,7 +378,7 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
         return 2 * i + 1 < nv ? w : (2 * i < nv ? (w & 0xFFFFu) : 0u);
     };
     auto lstore = [&](int buf, int k0) {
-        const int nv = a.n_k - k0;
+        const int nv = a.n_tot - k0;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             *reinterpret_cast<uint4*>(&ks[buf][ld_key][ld_off + 8 * i]) = pk[i];
@@ -359,10 +411,13 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
             s1 = mfma32(kb, qb[st], s1);
         }
         float sc[8], lmax = -INFINITY;
+        {
+            const uint32_t mb = vis.tile(k0) >> (4 * lg);
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            sc[c] = (k0 + 4 * lg + c < vis) ? s0[c] * a.sc : -INFINITY;
-            sc[4 + c] = (k0 + 16 + 4 * lg + c < vis) ? s1[c] * a.sc : -INFINITY;
+            for (int c = 0; c < 4; c++) {
+                sc[c] = (mb >> c) & 1u ? s0[c] * a.sc : -INFINITY;
+                sc[4 + c] = (mb >> (16 + c)) & 1u ? s1[c] * a.sc : -INFINITY;
+            }
         }
 #pragma unroll
         for (int e = 0; e < 8; e++) lmax = fmaxf(lmax, sc[e]);
@@ -455,16 +510,15 @@ void prefill_attn32_kernel(PrefillArgs a) {
     const int row0 = (blockIdx.x * 4 + wv) * 32;
     const int split = blockIdx.z;
     const int k_lo = split * a.keys_per_split;
-    const int k_hi = min(a.n_k, k_lo + a.keys_per_split);
+    const int k_hi = min(a.n_tot, k_lo + a.keys_per_split);
     const int H_q = a.h_kv * a.n_rep;
     const int r = row0 + ln;
     const bool r_ok = r < n_rows;
     const int jq = r_ok ? r / a.n_rep : 0;
     const int hq = h * a.n_rep + (r_ok ? r % a.n_rep : 0);
-    const int vis = r_ok ? min(a.n_k, a.vis0 + jq) : 0;
-    // the block's last visible key (rows are ordered by query)
+    const RowKeys vis(a, r_ok, jq);
     const int b_last = min((int)blockIdx.x * 128 + 127, n_rows - 1);
-    const int kt_hi = min(k_hi, min(a.n_k, a.vis0 + b_last / a.n_rep));
+    const int kt_hi = min(k_hi, block_key_end(a, blockIdx.x * 128, b_last));
 
     h8 qb[16];
     {
@@ -491,7 +545,7 @@ void prefill_attn32_kernel(PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) pk[i] = pv[i] = uint4{0u, 0u, 0u, 0u};
     auto gload = [&](int k0) {
-        const int key = min(k0 + ld_key, a.n_k - 1);
+        const int key = min(k0 + ld_key, a.n_tot - 1);
         const uint4* ksrc = reinterpret_cast<const uint4*>(kg + (size_t)key * a.h_kv * 256);
         const uint4* vsrc = reinterpret_cast<const uint4*>(vg + k0);
 #pragma unroll
@@ -504,7 +558,7 @@ void prefill_attn32_kernel(PrefillArgs a) {
         return 2 * i + 1 < nv ? w : (2 * i < nv ? (w & 0xFFFFu) : 0u);
     };
     auto lstore = [&](int buf, int k0) {
-        const int nv = a.n_k - k0;
+        const int nv = a.n_tot - k0;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             *reinterpret_cast<uint4*>(&ks[buf][ld_key][ld_off + 8 * i]) = pk[i];
@@ -544,11 +598,11 @@ void prefill_attn32_kernel(PrefillArgs a) {
             for (int i = 0; i < 8; i++) sc4[i & 3] = mfma3232(kop[i], qb[8 * half + i], sc4[i & 3]);
         }
         float sc[16], lmax = -INFINITY;
+        const uint32_t mb = vis.tile(k0) >> (4 * hh);
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const int key = k0 + 8 * (e >> 2) + 4 * hh + (e & 3);
+        for (int e = 0; e < 16; e++) {  // key k0 + 8 (e / 4) + 4 hh + e % 4
             const float x = (sc4[0][e] + sc4[1][e]) + (sc4[2][e] + sc4[3][e]);
-            sc[e] = key < vis ? x * a.sc : -INFINITY;
+            sc[e] = (mb >> (8 * (e >> 2) + (e & 3))) & 1u ? x * a.sc : -INFINITY;
             lmax = fmaxf(lmax, sc[e]);
         }
         // ---- raise the row's reference maximum only when needed (the row's
@@ -674,8 +728,11 @@ hipError_t launch_decompress(const DecompArgs& a, hipStream_t st) {
 }
 
 hipError_t launch_ring_gather(const GatherArgs& a, hipStream_t st) {
-    if (a.n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(pf::ring_gather_kernel, dim3((a.n + pf::TOK_BLK - 1) / pf::TOK_BLK, a.h_kv),
+    const int side = a.src_k && a.side_n > 0 ? 1 : 0;
+    const int n = std::max(a.n, side ? a.side_n : 0);
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(pf::ring_gather_kernel,
+                       dim3((n + pf::TOK_BLK - 1) / pf::TOK_BLK, a.h_kv, 1 + side),
                        dim3(pf::BLK_THR), 0, st, a);
     return hipGetLastError();
 }
