@@ -342,16 +342,24 @@ def bench_c5(args):
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     out = torch.empty((chunk, H_Q, D), device=dev, dtype=torch.float16)
-    for _ in range(args.warmup):
-        for L in fresh_layers(n_layers):
+    import gc
+
+    def run_chunk(layers):
+        for L in layers:
             L.prefill(q_c, kr_c, v_c, k_c, out, scale)
+
+    for _ in range(args.warmup):
+        run_chunk(fresh_layers(n_layers))
     ms = []
     n_steps = min(args.steps, 5)  # each step needs 16 freshly prefilled layer states
     for _ in range(n_steps):
         layers = fresh_layers(n_layers)
+        # the previous step's layers are destroyed here, outside the timed
+        # region (a destroy synchronizes the device and frees its buffers)
+        gc.collect()
+        torch.cuda.synchronize()
         e0.record(stream)
-        for L in layers:
-            L.prefill(q_c, kr_c, v_c, k_c, out, scale)
+        run_chunk(layers)
         e1.record(stream)
         torch.cuda.synchronize()
         ms.append(e0.elapsed_time(e1))
@@ -391,6 +399,7 @@ def bench_c5(args):
         "vs_baseline": None,
         "dtype": "f16-in/f32-acc",
         "timed_steps": n_steps,
+        "step_us_per_layer": [round(x * 1000.0 / n_layers, 1) for x in ms],
         "data": "synthetic: N(0,1) fp16 tokens, compressed by the library",
         "config": {
             "workload": f"C5: {n_layers} layers x one 128-token chunk at positions 8192..8319 "
