@@ -71,6 +71,23 @@ hipError_t launch_step_finish(const FinishArgs& a, int H_q, hipStream_t st);
 hipError_t launch_step_finish_batched(const FinishArgs* args, int n_seq, int H_q,
                                       hipStream_t st);
 
+// One compressor job (the arguments of launch_compress without is_v).
+struct CompressJob {
+    const __half* x;
+    const __half* d_vec;
+    const __half* rotor;
+    const __half* cents;
+    const __half* vq;
+    uint32_t* out_mask;
+    __half* out_norms;
+    __half* out_rn;
+    uint8_t* out_pay;
+    uint8_t* out_sm;
+    int n;
+    float ts, alpha;
+};
+// The K and V jobs of one compression event in one launch.
+hipError_t launch_compress_pair(const CompressJob& k, const CompressJob& v, hipStream_t st);
 hipError_t launch_compress(const __half* x, const __half* d_vec, const __half* rotor,
                            const __half* cents, const __half* vq, uint32_t* out_mask,
                            __half* out_norms, __half* out_rn, uint8_t* out_pay,

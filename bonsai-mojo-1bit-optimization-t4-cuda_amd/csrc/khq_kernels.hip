@@ -69,13 +69,13 @@ __device__ __forceinline__ void fwht256(float (&v)[4]) {
 // three order-sensitive sums (sum of squares, sum_normals/sum_cbase, the V
 // energies) are kept sequential here by staging the terms in LDS and letting
 // every lane fold them in index order.
-__global__ __launch_bounds__(256) void compress_kernel(
+__device__ __forceinline__ void compress_block(
     const __half* __restrict__ x, const __half* __restrict__ d_vec,
     const __half* __restrict__ rotor, const __half* __restrict__ cents,
     const __half* __restrict__ vq, uint32_t* __restrict__ out_mask,
     __half* __restrict__ out_norms, __half* __restrict__ out_rn,
     uint8_t* __restrict__ out_pay, uint8_t* __restrict__ out_sm, int n, float ts,
-    float alpha, int is_v) {
+    float alpha, int is_v, int bid) {
     __shared__ float s_a[4][256];
     __shared__ float s_b[4][256];
     __shared__ uint32_t s_w[4][32];
@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256) void compress_kernel(
     // K: one row per wavefront.  V: one row per block, the four wavefronts
     // search a quarter of the codebook each and all finish the row; wavefront
     // 0 writes it.
-    const int row = is_v ? (int)blockIdx.x : (int)blockIdx.x * 4 + wave;
+    const int row = is_v ? bid : bid * 4 + wave;
     const bool valid = row < n;
     const bool live = valid && (!is_v || wave == 0);
     const float f_s = 0.0625f;
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(256) void compress_kernel(
                 reinterpret_cast<uint32_t*>(out_pay + (size_t)row * 40)[lane] = s_w[wave][lane];
             if (lane == 0) {
                 out_rn[row] = __float2half(rs);
-                *reinterpret_cast<uint32_t*>(out_sm + (size_t)row * 4) = 0u;
+                if (out_sm) *reinterpret_cast<uint32_t*>(out_sm + (size_t)row * 4) = 0u;
             }
         }
         return;
@@ -306,6 +306,30 @@ __global__ __launch_bounds__(256) void compress_kernel(
         out_rn[row] = __float2half(sqrtf(st / (sv + 1e-8f)));
         *reinterpret_cast<float*>(out_sm + (size_t)row * 4) = max_res;
     }
+}
+
+__global__ __launch_bounds__(256) void compress_kernel(
+    const __half* __restrict__ x, const __half* __restrict__ d_vec,
+    const __half* __restrict__ rotor, const __half* __restrict__ cents,
+    const __half* __restrict__ vq, uint32_t* __restrict__ out_mask,
+    __half* __restrict__ out_norms, __half* __restrict__ out_rn,
+    uint8_t* __restrict__ out_pay, uint8_t* __restrict__ out_sm, int n, float ts,
+    float alpha, int is_v) {
+    compress_block(x, d_vec, rotor, cents, vq, out_mask, out_norms, out_rn, out_pay, out_sm, n, ts,
+                   alpha, is_v, (int)blockIdx.x);
+}
+
+// K and V of one compression event in one launch: blocks [0, nb_k) run the K
+// rows, the rest the V rows (the K job's shared-meta word, which the V job
+// sets, is not written).
+__global__ __launch_bounds__(256) void compress_pair_kernel(CompressJob k, CompressJob v,
+                                                            int nb_k) {
+    if ((int)blockIdx.x < nb_k)
+        compress_block(k.x, k.d_vec, k.rotor, k.cents, k.vq, k.out_mask, k.out_norms, k.out_rn,
+                       k.out_pay, nullptr, k.n, k.ts, k.alpha, 0, (int)blockIdx.x);
+    else
+        compress_block(v.x, v.d_vec, v.rotor, v.cents, v.vq, v.out_mask, v.out_norms, v.out_rn,
+                       v.out_pay, v.out_sm, v.n, v.ts, v.alpha, 1, (int)blockIdx.x - nb_k);
 }
 
 // ------------------------------------------------- compressed-region parts
@@ -840,6 +864,12 @@ hipError_t launch_compress(const __half* x, const __half* d_vec, const __half* r
     const int blocks = is_v ? n : (n + 3) / 4;
     hipLaunchKernelGGL(compress_kernel, dim3(blocks), dim3(256), 0, st, x, d_vec, rotor, cents,
                        vq, out_mask, out_norms, out_rn, out_pay, out_sm, n, ts, alpha, is_v);
+    return hipGetLastError();
+}
+
+hipError_t launch_compress_pair(const CompressJob& k, const CompressJob& v, hipStream_t st) {
+    const int nb_k = (k.n + 3) / 4;
+    hipLaunchKernelGGL(compress_pair_kernel, dim3(nb_k + v.n), dim3(256), 0, st, k, v, nb_k);
     return hipGetLastError();
 }
 

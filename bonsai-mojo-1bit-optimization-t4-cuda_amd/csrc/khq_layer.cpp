@@ -72,16 +72,16 @@ int compress_event(khq_layer* L, hipStream_t stream) {
     const int s0 = L->boundary % kRing;
     const size_t r0 = (size_t)L->boundary * L->H_kv;
     const int n = kChunk * L->H_kv;
-    int rc = launch_khq_compress_fp16(L->ring_u + (size_t)s0 * kv, L->d_k, L->rotor_k, L->cents_k,
-                                      L->cents_k, L->kmask + r0 * 16, L->knorm + r0, L->krn + r0,
-                                      L->kpay + r0 * 40, L->vsm + r0 * 4, n, kD, L->ts_k,
-                                      L->alpha_k, 0, stream);
-    if (rc) return rc;
-    rc = launch_khq_compress_fp16(L->ring_v + (size_t)s0 * kv, L->d_v, L->rotor_v, L->cents_v,
-                                  L->vq, L->kmask + r0 * 16, L->vnorm + r0, L->vrn + r0,
-                                  L->vpay + r0 * 104, L->vsm + r0 * 4, n, kD, L->ts_v,
-                                  L->alpha_v, 1, stream);
-    if (rc) return rc;
+    // K and V rows in one launch (the two jobs write disjoint outputs)
+    auto h = [](const void* p) { return static_cast<const __half*>(p); };
+    khq::CompressJob kj{L->ring_u + (size_t)s0 * kv, h(L->d_k), h(L->rotor_k), h(L->cents_k), h(L->cents_k),
+                        L->kmask + r0 * 16, L->knorm + r0, L->krn + r0, L->kpay + r0 * 40,
+                        nullptr, n, L->ts_k, L->alpha_k};
+    khq::CompressJob vj{L->ring_v + (size_t)s0 * kv, h(L->d_v), h(L->rotor_v), h(L->cents_v), h(L->vq),
+                        L->kmask + r0 * 16, L->vnorm + r0, L->vrn + r0, L->vpay + r0 * 104,
+                        L->vsm + r0 * 4, n, L->ts_v, L->alpha_v};
+    const hipError_t e = khq::launch_compress_pair(kj, vj, stream);
+    if (e != hipSuccess) return (int)e;
     L->boundary += kChunk;
     L->n_events += 1;
     return 0;
