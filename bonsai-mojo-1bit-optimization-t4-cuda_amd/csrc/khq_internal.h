@@ -191,6 +191,8 @@ struct PrefillArgs {
 };
 hipError_t launch_decompress(const DecompArgs& a, hipStream_t st);
 hipError_t launch_ring_gather(const GatherArgs& a, hipStream_t st);
+// A decode and a gather whose outputs are disjoint, in one launch.
+hipError_t launch_decompress_gather(const DecompArgs& d, const GatherArgs& g, hipStream_t st);
 int prefill_splits(int n_q, int n_rep, int h_kv, int n_k, int* keys_per_split);
 hipError_t launch_prefill_attn(const PrefillArgs& a, hipStream_t st);
 // Prefill attention plus merge and gate through the shared workspace; the

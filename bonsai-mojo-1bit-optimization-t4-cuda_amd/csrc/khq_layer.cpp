@@ -91,6 +91,36 @@ bool event_due(const khq_layer* L, int write_pos) {  // ref runtime.mojo:494-497
     return write_pos - L->boundary >= kWatermark && L->boundary + kChunk <= L->cap;
 }
 
+// Decode of rows [d0, d0 + nd) into the dense key space at the same positions.
+void decomp_args(const khq_layer* L, int d0, int nd, khq::DecompArgs* a) {
+    a->kpay = L->kpay;
+    a->vpay = L->vpay;
+    a->vsm = L->vsm;
+    a->kmask = L->kmask;
+    a->knorm = L->knorm;
+    a->krn = L->krn;
+    a->vnorm = L->vnorm;
+    a->vrn = L->vrn;
+    a->cents_k = static_cast<const __half*>(L->cents_k);
+    a->cents_v = static_cast<const __half*>(L->cents_v);
+    a->vq = static_cast<const __half*>(L->vq);
+    a->rotor_k = static_cast<const __half*>(L->rotor_k);
+    a->rotor_v = static_cast<const __half*>(L->rotor_v);
+    a->dk = static_cast<const __half*>(L->d_k);
+    a->dv = static_cast<const __half*>(L->d_v);
+    a->out_k = L->dk;
+    a->out_vt = L->dvt;
+    a->h_kv = L->H_kv;
+    a->tok0 = d0;
+    a->n_tok = nd;
+    a->start_pos = 0;
+    a->key0 = d0;
+    a->ld_vt = L->d_ld;
+    a->a_k = L->alpha_k;
+    a->a_v = L->alpha_v;
+    a->rope_base = L->rope_base;
+}
+
 int split_count(int c_len, int splits) {  // ref runtime.mojo:211-222
     if (splits <= 1 || c_len <= 0) return 1;
     return std::max(1, std::min(c_len / 8, splits));
@@ -304,8 +334,14 @@ int khq_layer_prefill(khq_layer* L, const void* q_gate, const void* k_roped, con
             cw.side_from_src = std::min(w0 - c_a, kChunk);
             cw.side_key0 = side0;
         }
-        hipError_t e = khq::launch_ring_gather(cw, stream);
-        if (e != hipSuccess) return (int)e;
+        // With the compressed chunk wholly before the sub-chunk (the steady
+        // state), the event reads no ring slot this launch writes: the append
+        // then rides in the decode launch below instead of a launch of its own.
+        const bool defer = combine && w0 >= c_a + kChunk && L->dec_hi < c_a + kChunk;
+        if (!defer) {
+            const hipError_t e = khq::launch_ring_gather(cw, stream);
+            if (e != hipSuccess) return (int)e;
+        }
         if (L->raw_lo < L->raw_hi && L->raw_hi == w0)
             L->raw_hi = w0 + m;
         else {
@@ -313,14 +349,22 @@ int khq_layer_prefill(khq_layer* L, const void* q_gate, const void* k_roped, con
             L->raw_hi = w0 + m;
         }
         // decoded rows up to c_len, raw rows [c_len, n_k) in the dense key space
-        auto prepare = [&](int c_len, int n_k) -> int {
+        auto prepare = [&](int c_len, int n_k, const khq::GatherArgs* with) -> int {
             if (L->dec_hi < c_len) {
                 const int d0 = L->dec_hi, nd = c_len - d0;
-                const int rc = khq_decompress_fp16(
-                    L->kpay, L->vpay, L->vsm, L->kmask, L->knorm, L->krn, L->vnorm, L->vrn,
-                    L->cents_k, L->cents_v, L->vq, L->rotor_k, L->rotor_v, L->d_k, L->d_v, L->H_kv,
-                    d0, nd, 0, L->alpha_k, L->alpha_v, L->rope_base, L->dk, d0, L->dvt, L->d_ld,
-                    stream);
+                int rc;
+                if (with) {
+                    khq::DecompArgs da{};
+                    decomp_args(L, d0, nd, &da);
+                    const hipError_t de = khq::launch_decompress_gather(da, *with, stream);
+                    rc = de == hipSuccess ? 0 : (int)de;
+                } else {
+                    rc = khq_decompress_fp16(
+                        L->kpay, L->vpay, L->vsm, L->kmask, L->knorm, L->krn, L->vnorm, L->vrn,
+                        L->cents_k, L->cents_v, L->vq, L->rotor_k, L->rotor_v, L->d_k, L->d_v,
+                        L->H_kv, d0, nd, 0, L->alpha_k, L->alpha_v, L->rope_base, L->dk, d0,
+                        L->dvt, L->d_ld, stream);
+                }
                 if (rc) return rc;
                 L->dec_hi = c_len;
                 // V^T columns up to the decode's last 16-column block are rewritten
@@ -354,7 +398,7 @@ int khq_layer_prefill(khq_layer* L, const void* q_gate, const void* k_roped, con
             if (rc) return rc;
             const int c_b = L->boundary;  // c_a + kChunk
             const int n_k = w0 + m;
-            rc = prepare(c_b, n_k);
+            rc = prepare(c_b, n_k, defer ? &cw : nullptr);
             if (rc) return rc;
             rc = khq::prefill_attn_run(qg + (size_t)done * L->H_q * 2 * kD, L->dk, L->dvt,
                                        L->d_ld, n_k, m, w0 + 1, L->H_q, L->H_kv, scale,
@@ -375,7 +419,7 @@ int khq_layer_prefill(khq_layer* L, const void* q_gate, const void* k_roped, con
             const int c_len = L->boundary;
             const int n_k = w0 + je;
             if (n_k - c_len > kRing) return -102;
-            int rc = prepare(c_len, n_k);
+            int rc = prepare(c_len, n_k, nullptr);
             if (rc) return rc;
             rc = khq_prefill_attn_fp16(qg + (size_t)(done + j) * L->H_q * 2 * kD, L->dk, L->dvt,
                                        L->d_ld, n_k, je - j, w0 + j + 1, L->H_q, L->H_kv, scale,

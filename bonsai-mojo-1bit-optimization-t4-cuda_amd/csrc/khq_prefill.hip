@@ -66,11 +66,10 @@ __device__ __forceinline__ void store_vt_cols(const _Float16 (*sv)[TOK_BLK + VT_
 // Block (16 tokens, KV head h), one wavefront per token (the decode of one
 // row is a chain of dependent loads: tokens in parallel hide it); lane p owns
 // patch p = dims 4 p .. 4 p + 3.
-__global__ __launch_bounds__(BLK_THR) void decompress_kernel(DecompArgs a) {
+__device__ __forceinline__ void decompress_block(const DecompArgs& a, int bx, int h) {
     __shared__ __align__(16) _Float16 sv[256][TOK_BLK + VT_PAD];
-    const int h = blockIdx.y;
     const int wv = threadIdx.x >> 6, p = threadIdx.x & 63;
-    const int t_blk = blockIdx.x * TOK_BLK;
+    const int t_blk = bx * TOK_BLK;
     // per-lane constants
     float cbk[4], ldk[4], ldv[4], rk[16], rv[16];
 #pragma unroll
@@ -204,13 +203,12 @@ staged:
 // transposed through LDS.  In chunk mode the keys come from the caller's new
 // tokens, which also go to their ring slots (one launch appends a chunk to
 // the ring and to the dense key space).
-__global__ __launch_bounds__(BLK_THR) void ring_gather_kernel(GatherArgs a) {
+__device__ __forceinline__ void gather_block(const GatherArgs& a, int bx, int h, int bz) {
     __shared__ __align__(16) _Float16 sv[256][TOK_BLK + VT_PAD];
-    const int h = blockIdx.y;
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int t_blk = blockIdx.x * TOK_BLK;
+    const int t_blk = bx * TOK_BLK;
     // job 0: the gather / chunk write; job 1: the side copy (block-uniform)
-    const bool side = blockIdx.z == 1;
+    const bool side = bz == 1;
     const int n = side ? a.side_n : a.n;
     const int key0 = side ? a.side_key0 : a.key0;
     if (t_blk >= n) return;
@@ -262,6 +260,32 @@ staged:
         store_vt_cols(sv, a.out_vt, a.ld_vt, h, key0 + t_blk, min(TOK_BLK, n - t_blk));
     else
         store_vt(sv, a.out_vt, a.ld_vt, h, key0 + t_blk);
+}
+
+__global__ __launch_bounds__(BLK_THR) void decompress_kernel(DecompArgs a) {
+    decompress_block(a, blockIdx.x, blockIdx.y);
+}
+
+__global__ __launch_bounds__(BLK_THR) void ring_gather_kernel(GatherArgs a) {
+    gather_block(a, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+// A decode and an independent gather (disjoint outputs, no data passed
+// between them) in one launch: blocks [0, nb_d) decode (x fastest, then the
+// KV head), the rest gather (x, then the KV head, then the job plane).
+__global__ __launch_bounds__(BLK_THR) void decompress_gather_kernel(DecompArgs d, GatherArgs g,
+                                                                    int nx_d, int nx_g) {
+    const int nb_d = nx_d * d.h_kv;
+    int b = blockIdx.x;
+    if (b < nb_d) {
+        decompress_block(d, b % nx_d, b / nx_d);
+        return;
+    }
+    b -= nb_d;
+    const int per_plane = nx_g * g.h_kv;
+    const int bz = b / per_plane;
+    b -= bz * per_plane;
+    gather_block(g, b % nx_g, b / nx_g, bz);
 }
 
 // Visibility of the keys of one 32-key tile to one query row, as a bit mask
@@ -724,6 +748,19 @@ hipError_t launch_decompress(const DecompArgs& a, hipStream_t st) {
     if (a.n_tok <= 0) return hipSuccess;
     hipLaunchKernelGGL(pf::decompress_kernel, dim3((a.n_tok + pf::TOK_BLK - 1) / pf::TOK_BLK, a.h_kv),
                        dim3(pf::BLK_THR), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_decompress_gather(const DecompArgs& d, const GatherArgs& g, hipStream_t st) {
+    const int side = g.src_k && g.side_n > 0 ? 1 : 0;
+    const int n_g = std::max(g.n, side ? g.side_n : 0);
+    if (d.n_tok <= 0) return launch_ring_gather(g, st);
+    if (n_g <= 0) return launch_decompress(d, st);
+    const int nx_d = (d.n_tok + pf::TOK_BLK - 1) / pf::TOK_BLK;
+    const int nx_g = (n_g + pf::TOK_BLK - 1) / pf::TOK_BLK;
+    hipLaunchKernelGGL(pf::decompress_gather_kernel,
+                       dim3(nx_d * d.h_kv + nx_g * g.h_kv * (1 + side)), dim3(pf::BLK_THR), 0, st,
+                       d, g, nx_d, nx_g);
     return hipGetLastError();
 }
 
