@@ -265,87 +265,85 @@ __global__ __launch_bounds__(256) void step_finish_batched_kernel(const FinishAr
 // load is issued before the first value is used.
 __device__ __forceinline__ f2 ld_ml(const float* pp) { return ldg_f2(pp + 256); }
 
-// Merge-only finish: one 512-thread block per (query head, 32-dim slice).
-// Eight consecutive lanes read one partial's 32 dims (128 contiguous bytes),
-// so a wavefront load touches 8 partials instead of 64 scattered rows; the
-// eight wavefronts take interleaved partials and are summed through LDS.
-__global__ __launch_bounds__(512) void step_merge_kernel(FinishArgs a) {
-    __shared__ float s_m[8], s_num[8][32], s_den[8];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int dl = lane & 7, pg = lane >> 3;
+__global__ __launch_bounds__(256) void step_merge_kernel(FinishArgs a) {
+    const int lane = threadIdx.x & 63;
     const int hq = blockIdx.x;
-    const int d0 = blockIdx.y * 32 + dl * 4;
+    const int d0 = blockIdx.y * 32 + (threadIdx.x >> 6) * 8;
     const float* base = a.part + (size_t)hq * a.part_stride * 258;
     const int np = a.n_parts, last = max(np - 1, 0);
-    const int p0 = wave * 8 + pg;  // this lane's first partial; stride 64
-    f4 num = {0.0f, 0.0f, 0.0f, 0.0f};
-    float den = 0.0f, M = -3.0e38f;
+    float num[8], den = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) num[j] = 0.0f;
     if (np <= 256) {
         f2 ml[4];
-        f4 o[4];
+        f4 o[4][2];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const float* pp = base + (size_t)min(p0 + 64 * k, last) * 258;
+            const float* pp = base + (size_t)min(lane + 64 * k, last) * 258;
             ml[k] = ld_ml(pp);
-            o[k] = ldg_f4(pp + d0);
+            o[k][0] = ldg_f4(pp + d0);
+            o[k][1] = ldg_f4(pp + d0 + 4);
         }
+        float M = -3.0e38f;
 #pragma unroll
         for (int k = 0; k < 4; k++) M = fmaxf(M, ml[k].x);
         M = wave_max(M);
-        if (lane == 0) s_m[wave] = M;
-        __syncthreads();
-#pragma unroll
-        for (int w = 0; w < 8; w++) M = fmaxf(M, s_m[w]);
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const float w = p0 + 64 * k < np ? __expf(ml[k].x - M) : 0.0f;
+            const float w = lane + 64 * k < np ? __expf(ml[k].x - M) : 0.0f;
             den = fmaf(ml[k].y, w, den);
-            num = num + o[k] * w;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                num[j] = fmaf(o[k][0][j], w, num[j]);
+                num[4 + j] = fmaf(o[k][1][j], w, num[4 + j]);
+            }
         }
     } else {
-        for (int p = p0; p < np; p += 64) M = fmaxf(M, base[(size_t)p * 258 + 256]);
+        float M = -3.0e38f;
+        for (int p = lane; p < np; p += 64) M = fmaxf(M, base[(size_t)p * 258 + 256]);
         M = wave_max(M);
-        if (lane == 0) s_m[wave] = M;
-        __syncthreads();
-#pragma unroll
-        for (int w = 0; w < 8; w++) M = fmaxf(M, s_m[w]);
-        for (int p = p0; p < np; p += 64) {
+        for (int p = lane; p < np; p += 64) {
             const float* pp = base + (size_t)p * 258;
             const f2 ml = ld_ml(pp);
-            const f4 o = ldg_f4(pp + d0);
+            const f4 o0 = ldg_f4(pp + d0), o1 = ldg_f4(pp + d0 + 4);
             const float w = __expf(ml.x - M);
             den = fmaf(ml.y, w, den);
-            num = num + o * w;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                num[j] = fmaf(o0[j], w, num[j]);
+                num[4 + j] = fmaf(o1[j], w, num[4 + j]);
+            }
         }
     }
-    // sum over the eight partial groups of the wavefront (lane bits 3..5)
+    den = wave_sum(den);
+    // reduce-scatter: xor 32 keeps half (4 + 2 + 1 values), then sum the rest
+    const bool b5 = (lane & 32) != 0, b4 = (lane & 16) != 0, b3 = (lane & 8) != 0;
+    float k4[4], k2[2];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        float v = num[j];
-        v += xor_lane<8>(v);
-        v += xor_lane<16>(v);
-        v += xor_lane<32>(v);
-        num[j] = v;
+    for (int i = 0; i < 4; i++) {
+        const float keep = b5 ? num[4 + i] : num[i];
+        const float send = b5 ? num[i] : num[4 + i];
+        k4[i] = keep + xor_lane<32>(send);
     }
-    den += xor_lane<8>(den);
-    den += xor_lane<16>(den);
-    den += xor_lane<32>(den);
-    if (pg == 0) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) s_num[wave][dl * 4 + j] = num[j];
-        if (dl == 0) s_den[wave] = den;
+    for (int i = 0; i < 2; i++) {
+        const float keep = b4 ? k4[2 + i] : k4[i];
+        const float send = b4 ? k4[i] : k4[2 + i];
+        k2[i] = keep + xor_lane<16>(send);
     }
-    __syncthreads();
-    if (threadIdx.x < 32) {
-        float v = 0.0f, dsum = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 8; w++) {
-            v += s_num[w][threadIdx.x];
-            dsum += s_den[w];
-        }
-        const int d = blockIdx.y * 32 + threadIdx.x;
+    float v;
+    {
+        const float keep = b3 ? k2[1] : k2[0];
+        const float send = b3 ? k2[0] : k2[1];
+        v = keep + xor_lane<8>(send);
+    }
+    v += xor_lane<1>(v);
+    v += xor_lane<2>(v);
+    v += xor_lane<4>(v);
+    if ((lane & 7) == 0) {
+        const int d = d0 + (lane >> 3);
         const float g = __half2float(a.q[(size_t)hq * 512 + 256 + d]);
-        const float val = v / (dsum + a.eps) * (1.0f / (1.0f + expf(-g)));
+        const float val = v / (den + a.eps) * (1.0f / (1.0f + expf(-g)));
         a.out[(size_t)hq * 256 + d] = __float2half(val);
     }
 }
@@ -363,7 +361,7 @@ hipError_t launch_step_finish(const FinishArgs& a, int H_q, hipStream_t st) {
     if (a.n_parts > fin::MAX_PARTS || a.win_len > fin::MAX_WIN || a.n_rep <= 0)
         return hipErrorInvalidValue;
     if (a.win_len == 0 && a.n_parts > 0) {
-        hipLaunchKernelGGL(fin::step_merge_kernel, dim3(H_q, 8), dim3(512), 0, st, a);
+        hipLaunchKernelGGL(fin::step_merge_kernel, dim3(H_q, 8), dim3(256), 0, st, a);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(fin::step_finish_kernel, dim3(H_q, 256 / fin::DS), dim3(256), 0, st, a);
