@@ -6,6 +6,7 @@
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
+#include <cstring>
 #include <mutex>
 #include <vector>
 
@@ -542,12 +543,14 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
     float* ws = nullptr;
     hipError_t e = workspace(meta_off + meta_bytes, &ws);
     if (e != hipSuccess) return rc_of(e);
+    // metadata block (device and host staging share the layout): the
+    // attention arguments, the finishing arguments, then the block map
     char* meta = reinterpret_cast<char*>(ws) + meta_off;
+    const size_t o_fin = (n_seq * sizeof(khq::AttnArgs) + 15) & ~(size_t)15;
+    const size_t o_map = (o_fin + n_seq * sizeof(khq::FinishArgs) + 15) & ~(size_t)15;
     khq::AttnArgs* d_args = reinterpret_cast<khq::AttnArgs*>(meta);
-    khq::FinishArgs* d_fin = reinterpret_cast<khq::FinishArgs*>(
-        (reinterpret_cast<uintptr_t>(d_args + n_seq) + 15) & ~(uintptr_t)15);
-    int2* d_map = reinterpret_cast<int2*>(
-        (reinterpret_cast<uintptr_t>(d_fin + n_seq) + 15) & ~(uintptr_t)15);
+    khq::FinishArgs* d_fin = reinterpret_cast<khq::FinishArgs*>(meta + o_fin);
+    int2* d_map = reinterpret_cast<int2*>(meta + o_map);
     for (int i = 0; i < n_seq; i++) {
         const khq_seq& q = seqs[i];
         khq::AttnArgs a = attn_args(q.q_gate, q.k_payload, q.v_payload, q.v_shared_meta, q.k_mask,
@@ -605,14 +608,15 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
                          });
         for (const auto& x : cb) h_map.push_back(x.second);
     }
-    e = hipMemcpyAsync(d_args, h_args.data(), n_seq * sizeof(khq::AttnArgs),
-                       hipMemcpyHostToDevice, stream);
-    if (e == hipSuccess)
-        e = hipMemcpyAsync(d_fin, h_fin.data(), n_seq * sizeof(khq::FinishArgs),
-                           hipMemcpyHostToDevice, stream);
-    if (e == hipSuccess)
-        e = hipMemcpyAsync(d_map, h_map.data(), h_map.size() * sizeof(int2),
-                           hipMemcpyHostToDevice, stream);
+    // one host-to-device copy of the whole block (each copy is a fixed cost
+    // on the stream); pageable staging, so the next call may reuse it at once
+    static thread_local std::vector<char> h_meta;
+    const size_t n_meta = o_map + h_map.size() * sizeof(int2);
+    h_meta.resize(n_meta);
+    std::memcpy(h_meta.data(), h_args.data(), n_seq * sizeof(khq::AttnArgs));
+    std::memcpy(h_meta.data() + o_fin, h_fin.data(), n_seq * sizeof(khq::FinishArgs));
+    std::memcpy(h_meta.data() + o_map, h_map.data(), h_map.size() * sizeof(int2));
+    e = hipMemcpyAsync(meta, h_meta.data(), n_meta, hipMemcpyHostToDevice, stream);
     if (e != hipSuccess) return rc_of(e);
     e = khq::launch_attn_ws_batched(d_args, d_map, (int)h_map.size(), per, stream);
     if (e != hipSuccess) return rc_of(e);
