@@ -34,8 +34,7 @@ ROW_BYTES = 220
 HBM_PEAK_GBS = 8000.0
 RING = 256
 KERNEL_NAMES = {"auto": "attn_ws_kernel (compressed region)",
-                "portable": "attn_part_kernel<6> (compressed region)",
-                "mfma-single": "attn_mfma_kernel (compressed region)"}
+                "portable": "attn_part_kernel<6> (compressed region)"}
 
 
 def parse():
@@ -48,7 +47,7 @@ def parse():
     ap.add_argument("--win", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--kernel", choices=["auto", "portable", "mfma-single"], default="auto",
+    ap.add_argument("--kernel", choices=["auto", "portable"], default="auto",
                     help="compressed-region kernel (library default: auto)")
     ap.add_argument("--data", choices=["uniform", "compressed"], default="uniform",
                     help="payload: seeded uniform-random packed codes with outlier counts "
@@ -64,8 +63,10 @@ def parse():
                     help="profiling aid for rocprofv3 --pmc: a 256 MiB device copy (the "
                          "calibration kernel of known size), then the compressed-region kernel "
                          "on 4 C3 layers, 3 times; prints no JSON")
-    ap.add_argument("--sweep", action="store_true",
-                    help="also time the reference entry points at splits 1/8/32/64")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip the C3 sweep of the reference entry sequence at splits "
+                         "1/8/32/64 (launch_khq_attn_fp16 + window + merge, and the split-K "
+                         "reduce alone)")
     return ap.parse_args()
 
 
@@ -78,7 +79,7 @@ def main():
 
     from khq import _lib, ops, synth
 
-    _lib.call("khq_select_kernel", ["auto", "portable", "mfma-single"].index(args.kernel))
+    _lib.call("khq_select_kernel", ["auto", "portable"].index(args.kernel))
     if args.config in ("c1", "c2"):
         return bench_small(args)
     if args.config == "c4":
@@ -170,7 +171,7 @@ def main():
     del xa, xb
 
     traffic = {}
-    tname = {"auto": "attn_ws_c3_traffic.json", "mfma-single": "attn_mfma_c3_traffic.json"}
+    tname = {"auto": "attn_ws_c3_traffic.json"}
     tpath = os.path.join(ROOT, "profiles", tname.get(args.kernel, "none"))
     if os.path.exists(tpath) and c_len == 32640:
         with open(tpath) as f:
@@ -233,16 +234,22 @@ def main():
             e0.elapsed_time(e1) * 1000.0 / args.steps, 3)
         del upay
 
-    if args.sweep:
-        sweep = {}
+    if not args.no_sweep:
+        # the reference's launch sequence per layer (ref:src/khq/runtime.mojo:554-613):
+        # launch_khq_attn_fp16 (split-K partials into out_partial + reduce),
+        # launch_khq_window_attn_fp16, launch_khq_merge_gate_fp16; and the
+        # split-K reduce (khq_attn_reduce_kernel's counterpart) timed alone
+        sweep, reduce_us = {}, {}
         ac = torch.empty((H_Q, D + 2), device=dev)
         aw = torch.empty((H_Q, D + 2), device=dev)
         ap_ = torch.empty((H_Q, 64, D + 2), device=dev)
         for sp in (1, 8, 32, 64):
+            part = ap_[:, :sp].contiguous() if sp > 1 else None
+
             def ref_step():
                 for L in layers:
                     ops.attn(L["q"], L["pay"], L["cents"], ac, c_len=c_len, H_q=H_Q, H_kv=H_KV,
-                             scale=scale, num_splits=sp, out_partial=ap_ if sp > 1 else None)
+                             scale=scale, num_splits=sp, out_partial=part)
                     ops.window_attn(L["q"], L["ring_k"], L["ring_v"], aw, win_start=win_start,
                                     win_len=win_len, ring_cap=RING, H_q=H_Q, H_kv=H_KV,
                                     scale=scale)
@@ -255,7 +262,15 @@ def main():
             e1.record(stream)
             torch.cuda.synchronize()
             sweep[f"splits_{sp}"] = round(e0.elapsed_time(e1) * 1000.0 / n_launch, 3)
+            if sp > 1:
+                e0.record(stream)
+                for _ in range(n_launch):
+                    ops.attn_reduce(part, ac, num_queries=H_Q, num_splits=sp)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                reduce_us[f"splits_{sp}"] = round(e0.elapsed_time(e1) * 1000.0 / n_launch, 3)
         result["reference_entry_us_per_layer_step"] = sweep
+        result["split_reduce_us"] = reduce_us
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(layers[0], c_len, win_len, win_start, scale,

@@ -44,6 +44,7 @@
 #include <stdint.h>
 #include <math.h>
 #include <string.h>
+#include <stdlib.h>
 
 #include "khq_internal.h"
 #include "khq_mfma_util.h"
@@ -104,17 +105,26 @@ struct __align__(16) Smem {
     float s3[4][8];              // final dump-offset sums per query head
     int kdone[4];                // tiles whose scores the key wavefront has published
     int vread[4];                // tiles whose scores the value wavefront has read
+    int fault;                   // a hand-off wait gave up
 };
 
 // Hand-off between the key and value wavefronts of one KV head through LDS
 // counters (release / acquire at workgroup scope), so each pair runs at its
 // own pace instead of meeting the other pairs at a block barrier every tile.
-// The wait is bounded: a wavefront never spins for more than ~2^20 sleeps.
-__device__ __forceinline__ void wait_count(const int* f, int target) {
+// The wait is bounded (spin_limit sleeps, 2^20 by default): a wavefront that
+// gives up records the fault in the block's LDS flag, and the block then
+// writes NaN maxima into its partials and raises the library's device fault
+// word (khq_fault_status), so a timed-out result is never silently wrong.
+__device__ int g_fault;
+
+__device__ __forceinline__ void wait_count(const int* f, int target, int limit, int* fault) {
     int n = 0;
     while (__hip_atomic_load(f, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+        if (++n > limit) {
+            __hip_atomic_store(fault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            break;
+        }
         __builtin_amdgcn_s_sleep(1);
-        if (++n > (1 << 20)) break;
     }
 }
 __device__ __forceinline__ void publish_count(int* f, int v) {
@@ -567,7 +577,7 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
             // ---- raw scores to the value side (it keeps the softmax state);
             // buffer t & 1 last held tile t - 2
             const int buf = t & 1;
-            wait_count(&S.vread[h], t - 1);
+            wait_count(&S.vread[h], t - 1, a.spin_limit, &S.fault);
             if (lg < 3) {
                 S.pw[buf][h][2 * lg][li] = sc2[0];
                 S.pw[buf][h][2 * lg + 1][li] = sc2[1];
@@ -686,7 +696,7 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
             const int buf = t & 1;
             // ---- the key side's scores of this tile: row head r_head, tokens
             // 4 lg .. 4 lg + 3 (read first: their latency overlaps the staging)
-            wait_count(&S.kdone[h], t + 1);
+            wait_count(&S.kdone[h], t + 1, a.spin_limit, &S.fault);
             f4 sc4 = f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
             if (r_ok) sc4 = *reinterpret_cast<const f4*>(&S.pw[buf][h][r_head][4 * lg]);
             // ---- take the staged tile, start loading the next one
@@ -1147,8 +1157,16 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
         return;
     }
     const int c_len = a.c_len;
-    const int s_lo = min(chunk * tiles_per_chunk * TT, c_len);
-    const int s_hi = min(s_lo + tiles_per_chunk * TT, c_len);
+    int s_lo, s_hi;
+    if (a.split_per > 0) {  // the reference's split partition, cut into chunks
+        const int sp = chunk / a.split_subs, sub = chunk - sp * a.split_subs;
+        const int lo = min(sp * a.split_per, c_len), hi = min(lo + a.split_per, c_len);
+        s_lo = min(lo + sub * tiles_per_chunk * TT, hi);
+        s_hi = min(s_lo + tiles_per_chunk * TT, hi);
+    } else {
+        s_lo = min(chunk * tiles_per_chunk * TT, c_len);
+        s_hi = min(s_lo + tiles_per_chunk * TT, c_len);
+    }
     const int n_tiles = (s_hi - s_lo + TT - 1) / TT;
 #ifdef KHQ_PHASE_TIMING
     unsigned long long ph_t = __builtin_amdgcn_s_memtime();
@@ -1174,6 +1192,7 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
             S.kdone[tid] = 0;
             S.vread[tid] = 0;
         }
+        if (tid == 0) S.fault = 0;
         if (wv < 4) {
             h4 s;
 #pragma unroll
@@ -1230,6 +1249,9 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
 #endif
 
     // ---- output: wavefront wv handles query heads 3 (wv / 4) .. + 2 of KV head h
+    // (S.fault is final: every wait precedes the roles' last block barrier)
+    const bool bad = __hip_atomic_load(&S.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0;
+    if (bad && tid == 0) atomicOr(&g_fault, 1);
     const float* ep = S.o[h];
     float rv[16];
 #pragma unroll
@@ -1255,7 +1277,7 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
         fwht256(u, lane);
         const int hq = h * 6 + hd;
         float* out = a.part + ((size_t)hq * a.part_stride + a.part_offset + chunk) * 258;
-        const float M = S.ml[h][hd][0];
+        const float M = bad ? __builtin_nanf("") : S.ml[h][hd][0];
         const float L = S.ml[h][hd][1];
         const bool empty = (M == -INFINITY);
         // partial rows are 258 floats: 8-byte aligned, so 8-byte stores
@@ -1293,6 +1315,24 @@ __global__ __launch_bounds__(NTHR, 1) void attn_ws_batched_kernel(const AttnArgs
 }  // namespace ws
 
 size_t attn_ws_smem_bytes() { return sizeof(ws::Smem); }
+
+int g_spin_limit = 1 << 20;
+
+// Chunking of the compressed region: at most 255 chunks (one CU of a 256-CU
+// part left for the window block), each of the same whole number of tiles.
+int attn_ws_tiles_per_chunk(int c_len, int* n_chunks) {
+    static const int max_chunks = [] {
+        const char* e = getenv("KHQ_MAX_CHUNKS");
+        const int v = e ? atoi(e) : 0;
+        return v > 0 ? v : 255;
+    }();
+    const int tiles = (c_len + ws::TT - 1) / ws::TT;
+    int chunks = tiles < max_chunks ? tiles : max_chunks;
+    if (chunks < 1) chunks = 1;
+    const int per = (tiles + chunks - 1) / chunks;
+    *n_chunks = (tiles + per - 1) / per;
+    return per;
+}
 
 void fill_rope_table(AttnArgs& a) {
     // freq = powf(base, -2 m / 64) as the oracle and the portable kernels
@@ -1335,6 +1375,7 @@ hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks, 
     b.win_blocks = n_chunks + ws::NWIN <= n_cu ? ws::NWIN : 1;
     const int blocks = n_chunks + (a.win_len > 0 ? b.win_blocks : 0);
     fill_rope_table(b);
+    b.spin_limit = g_spin_limit;
     hipLaunchKernelGGL(ws::attn_ws_kernel, dim3(blocks), dim3(ws::NTHR), smem, st, b,
                        tiles_per_chunk, n_chunks);
     return hipGetLastError();
@@ -1353,6 +1394,15 @@ hipError_t launch_attn_ws_batched(const AttnArgs* args, const int2* map, int n_b
     hipLaunchKernelGGL(ws::attn_ws_batched_kernel, dim3(n_blocks), dim3(ws::NTHR), smem, st,
                        args, map, tiles_per_chunk);
     return hipGetLastError();
+}
+
+hipError_t fault_status(int* out, int clear) {
+    hipError_t e = hipMemcpyFromSymbol(out, HIP_SYMBOL(ws::g_fault), sizeof(int));
+    if (e == hipSuccess && clear && *out) {
+        const int z = 0;
+        e = hipMemcpyToSymbol(HIP_SYMBOL(ws::g_fault), &z, sizeof(int));
+    }
+    return e;
 }
 
 }  // namespace khq

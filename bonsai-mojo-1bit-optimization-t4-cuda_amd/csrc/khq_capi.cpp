@@ -48,8 +48,7 @@ hipError_t workspace(size_t bytes, float** out) {
 }
 
 // 0 = automatic (wavefront-specialised matrix-core kernel for the 24/4/256
-// shape), 1 = portable lane-per-patch kernel for every shape, 2 = the
-// single-role matrix-core kernel for the 24/4/256 shape.
+// shape), 1 = portable lane-per-patch kernel for every shape.
 int g_kernel_choice = 0;
 
 bool use_mfma(int n_rep, int h_kv, int L_q) {
@@ -62,9 +61,8 @@ hipError_t launch_compressed(khq::AttnArgs a, int n_rep, int L_q, int* parts_use
                              hipStream_t stream) {
     if (use_mfma(n_rep, a.h_kv, L_q)) {
         int n_chunks = 0;
-        const int per = khq::attn_mfma_tiles_per_chunk(a.c_len, &n_chunks);
+        const int per = khq::attn_ws_tiles_per_chunk(a.c_len, &n_chunks);
         *parts_used = n_chunks;
-        if (g_kernel_choice == 2) return khq::launch_attn_mfma(a, per, n_chunks, stream);
         return khq::launch_attn_ws(a, per, n_chunks, stream);
     }
     *parts_used = a.n_parts;
@@ -75,7 +73,7 @@ int compressed_parts(int c_len, int n_rep, int h_kv, int L_q) {
     if (c_len <= 0) return 0;
     if (use_mfma(n_rep, h_kv, L_q)) {
         int n_chunks = 0;
-        khq::attn_mfma_tiles_per_chunk(c_len, &n_chunks);
+        khq::attn_ws_tiles_per_chunk(c_len, &n_chunks);
         return n_chunks;
     }
     return std::max(1, std::min(256, (c_len + 31) / 32));
@@ -118,8 +116,19 @@ const char* khq_version(void) { return "khq-mi355x 0.1 (gfx950)"; }
 int khq_attn_parts(int c_len) { return compressed_parts(c_len, 6, 4, 1); }
 
 int khq_select_kernel(int which) {
-    if (which < 0 || which > 2) return -100;
+    if (which < 0 || which > 1) return -100;
     g_kernel_choice = which;
+    return 0;
+}
+
+int khq_fault_status(int* flags, int clear) {
+    if (!flags) return -100;
+    return rc_of(khq::fault_status(flags, clear));
+}
+
+int khq_set_spin_limit(int sleeps) {
+    if (sleeps < 0) return -100;
+    khq::g_spin_limit = sleeps > 0 ? sleeps : (1 << 20);
     return 0;
 }
 
@@ -161,29 +170,85 @@ int launch_khq_attn_fp16(const void* q, const void* k_payload, const void* v_pay
         num_queries != num_heads * L_q)
         return -100;
     const int h_kv = num_heads / n_rep;
-    const int np = compressed_parts(L_q > 1 ? std::min(c_len, L_q) : c_len, n_rep, h_kv, L_q);
-    float* ws = nullptr;
-    hipError_t e = workspace((size_t)num_queries * np * 258 * sizeof(float), &ws);
-    if (e != hipSuccess) return rc_of(e);
     khq::AttnArgs a = attn_args(q, k_payload, v_payload, v_shared_meta, k_mask, k_norms,
                                 k_r_norms, v_norms, v_r_norms, centroids_k, centroids_v,
                                 vq_centroids, k_rotor, v_rotor, d_vec_k, d_vec_v);
-    a.part = ws;
     a.c_len = c_len;
     a.h_kv = h_kv;
     a.L_q = L_q;
     a.start_pos = start_pos;
-    a.n_parts = np;
-    a.part_stride = np;
     a.part_offset = 0;
     a.sc = scale;
     a.a_k = alpha_k;
     a.a_v = alpha_v;
     a.rope_base = rope_base;
+    float* outp = static_cast<float*>(out_partial);
+    hipError_t e;
+    if (num_splits > 1 && !use_mfma(n_rep, h_kv, L_q)) {
+        // the portable kernel cuts the tokens exactly as the reference does
+        // (per = ceil(s_limit / n_sp), .cu:1542-1553) and writes the split
+        // triples straight into out_partial [query][split][258]
+        a.part = outp;
+        a.n_parts = num_splits;
+        a.part_stride = num_splits;
+        e = khq::launch_attn_parts(a, n_rep, dim3(num_splits, h_kv, L_q), stream);
+        if (e != hipSuccess) return rc_of(e);
+        return rc_of(khq::launch_lse_reduce(outp, static_cast<float*>(out_attn), num_queries,
+                                            num_splits, stream));
+    }
+    if (num_splits > 1) {
+        // Matrix-core kernel: each reference split [sp * per, (sp + 1) * per)
+        // is cut into `subs` chunks of whole tiles, so no chunk straddles a
+        // split; the chunk triples merge into out_partial (the reference's
+        // split triples, empty splits (0, -1e20, 0)), and those into out_attn.
+        const int per = (c_len + num_splits - 1) / num_splits;
+        const int split_tiles = (per + 15) / 16;
+        const int want = std::max(1, std::min(split_tiles, 255 / num_splits));
+        const int tpc = (split_tiles + want - 1) / want;
+        const int subs = (split_tiles + tpc - 1) / tpc;
+        const int nch = num_splits * subs;
+        float* part = outp;
+        if (subs > 1) {
+            float* ws = nullptr;
+            e = workspace((size_t)num_queries * nch * 258 * sizeof(float), &ws);
+            if (e != hipSuccess) return rc_of(e);
+            part = ws;
+        }
+        a.part = part;
+        a.n_parts = nch;
+        a.part_stride = nch;
+        a.split_per = per;
+        a.split_subs = subs;
+        e = khq::launch_attn_ws(a, tpc, nch, stream);
+        if (e != hipSuccess) return rc_of(e);
+        if (subs > 1) {
+            e = khq::launch_lse_reduce(part, outp, num_queries * num_splits, subs, stream);
+            if (e != hipSuccess) return rc_of(e);
+        }
+        return rc_of(khq::launch_lse_reduce(outp, static_cast<float*>(out_attn), num_queries,
+                                            num_splits, stream));
+    }
+    // num_splits = 1: the library's own partition in its workspace, merged
+    // into out_attn (the reference computes the same triple in one pass)
+    const int np = compressed_parts(L_q > 1 ? std::min(c_len, L_q) : c_len, n_rep, h_kv, L_q);
+    float* ws = nullptr;
+    e = workspace((size_t)num_queries * np * 258 * sizeof(float), &ws);
+    if (e != hipSuccess) return rc_of(e);
+    a.part = ws;
+    a.n_parts = np;
+    a.part_stride = np;
     int used = 0;
     e = launch_compressed(a, n_rep, L_q, &used, stream);
     if (e != hipSuccess) return rc_of(e);
     return rc_of(khq::launch_lse_reduce(ws, static_cast<float*>(out_attn), num_queries, np,
+                                        stream));
+}
+
+int khq_attn_reduce_f32(const void* partial, void* out_attn, int num_queries, int num_splits,
+                        hipStream_t stream) {
+    if (!partial || !out_attn || num_queries <= 0 || num_splits < 1) return -100;
+    return rc_of(khq::launch_lse_reduce(static_cast<const float*>(partial),
+                                        static_cast<float*>(out_attn), num_queries, num_splits,
                                         stream));
 }
 
@@ -576,6 +641,7 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
         a.ring_cap = ring;
         a.win_blocks = 4;
         khq::fill_rope_table(a);
+        a.spin_limit = khq::g_spin_limit;
         h_args[i] = a;
         if (np[i] > chunks[i])  // window blocks, one per KV head
             for (int w = 0; w < 4; w++) h_map.push_back(int2{i, chunks[i] + w});

@@ -37,6 +37,14 @@ struct AttnArgs {
     const __half* ring_v;
     int win_start, win_len, ring_cap;
     int win_blocks;  // window blocks after the chunks: 4 (one per KV head) or 1 (all heads)
+    // Bound of the key / value hand-off waits of the wavefront-specialised
+    // kernel, in sleeps (set by the launchers; a test knob may lower it).
+    int spin_limit;
+    // Reference split partition (wavefront-specialised kernel): split_per > 0
+    // cuts [0, c_len) into splits of split_per tokens, each into split_subs
+    // chunks of tiles_per_chunk tiles; chunk = split * split_subs + sub.
+    // split_per = 0: chunk i covers tiles [i * tiles_per_chunk, + tiles_per_chunk).
+    int split_per, split_subs;
     // RoPE table of the wavefront-specialised kernel, [lane group g][3][u]:
     // freq of dim pair m = 16 (u / 4) + 4 g + u % 4, cos and sin of 16 freq
     // (filled by the launchers from rope_base).
@@ -107,13 +115,15 @@ hipError_t launch_ring_write(__half* rk, __half* rv, __half* ru, const __half* k
 hipError_t launch_partial_rope(__half* vec, int num_heads, int head_dim, int rotary_dim, int pos,
                                float theta, int stride, hipStream_t st);
 
-// MFMA compressed-region kernel (H_kv = 4, n_rep = 6, L_q = 1): one block per
-// chunk of tiles_per_chunk 16-token tiles; partial index = part_offset + chunk.
-size_t attn_mfma_smem_bytes();
-int attn_mfma_tiles_per_chunk(int c_len, int* n_chunks);
-hipError_t launch_attn_mfma(const AttnArgs& a, int tiles_per_chunk, int n_chunks,
-                            hipStream_t st);
-// Wavefront-specialised variant of the same contract (512 threads per block).
+// Compressed-region kernel for H_kv = 4, n_rep = 6, L_q = 1 (wavefront-
+// specialised, 512 threads per block): one block per chunk of
+// tiles_per_chunk 16-token tiles; partial index = part_offset + chunk.
+int attn_ws_tiles_per_chunk(int c_len, int* n_chunks);
+// Device fault word of the wavefront-specialised kernel (nonzero after a
+// hand-off wait gave up), read with a synchronous copy; clear resets it.
+hipError_t fault_status(int* out, int clear);
+// Hand-off wait bound used by the launchers (default 2^20 sleeps).
+extern int g_spin_limit;
 size_t attn_ws_smem_bytes();
 // Fills a.rope_tab from a.rope_base (host).
 void fill_rope_table(AttnArgs& a);

@@ -38,6 +38,9 @@ SIGNATURES = {
     "khq_attn_parts": [I],
     "khq_select_kernel": [I],
     "khq_workspace_reserve": [ctypes.c_size_t],
+    "khq_attn_reduce_f32": [P, P, I, I, P],
+    "khq_fault_status": [P, I],
+    "khq_set_spin_limit": [I],
     # per-layer runtime
     "khq_layer_create": [I, I, I] + [P] * 7 + [F, F, F, F, F, I, I],
     "khq_layer_destroy": [P],

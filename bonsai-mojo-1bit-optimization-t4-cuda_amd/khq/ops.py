@@ -265,3 +265,26 @@ def attn_parts(c_len: int) -> int:
 
 def workspace_reserve(nbytes: int) -> None:
     call("khq_workspace_reserve", nbytes)
+
+
+def attn_reduce(partial, out_attn, *, num_queries: int, num_splits: int, stream=None,
+                check: bool = True) -> int:
+    """khq_attn_reduce_f32: logsumexp merge of split triples (the reduce
+    launch_khq_attn_fp16 issues for num_splits > 1)."""
+    _need(partial, torch.float32, num_queries * num_splits * (D + 2), "partial")
+    _need(out_attn, torch.float32, num_queries * (D + 2), "out_attn")
+    return call("khq_attn_reduce_f32", ptr(partial), ptr(out_attn), num_queries, num_splits,
+                stream_handle(stream), check=check)
+
+
+def fault_status(clear: bool = True) -> int:
+    """khq_fault_status: nonzero when a hand-off wait of the compressed-region
+    kernel gave up since the last clear (those blocks wrote NaN maxima)."""
+    v = ctypes.c_int(0)
+    call("khq_fault_status", ctypes.addressof(v), 1 if clear else 0)
+    return v.value
+
+
+def set_spin_limit(sleeps: int) -> None:
+    """Test knob: bound of the kernel's hand-off waits (0 = default 2^20)."""
+    call("khq_set_spin_limit", sleeps)

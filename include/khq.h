@@ -46,11 +46,14 @@ int launch_khq_compress_fp16(const void* x, const void* d_vec, const void* rotor
 /* Replaces launch_khq_attn_fp16, ref:.cu:4314-4375.  Attention of
  * num_queries = num_heads * L_q queries over compressed tokens [0, c_len),
  * RoPE on dims 0..63 at absolute position start_pos + s.  Writes the
- * unnormalised triple to out_attn.  num_splits keeps the reference's
- * contract (-101 when > 1 and out_partial is NULL); the token partition used
- * internally is the library's own and out_partial is not written, so its
- * contents are unspecified after the call.  stride_s is unused, as in the
- * reference. */
+ * unnormalised triple to out_attn.  num_splits > 1 (out_partial required,
+ * else -101) selects the reference's partition: split i covers tokens
+ * [i * per, (i + 1) * per), per = ceil(s_limit / num_splits), and its triple
+ * is written to out_partial f32 [num_queries][num_splits][258] (empty splits:
+ * acc 0, max -1e20, sum 0); out_attn is their logsumexp merge.  Internally
+ * each split may be cut further (library workspace) and merged into its
+ * triple first.  num_splits <= 1: the library's own partition, out_partial
+ * untouched.  stride_s is unused, as in the reference. */
 int launch_khq_attn_fp16(const void* q, const void* k_payload, const void* v_payload,
                          const void* v_shared_meta, const void* k_mask,
                          const void* k_norms, const void* k_r_norms, const void* v_norms,
@@ -62,6 +65,14 @@ int launch_khq_attn_fp16(const void* q, const void* k_payload, const void* v_pay
                          int stride_s, int n_rep, float scale, float alpha_k,
                          float alpha_v, float rope_base, int start_pos,
                          int num_splits, hipStream_t stream);
+
+/* The split-K merge launch_khq_attn_fp16 issues when num_splits > 1, on its
+ * own (the reference launches khq_attn_reduce_kernel, ref:.cu:1836-1877,
+ * only inside launch_khq_attn_fp16, :4366-4373): logsumexp merge of
+ * partial f32 [num_queries][num_splits][258] into out_attn f32
+ * [num_queries][258].  Empty splits (max -1e20, sum 0) weigh nothing. */
+int khq_attn_reduce_f32(const void* partial, void* out_attn, int num_queries, int num_splits,
+                        hipStream_t stream);
 
 /* Replaces launch_khq_window_attn_fp16, ref:.cu:4378-4396.  fp16 attention of
  * H_q heads over ring slots (win_start + s) % ring_cap, s < win_len (K already
@@ -200,6 +211,18 @@ int khq_attn_parts(int c_len);
  * n_rep 6 / L_q 1, portable kernel otherwise), 1 = portable kernel always.
  * Process-wide; returns -100 for other values. */
 int khq_select_kernel(int which);
+
+/* Fault word of the compressed-region kernel on the current device (no
+ * reference counterpart).  The kernel's key and value wavefronts hand tiles
+ * over through bounded waits; a wait that gives up makes that block write NaN
+ * maxima into its partials (so the merged output is NaN, never silently
+ * wrong) and sets bit 0 of this word.  Synchronous (it waits for the device's
+ * queued work); clear = 1 resets the word after reading it. */
+int khq_fault_status(int* flags, int clear);
+
+/* Test knob (no reference counterpart): bound of those hand-off waits in
+ * sleeps, process-wide; 0 restores the default (2^20). */
+int khq_set_spin_limit(int sleeps);
 
 /* Grows the library's device workspace (split partials) to at least `bytes`
  * on the current device.  Every launcher grows it on demand; call this first
