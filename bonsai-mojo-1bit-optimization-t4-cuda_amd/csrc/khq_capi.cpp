@@ -47,6 +47,34 @@ hipError_t workspace(size_t bytes, float** out) {
     return hipSuccess;
 }
 
+// Partials of khq_attn_step_noalloc_fp16: a fixed device array per GPU
+// (8 MiB, enough for H_q 24 at any context: at most 255 chunk parts + 64
+// window parts of 258 floats per query head), never allocated at run time.
+// Each device holds its own copy at its own address, which is looked up once
+// per device (with that device current) and kept; the array's name is a
+// host-side stand-in and is never passed to a kernel or a copy.  Every call
+// on a GPU shares that GPU's array: calls that overlap on one GPU race.
+constexpr size_t kScratchBytes = (size_t)8 << 20;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+hipError_t scratch_ptr(float** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+
 // 0 = automatic (wavefront-specialised matrix-core kernel for the 24/4/256
 // shape), 1 = portable lane-per-patch kernel for every shape.
 int g_kernel_choice = 0;
@@ -387,7 +415,9 @@ int khq_attn_partials_fp16(const void* q_gate, const void* k_payload, const void
     return rc_of(launch_compressed(a, H_q / H_kv, 1, &used, stream));
 }
 
-int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_payload,
+}  // extern "C"
+
+static int attn_step_impl(const void* q_gate, const void* k_payload, const void* v_payload,
                        const void* v_shared_meta, const void* k_mask, const void* k_norms,
                        const void* k_r_norms, const void* v_norms, const void* v_r_norms,
                        const void* centroids_k, const void* centroids_v,
@@ -395,7 +425,8 @@ int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_
                        const void* d_vec_k, const void* d_vec_v, const void* ring_k,
                        const void* ring_v, void* out, int H_q, int H_kv, int c_len,
                        int win_start, int win_len, int ring_cap, float scale, float alpha_k,
-                       float alpha_v, float rope_base, hipStream_t stream) {
+                       float alpha_v, float rope_base, hipStream_t stream,
+                          bool noalloc) {
     if (c_len < 0 || win_len < 0 || (c_len == 0 && win_len == 0)) return -100;
     if (H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || H_q / H_kv > 8) return -100;
     if (win_len > 0 && (ring_cap <= 0 || win_len > ring_cap || win_start < 0)) return -100;
@@ -411,8 +442,15 @@ int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_
                            use_mfma(n_rep, H_kv, 1);
     const int npw = (win_len > 0 && !fused_tail) ? window_parts(win_len) : (win_in_ws ? 1 : 0);
     const int np = npc + npw;
+    const size_t ws_bytes = (size_t)H_q * std::max(np, 1) * 258 * sizeof(float);
     float* ws = nullptr;
-    hipError_t e = workspace((size_t)H_q * std::max(np, 1) * 258 * sizeof(float), &ws);
+    hipError_t e;
+    if (noalloc) {
+        if (ws_bytes > kScratchBytes) return -103;
+        e = scratch_ptr(&ws);
+    } else {
+        e = workspace(ws_bytes, &ws);
+    }
     if (e != hipSuccess) return rc_of(e);
     const int ring = ring_cap > 0 ? ring_cap : 1;
     if (npc > 0) {
@@ -480,6 +518,40 @@ int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_
     }
     return rc_of(khq::launch_combine_gate(ws, static_cast<const __half*>(q_gate),
                                           static_cast<__half*>(out), H_q, np, 1e-8f, stream));
+}
+
+extern "C" {
+
+int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_payload,
+                       const void* v_shared_meta, const void* k_mask, const void* k_norms,
+                       const void* k_r_norms, const void* v_norms, const void* v_r_norms,
+                       const void* centroids_k, const void* centroids_v,
+                       const void* vq_centroids, const void* k_rotor, const void* v_rotor,
+                       const void* d_vec_k, const void* d_vec_v, const void* ring_k,
+                       const void* ring_v, void* out, int H_q, int H_kv, int c_len,
+                       int win_start, int win_len, int ring_cap, float scale, float alpha_k,
+                       float alpha_v, float rope_base, hipStream_t stream) {
+    return attn_step_impl(q_gate, k_payload, v_payload, v_shared_meta, k_mask, k_norms,
+                          k_r_norms, v_norms, v_r_norms, centroids_k, centroids_v,
+                          vq_centroids, k_rotor, v_rotor, d_vec_k, d_vec_v, ring_k, ring_v,
+                          out, H_q, H_kv, c_len, win_start, win_len, ring_cap, scale,
+                          alpha_k, alpha_v, rope_base, stream, false);
+}
+
+int khq_attn_step_noalloc_fp16(const void* q_gate, const void* k_payload, const void* v_payload,
+                       const void* v_shared_meta, const void* k_mask, const void* k_norms,
+                       const void* k_r_norms, const void* v_norms, const void* v_r_norms,
+                       const void* centroids_k, const void* centroids_v,
+                       const void* vq_centroids, const void* k_rotor, const void* v_rotor,
+                       const void* d_vec_k, const void* d_vec_v, const void* ring_k,
+                       const void* ring_v, void* out, int H_q, int H_kv, int c_len,
+                       int win_start, int win_len, int ring_cap, float scale, float alpha_k,
+                       float alpha_v, float rope_base, hipStream_t stream) {
+    return attn_step_impl(q_gate, k_payload, v_payload, v_shared_meta, k_mask, k_norms,
+                          k_r_norms, v_norms, v_r_norms, centroids_k, centroids_v,
+                          vq_centroids, k_rotor, v_rotor, d_vec_k, d_vec_v, ring_k, ring_v,
+                          out, H_q, H_kv, c_len, win_start, win_len, ring_cap, scale,
+                          alpha_k, alpha_v, rope_base, stream, true);
 }
 
 int khq_decompress_fp16(const void* k_payload, const void* v_payload, const void* v_shared_meta,

@@ -31,6 +31,7 @@ SIGNATURES = {
     "launch_khq_partial_rope_fp16": [P, I, I, I, I, F, I, P],
     "launch_khq_gqa_attn_fp16": [P] * 4 + [I, I, I, I, F, P],
     "khq_attn_step_fp16": [P] * 19 + [I, I, I, I, I, I, F, F, F, F, P],
+    "khq_attn_step_noalloc_fp16": [P] * 19 + [I, I, I, I, I, I, F, F, F, F, P],
     "khq_attn_step_batched_fp16": [P, I] + [P] * 7 + [I, I, F, F, F, F, P],
     "khq_decompress_fp16": [P] * 15 + [I, I, I, I, F, F, F, P, I, P, I, P],
     "khq_prefill_attn_fp16": [P, P, P, I, I, I, I, I, I, F, P, P],

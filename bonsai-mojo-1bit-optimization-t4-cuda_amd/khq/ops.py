@@ -169,8 +169,11 @@ def gqa_attn(q_gate, k_cache, v_cache, out, *, seq_len: int, H_q: int, H_kv: int
 
 def attn_step(q_gate, pay: Payload, cents: Centroids, ring_k, ring_v, out, *, H_q: int,
               H_kv: int, c_len: int, win_start: int, win_len: int, ring_cap: int,
-              scale: float, rope_base: float = 1e7, check: bool = True, stream=None) -> int:
-    """khq_attn_step_fp16: both regions + merge + gate in one library call."""
+              scale: float, rope_base: float = 1e7, check: bool = True, stream=None,
+              noalloc: bool = False) -> int:
+    """khq_attn_step_fp16: both regions + merge + gate in one library call
+    (noalloc: khq_attn_step_noalloc_fp16, partials in the library's fixed
+    device array instead of its growable workspace)."""
     _need(q_gate, torch.float16, H_q * 2 * D, "q_gate")
     _need(out, torch.float16, H_q * D, "out")
     if c_len * H_kv > pay.rows:
@@ -178,7 +181,8 @@ def attn_step(q_gate, pay: Payload, cents: Centroids, ring_k, ring_v, out, *, H_
     if win_len > 0:
         _need(ring_k, torch.float16, ring_cap * H_kv * D, "ring_k")
         _need(ring_v, torch.float16, ring_cap * H_kv * D, "ring_v")
-    return call("khq_attn_step_fp16", ptr(q_gate), ptr(pay.kpay), ptr(pay.vpay), ptr(pay.vsm),
+    name = "khq_attn_step_noalloc_fp16" if noalloc else "khq_attn_step_fp16"
+    return call(name, ptr(q_gate), ptr(pay.kpay), ptr(pay.vpay), ptr(pay.vsm),
                 ptr(pay.kmask), ptr(pay.knorm), ptr(pay.krn), ptr(pay.vnorm), ptr(pay.vrn),
                 ptr(cents.cents_k), ptr(cents.cents_v), ptr(cents.vq), ptr(cents.rotor_k),
                 ptr(cents.rotor_v), ptr(cents.d_k), ptr(cents.d_v), ptr(ring_k), ptr(ring_v),

@@ -136,6 +136,26 @@ int khq_attn_step_fp16(const void* q_gate, const void* k_payload, const void* v_
                        int win_start, int win_len, int ring_cap, float scale,
                        float alpha_k, float alpha_v, float rope_base, hipStream_t stream);
 
+/* No counterpart in the reference: khq_attn_step_fp16 for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results; its
+ * split partials live in a fixed 8 MiB device array of the library (one per
+ * GPU, held until the process ends) instead of the growable workspace, so it
+ * calls no hipMalloc / hipFree.  Returns -103 when the partials would exceed
+ * that array (H_q * parts * 258 floats; H_q 24 fits at any context).  Calls
+ * that overlap on one GPU share the array and race. */
+int khq_attn_step_noalloc_fp16(const void* q_gate, const void* k_payload,
+                               const void* v_payload, const void* v_shared_meta,
+                               const void* k_mask, const void* k_norms, const void* k_r_norms,
+                               const void* v_norms, const void* v_r_norms,
+                               const void* centroids_k, const void* centroids_v,
+                               const void* vq_centroids, const void* k_rotor,
+                               const void* v_rotor, const void* d_vec_k, const void* d_vec_v,
+                               const void* ring_k, const void* ring_v, void* out, int H_q,
+                               int H_kv, int c_len, int win_start, int win_len, int ring_cap,
+                               float scale, float alpha_k, float alpha_v, float rope_base,
+                               hipStream_t stream);
+
 /* ---- batched decode (no reference counterpart: the reference decodes one
  * sequence at a time through khq_step, ref:src/khq/runtime.mojo:454-613) ----
  * n_seq independent sequences of one layer (shared constant tensors), one
