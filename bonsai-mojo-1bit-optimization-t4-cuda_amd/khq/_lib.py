@@ -51,9 +51,17 @@ SIGNATURES = {
     "khq_layer_capture_unroped": [P, P, P],
     "khq_layer_step": [P] * 6 + [F, P],
     "khq_layer_prefill": [P] * 6 + [I, F, P],
+    # calibration dumps
+    "khq_dump_create": [ctypes.c_char_p, I, I, I],
+    "khq_dump_destroy": [P],
+    "khq_dump_count": [P, I],
+    "khq_dump_kv": [P, I, P, P, P],
+    "khq_dump_attn": [P, I, P, P, I, I, I, I, F, P],
+    "khq_dump_flush": [P],
 }
 # return types other than int
-RESTYPES = {"khq_layer_create": ctypes.c_void_p, "khq_layer_destroy": None}
+RESTYPES = {"khq_layer_create": ctypes.c_void_p, "khq_layer_destroy": None,
+            "khq_dump_create": ctypes.c_void_p, "khq_dump_destroy": None}
 
 
 class KhqSeq(ctypes.Structure):

@@ -296,6 +296,41 @@ int khq_layer_step(khq_layer* layer, const void* q_gate, const void* k_roped, co
 int khq_layer_prefill(khq_layer* layer, const void* q_gate, const void* k_roped, const void* v,
                       const void* k_unroped, void* out, int n, float scale, hipStream_t stream);
 
+/* ---- calibration dumps (replaces ref:src/models/qwen3_5/khq_dump.mojo) ----
+ * A recorder of the two files the calibration reads:
+ *   <dir>/kv_dump.bin  ('KHQD'): u32 magic | u32 n_layers | u32 dim, then
+ *       n_layers x (u32 layer_id | u32 n_tokens), then per layer n_tokens x dim
+ *       f32 K rows followed by n_tokens x dim f32 V rows (khq_dump.mojo:9-14,
+ *       319-368);
+ *   <dir>/attn_<layer>.bin ('KHQA'): u32 magic | u32 H_q | u32 H_kv | u32 D,
+ *       then per token u32 n_valid (= pos + 1) and H_q x n_valid fp16 softmax
+ *       scores (khq_dump.mojo:87-93, 199-316).
+ * flags: KHQ_DUMP_KV and/or KHQ_DUMP_ATTN.  Returns NULL on bad arguments. */
+#define KHQ_DUMP_KV 1
+#define KHQ_DUMP_ATTN 2
+typedef struct khq_dump khq_dump;
+/* Replaces khq_dump_configure (khq_dump.mojo:28-39); kv_dim = H_kv * head_dim. */
+khq_dump* khq_dump_create(const char* dir, int max_tokens, int kv_dim, int flags);
+void khq_dump_destroy(khq_dump* dump);
+/* Tokens recorded so far for `layer` (KHQD). */
+int khq_dump_count(const khq_dump* dump, int layer);
+/* Replaces khq_dump_kv (khq_dump.mojo:46-85): appends one token's post-norm,
+ * pre-RoPE K and its V (f16 [kv_dim] each, device) to layer `layer`'s rows, as
+ * an asynchronous device copy on `stream`; ignored once max_tokens are held. */
+int khq_dump_kv(khq_dump* dump, int layer, const void* k, const void* v, hipStream_t stream);
+/* Replaces khq_dump_attn (khq_dump.mojo:199-316): appends this token's roped K
+ * (f16 [H_kv][D]) to the layer's history row `pos` (pos 0 clears it), computes
+ * on the GPU the softmax over rows 0..pos of scale * q.k for every query head
+ * (q = first D halves of each q_gate row [H_q][2 D]) and writes the record to
+ * attn_<layer>.bin; synchronises `stream`.  Ignored for pos >= max_tokens or a
+ * shape that differs from the first call's; -104 on a file error. */
+int khq_dump_attn(khq_dump* dump, int layer, const void* q_gate, const void* k_roped, int pos,
+                  int H_q, int H_kv, int D, float scale, hipStream_t stream);
+/* Replaces khq_dump_flush (khq_dump.mojo:319-368): closes the KHQA files and
+ * writes kv_dump.bin (no file when nothing was recorded), then restarts the
+ * KHQD recording.  Synchronises the device. */
+int khq_dump_flush(khq_dump* dump);
+
 #ifdef __cplusplus
 }
 #endif
