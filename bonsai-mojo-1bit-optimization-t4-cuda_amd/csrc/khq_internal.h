@@ -135,6 +135,22 @@ hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks,
 hipError_t launch_attn_ws_batched(const AttnArgs* args, const int2* map, int n_blocks,
                                   int tiles_per_chunk, hipStream_t st);
 
+// Head RMSNorm + unroped capture + partial RoPE + ring writes of one token
+// (D = 256, rot <= 64): q_gate [H_q][512] and k [H_kv][256] in place.
+struct NormRopeArgs {
+    __half* q_gate;
+    __half* k;
+    const __half* v;
+    const float* q_w;  // [256] or NULL
+    const float* k_w;  // [256] or NULL
+    __half* ring_k;
+    __half* ring_v;
+    __half* ring_u;
+    int H_q, H_kv, slot, pos, rot;
+    float eps, theta;
+};
+hipError_t launch_norm_rope(const NormRopeArgs& a, hipStream_t st);
+
 // ---- chunked prefill (khq_prefill.hip)
 // Compressed rows [tok0, tok0 + n_tok) of every KV head -> dense fp16 roped K
 // rows out_k[(key0 + t) * h_kv + h][256] and V^T out_vt[h][256][ld_vt]

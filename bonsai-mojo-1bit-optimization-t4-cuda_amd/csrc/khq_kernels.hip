@@ -831,6 +831,63 @@ __global__ void partial_rope_kernel(__half* __restrict__ vec, int head_dim, int 
     }
 }
 
+// Front of the attention step of one token (ref:src/models/qwen3_5/
+// attention.mojo:329-353) in one launch.  Block b < H_q: query head b of
+// q_gate (stride 2 D); block H_q + j: KV head j of k (stride D), whose
+// block also copies V head j into the ring.  Per head: RMSNorm over D = 256
+// (inv = 1 / sqrt(sum x^2 / D + eps), then (x * inv) * w when a weight is
+// given, rounded to fp16 as the reference stores it, elementwise_sm75.mojo:
+// 362-423), then half-split RoPE of dims 0..rot-1 at `pos` on the fp16 normed
+// values (the partial_rope arithmetic of partial_rope_kernel above).  Outputs:
+// q in place; k: normed (pre-RoPE) to ring_u, roped to k in place and to
+// ring_k; v to ring_v (ring rows `slot`).
+__global__ __launch_bounds__(64) void norm_rope_kernel(NormRopeArgs a) {
+    __shared__ float s_x[256];
+    const int b = blockIdx.x, t = threadIdx.x;
+    const bool is_q = b < a.H_q;
+    const int hk = b - a.H_q;
+    __half* row = is_q ? a.q_gate + (size_t)b * 512 : a.k + (size_t)hk * 256;
+    const float* w = is_q ? a.q_w : a.k_w;
+    const uint2 raw = *reinterpret_cast<const uint2*>(row + 4 * t);
+    const __half2 p0 = __builtin_bit_cast(__half2, raw.x), p1 = __builtin_bit_cast(__half2, raw.y);
+    const float x[4] = {__low2float(p0), __high2float(p0), __low2float(p1), __high2float(p1)};
+    float ss = (x[0] * x[0] + x[1] * x[1]) + (x[2] * x[2] + x[3] * x[3]);
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    const float inv = (1.0f / sqrtf(ss / 256.0f + a.eps)) * 1.0f;
+    __half nh[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        float v = x[c] * inv;
+        if (w) v *= w[4 * t + c];
+        nh[c] = __float2half(v);
+        s_x[4 * t + c] = __half2float(nh[c]);
+    }
+    const size_t slot_off = (size_t)a.slot * a.H_kv * 256 + (size_t)hk * 256 + 4 * t;
+    if (!is_q) {
+        *reinterpret_cast<uint2*>(a.ring_u + slot_off) =
+            uint2{__builtin_bit_cast(uint32_t, __halves2half2(nh[0], nh[1])),
+                  __builtin_bit_cast(uint32_t, __halves2half2(nh[2], nh[3]))};
+        *reinterpret_cast<uint2*>(a.ring_v + slot_off) =
+            *reinterpret_cast<const uint2*>(a.v + (size_t)hk * 256 + 4 * t);
+    }
+    __syncthreads();
+    const int half_rot = a.rot / 2;
+    if (t < half_rot) {
+        const float ex = -(float)(2 * t) / (float)a.rot;
+        const float fr = expf(logf(a.theta) * ex);
+        const float mt = (float)a.pos * fr;
+        const float c = cosf(mt), s = sinf(mt);
+        const float x0 = s_x[t], x1 = s_x[t + half_rot];
+        s_x[t] = __half2float(__float2half(fmaf(x0, c, -(x1 * s))));
+        s_x[t + half_rot] = __half2float(__float2half(fmaf(x0, s, x1 * c)));
+    }
+    __syncthreads();
+    const uint2 outw = uint2{__builtin_bit_cast(uint32_t, __floats2half2_rn(s_x[4 * t], s_x[4 * t + 1])),
+                             __builtin_bit_cast(uint32_t, __floats2half2_rn(s_x[4 * t + 2], s_x[4 * t + 3]))};
+    *reinterpret_cast<uint2*>(row + 4 * t) = outw;
+    if (!is_q) *reinterpret_cast<uint2*>(a.ring_k + slot_off) = outw;
+}
+
 // ------------------------------------------------------------ dispatchers
 hipError_t launch_attn_parts(const AttnArgs& a, int n_rep, dim3 grid, hipStream_t st) {
     switch (n_rep) {
@@ -914,6 +971,11 @@ hipError_t launch_partial_rope(__half* vec, int num_heads, int head_dim, int rot
                                float theta, int stride, hipStream_t st) {
     hipLaunchKernelGGL(partial_rope_kernel, dim3(num_heads), dim3(64), 0, st, vec, head_dim,
                        rotary_dim, pos, theta, stride);
+    return hipGetLastError();
+}
+
+hipError_t launch_norm_rope(const NormRopeArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL(norm_rope_kernel, dim3(a.H_q + a.H_kv), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 

@@ -45,6 +45,9 @@ struct khq_layer {
     // raw tokens [raw_lo, raw_hi) already copied (empty when raw_lo >= raw_hi)
     __half *dk = nullptr, *dvt = nullptr;
     int d_keys = 0, d_ld = 0, dec_hi = 0, raw_lo = 0, raw_hi = 0;
+    // calibration dumps of khq_layer_attention_step (not owned)
+    khq_dump* dump = nullptr;
+    int dump_layer = 0;
 };
 
 namespace {
@@ -216,6 +219,10 @@ int khq_layer_capture_unroped(khq_layer* L, const void* k_unroped, hipStream_t s
                                       slot, L->H_kv * kD, stream);
 }
 
+// khq_step after the ring writes of the token (ref runtime.mojo:489-613).
+static int step_after_ring_write(khq_layer* L, const void* q_gate, void* out, float scale,
+                                 hipStream_t stream);
+
 int khq_layer_step(khq_layer* L, const void* q_gate, const void* k_roped, const void* v,
                    const void* k_unroped, void* out, float scale, hipStream_t stream) {
     if (!L || !q_gate || !k_roped || !v || !out) return -100;
@@ -224,6 +231,53 @@ int khq_layer_step(khq_layer* L, const void* q_gate, const void* k_roped, const 
     int rc = launch_khq_ring_write_fp16(L->ring_k, L->ring_v, k_unroped ? L->ring_u : nullptr,
                                         k_roped, v, k_unroped, slot, kv, stream);
     if (rc) return rc;
+    return step_after_ring_write(L, q_gate, out, scale, stream);
+}
+
+int khq_layer_set_dump(khq_layer* L, khq_dump* dump, int layer_id) {
+    if (!L || layer_id < 0) return -100;
+    L->dump = dump;
+    L->dump_layer = layer_id;
+    return 0;
+}
+
+int khq_layer_attention_step(khq_layer* L, void* q_gate, void* k, const void* v,
+                             const float* q_norm_w, const float* k_norm_w, float eps, int pos,
+                             void* out, float scale, hipStream_t stream) {
+    if (!L || !q_gate || !k || !v || !out || pos < 0 || !(eps >= 0.0f)) return -100;
+    const int slot = L->write_pos % kRing;
+    khq::NormRopeArgs a{};
+    a.q_gate = static_cast<__half*>(q_gate);
+    a.k = static_cast<__half*>(k);
+    a.v = static_cast<const __half*>(v);
+    a.q_w = q_norm_w;
+    a.k_w = k_norm_w;
+    a.ring_k = L->ring_k;
+    a.ring_v = L->ring_v;
+    a.ring_u = L->ring_u;
+    a.H_q = L->H_q;
+    a.H_kv = L->H_kv;
+    a.slot = slot;
+    a.pos = pos;
+    a.rot = 64;  // the compressed kernels' rotary width (dims 0..63)
+    a.eps = eps;
+    a.theta = L->rope_base;
+    hipError_t e = khq::launch_norm_rope(a, stream);
+    if (e != hipSuccess) return (int)e;
+    if (L->dump) {  // calibration dumps (ref attention.mojo:340-341, 355-356)
+        const size_t kv = (size_t)L->H_kv * kD;
+        int rc = khq_dump_kv(L->dump, L->dump_layer, L->ring_u + (size_t)slot * kv, v, stream);
+        if (rc) return rc;
+        rc = khq_dump_attn(L->dump, L->dump_layer, q_gate, k, pos, L->H_q, L->H_kv, kD, scale,
+                           stream);
+        if (rc) return rc;
+    }
+    return step_after_ring_write(L, q_gate, out, scale, stream);
+}
+
+static int step_after_ring_write(khq_layer* L, const void* q_gate, void* out, float scale,
+                                 hipStream_t stream) {
+    int rc = 0;
     L->raw_lo = L->raw_hi = 0;  // the dense key space does not get this token
     L->write_pos += 1;
     if (event_due(L, L->write_pos)) {

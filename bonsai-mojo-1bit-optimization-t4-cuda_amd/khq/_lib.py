@@ -58,6 +58,8 @@ SIGNATURES = {
     "khq_dump_kv": [P, I, P, P, P],
     "khq_dump_attn": [P, I, P, P, I, I, I, I, F, P],
     "khq_dump_flush": [P],
+    "khq_layer_set_dump": [P, P, I],
+    "khq_layer_attention_step": [P] * 6 + [F, I, P, F, P],
 }
 # return types other than int
 RESTYPES = {"khq_layer_create": ctypes.c_void_p, "khq_layer_destroy": None,

@@ -299,6 +299,37 @@ class NativeKhqLayer:
             raise KhqError("khq_layer_step", rc)
         return rc == 1
 
+    def attention_step(self, q_gate, k, v, out, scale: float, *, pos: int, q_norm_w=None,
+                       k_norm_w=None, eps: float = 1e-6) -> bool:
+        """khq_layer_attention_step: head RMSNorm of q and k (in place), unroped
+        capture, partial RoPE at `pos` (in place), ring writes, dumps, then the
+        KHQ step (ref:src/models/qwen3_5/attention.mojo:319-365)."""
+        from ._lib import KhqError, stream_handle
+
+        for t, n in ((q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w")):
+            if t is not None and (t.dtype != torch.float32 or t.numel() != 256):
+                raise ValueError(f"{n} must be float32 [256]")
+        rc = self._lib.khq_layer_attention_step(
+            self.handle, q_gate.data_ptr(), k.data_ptr(), v.data_ptr(),
+            q_norm_w.data_ptr() if q_norm_w is not None else None,
+            k_norm_w.data_ptr() if k_norm_w is not None else None, eps, pos, out.data_ptr(),
+            scale, stream_handle())
+        if rc == -102:
+            raise RuntimeError(f"raw window exceeds the {RING}-slot ring (cap {self.cap} reached)")
+        if rc < 0 or rc > 1:
+            raise KhqError("khq_layer_attention_step", rc)
+        return rc == 1
+
+    def set_dump(self, recorder, layer_id: int) -> None:
+        """Attach a khq.dump.Recorder (None detaches) for attention_step."""
+        from ._lib import KhqError
+
+        rc = self._lib.khq_layer_set_dump(self.handle, recorder.handle if recorder else None,
+                                          layer_id)
+        if rc:
+            raise KhqError("khq_layer_set_dump", rc)
+        self._dump = recorder  # keep it alive while attached
+
     def prefill(self, q_gate, k_roped, v, k_unroped, out, scale: float) -> int:
         """khq_layer_prefill: n tokens at once (q_gate f16 [n][H_q][512], k_roped /
         v / k_unroped f16 [n][H_kv][256], out f16 [n][H_q][256]), the results of

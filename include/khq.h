@@ -331,6 +331,26 @@ int khq_dump_attn(khq_dump* dump, int layer, const void* q_gate, const void* k_r
  * KHQD recording.  Synchronises the device. */
 int khq_dump_flush(khq_dump* dump);
 
+/* Attaches a dump recorder to a layer (NULL detaches): its
+ * khq_layer_attention_step then records the token under `layer_id`
+ * (ref attention.mojo:340-341, 355-356).  The recorder is not owned. */
+int khq_layer_set_dump(khq_layer* layer, khq_dump* dump, int layer_id);
+
+/* Replaces the KHQ part of qwen3_5_gated_attention_step_gpu_from_proj
+ * (ref:src/models/qwen3_5/attention.mojo:319-365) for one token, from the
+ * projections: head RMSNorm of q (q_gate [H_q][512], the q halves, in place)
+ * and of k ([H_kv][256], in place) with optional f32 [256] weights (NULL = no
+ * weight, the has_norms = False path) and eps; the normed pre-RoPE K captured
+ * into ring_u; half-split RoPE of dims 0..63 at position `pos` (base = the
+ * layer's rope_base) on q and k; the roped K and v written to the ring; the
+ * attached dumps, if any; then khq_step (compression event, two-region
+ * attention, merge, gate) into out f16 [H_q][256].  q_gate and k hold the
+ * normed, roped values afterwards, as in the reference.  Returns as
+ * khq_layer_step. */
+int khq_layer_attention_step(khq_layer* layer, void* q_gate, void* k, const void* v,
+                             const float* q_norm_w, const float* k_norm_w, float eps, int pos,
+                             void* out, float scale, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
