@@ -1,0 +1,1418 @@
+// khq_calib.hip -- KHQ calibration on the GPU: the launch_cal_op steps
+// (ops 1..10) and the SmartVQ trainer launch_cal_svq_train of
+// ref:src/csrc/qmv_sm75_kernel.cu:2012-3349, 4434-4810, driven by
+// ref:src/khq/calib.mojo:285-566 (host driver: khq/calib.py here).
+//
+// Calibration is offline and small next to decode, so the kernels are
+// written for clarity and determinism first: reductions over rows go through
+// double-precision accumulators (the reference sums in float, sequentially or
+// with float atomics whose order varies run to run), per-row work runs one
+// 64-lane wavefront per row (FWHT across lanes) instead of one thread per row
+// with 2 KB of private arrays, and the dense products of the attention-aware
+// loss are LDS-tiled batched matrix products.  Results match the reference's
+// algorithm up to float rounding; the steps that pick a discrete winner
+// (tournaments, argmins) do so with the reference's tie rules.
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include <cmath>
+#include <cstdio>
+#include <vector>
+
+#include "khq.h"
+
+namespace khq {
+namespace cal {
+
+constexpr int D = 256, NP = 64, CB = NP * 768;  // codebook floats (64 x 256 x 3)
+constexpr float FS = 0.0625f;                   // 1 / sqrt(256)
+constexpr int OUT_MAX = 50;
+
+inline int blocks(long n, int t) { return (int)((n + t - 1) / t); }
+
+__device__ __forceinline__ float fp16r(float x) { return __half2float(__float2half(x)); }
+
+// ---- wavefront helpers (64 lanes, 4 values per lane = one 256-row)
+__device__ __forceinline__ float wsum(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wmax(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+// Natural-order FWHT-256 of a row held as lane l -> elements 4 l .. 4 l + 3:
+// the two in-lane stages (bits 0, 1), then lane bits 0..5 (element bits 2..7).
+__device__ __forceinline__ void fwht_row(float (&q)[4], int lane) {
+    float a = q[0] + q[1], b = q[0] - q[1], c = q[2] + q[3], d = q[2] - q[3];
+    q[0] = a + c; q[1] = b + d; q[2] = a - c; q[3] = b - d;
+    for (int m = 1; m < 64; m <<= 1) {
+        const bool lo = (lane & m) == 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float o = __shfl_xor(q[j], m, 64);
+            q[j] = lo ? q[j] + o : o - q[j];
+        }
+    }
+}
+
+// ------------------------------------------------------------------ op 1
+// norm[r] = sqrt(sum x^2 + 1e-8); base[r] = FWHT(x * fp16(d) / (norm + 1e-8)) / 16
+// (ref .cu:2019-2070).  One wavefront per row.
+__global__ __launch_bounds__(256) void fwht_base_kernel(const float* __restrict__ x,
+                                                        const float* __restrict__ d,
+                                                        float* __restrict__ norm,
+                                                        float* __restrict__ base, int rows) {
+    const int lane = threadIdx.x & 63;
+    const long r = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float4 v = *reinterpret_cast<const float4*>(x + r * D + 4 * lane);
+    float q[4] = {v.x, v.y, v.z, v.w};
+    const float n = sqrtf(wsum((q[0] * q[0] + q[1] * q[1]) + (q[2] * q[2] + q[3] * q[3])) + 1e-8f);
+    if (lane == 0) norm[r] = n;
+#pragma unroll
+    for (int j = 0; j < 4; j++) q[j] = (q[j] * fp16r(d[4 * lane + j])) / (n + 1e-8f);
+    fwht_row(q, lane);
+    *reinterpret_cast<float4*>(base + r * D + 4 * lane) =
+        make_float4(q[0] * FS, q[1] * FS, q[2] * FS, q[3] * FS);
+}
+
+// ------------------------------------------------------------------ op 3
+// out[n][p][c] = sum_k in[n][4p + k] rp[16p + 4k + c]  (ref .cu:2073-2085)
+__global__ void rotate_kernel(const float* __restrict__ in, const float* __restrict__ rp,
+                              float* __restrict__ out, int rows) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)rows * NP) return;
+    const int p = (int)(i & 63);
+    const float4 v = *reinterpret_cast<const float4*>(in + i * 4);
+    const float* R = rp + p * 16;
+    float4 o;
+    o.x = v.x * R[0] + v.y * R[4] + v.z * R[8] + v.w * R[12];
+    o.y = v.x * R[1] + v.y * R[5] + v.z * R[9] + v.w * R[13];
+    o.z = v.x * R[2] + v.y * R[6] + v.z * R[10] + v.w * R[14];
+    o.w = v.x * R[3] + v.y * R[7] + v.z * R[11] + v.w * R[15];
+    *reinterpret_cast<float4*>(out + i * 4) = o;
+}
+
+// inverse rotation back to the FWHT domain: dst[p][c] = sum_k src[p][k] rp[16p + 4c + k]
+__global__ void invrot_kernel(const float* __restrict__ src, const float* __restrict__ rp,
+                              float* __restrict__ dst, int rows) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)rows * NP) return;
+    const int p = (int)(i & 63);
+    const float4 v = *reinterpret_cast<const float4*>(src + i * 4);
+    const float* R = rp + p * 16;
+    float4 o;
+    o.x = v.x * R[0] + v.y * R[1] + v.z * R[2] + v.w * R[3];
+    o.y = v.x * R[4] + v.y * R[5] + v.z * R[6] + v.w * R[7];
+    o.z = v.x * R[8] + v.y * R[9] + v.z * R[10] + v.w * R[11];
+    o.w = v.x * R[12] + v.y * R[13] + v.z * R[14] + v.w * R[15];
+    *reinterpret_cast<float4*>(dst + i * 4) = o;
+}
+
+// ---- per-dim column statistics over rows (double accumulators)
+// acc[0][d] += x, acc[1][d] += |x|, acc[2][d] += (x - mean[d])^2 (pass 2)
+__global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ x, int rows,
+                                                     const double* __restrict__ mean,
+                                                     double* __restrict__ acc) {
+    const int d = threadIdx.x;
+    const int per = (rows + gridDim.x - 1) / gridDim.x;
+    const int r0 = blockIdx.x * per, r1 = min(rows, r0 + per);
+    double s = 0.0, a = 0.0;
+    for (int r = r0; r < r1; r++) {
+        const double v = x[(long)r * D + d];
+        if (mean) {
+            const double dv = v - mean[d];
+            s += dv * dv;
+        } else {
+            s += v;
+            a += fabs(v);
+        }
+    }
+    if (r1 > r0) {
+        if (mean) {
+            atomicAdd(&acc[2 * D + d], s);
+        } else {
+            atomicAdd(&acc[d], s);
+            atomicAdd(&acc[D + d], a);
+        }
+    }
+}
+__global__ void colmean_kernel(const double* __restrict__ acc, double* __restrict__ mean,
+                               int rows) {
+    const int d = threadIdx.x;
+    mean[d] = acc[d] / rows;
+}
+
+// ------------------------------------------------------------------ op 2
+// K static (ref .cu:2645-2681): sigma = population std per dim,
+// ts = 16 / sqrt(sum 0.528756 (0.935 sigma)^2 + 0.464545 sigma^2),
+// cents = [0, -c, +c, +c] with c = 0.935 sigma ts.
+__global__ void kstatic_kernel(const double* __restrict__ acc, int rows, float* __restrict__ cents,
+                               float* __restrict__ ts_out) {
+    __shared__ float s_sig[D];
+    __shared__ double s_red[D];
+    const int d = threadIdx.x;
+    const float sg = sqrtf((float)(acc[2 * D + d] / rows));
+    s_sig[d] = sg;
+    const float cb = 0.9350f * sg;
+    s_red[d] = (double)(0.528756f * cb * cb + 0.464545f * sg * sg);
+    __syncthreads();
+    for (int o = D / 2; o >= 1; o >>= 1) {
+        if (d < o) s_red[d] += s_red[d + o];
+        __syncthreads();
+    }
+    const float ts = 16.0f / sqrtf((float)s_red[0]);
+    const float c = 0.9350f * s_sig[d] * ts;
+    cents[d] = 0.0f;
+    cents[D + d] = -c;
+    cents[2 * D + d] = c;
+    cents[3 * D + d] = c;
+    if (d == 0) ts_out[0] = ts;
+}
+
+// ------------------------------------------------------------------ op 4
+// PCA per patch (ref .cu:3071-3145): uncentred 4x4 moment + 1e-3 I,
+// 5 Jacobi sweeps over the pairs (0,1) (0,2) (0,3) (1,2) (1,3) (2,3),
+// eigenvalues sorted descending; rotor column c takes eigenvector
+// order[{1, 2, 3, 0}[c]] (the largest-variance direction goes to dim 3).
+__global__ __launch_bounds__(256) void patch_moment_kernel(const float* __restrict__ base,
+                                                           const float* __restrict__ tgt, int rows,
+                                                           double* __restrict__ mom) {
+    // thread = (patch, i, j), 1024 of them over 4 blocks; rows cut over gridDim.y
+    const int id = blockIdx.x * 256 + threadIdx.x;  // < 1024
+    const int p = id >> 4, i = (id >> 2) & 3, j = id & 3;
+    const int per = (rows + gridDim.y - 1) / gridDim.y;
+    const int r0 = blockIdx.y * per, r1 = min(rows, r0 + per);
+    const float* b2 = tgt ? tgt : base;
+    double s = 0.0;
+    for (int r = r0; r < r1; r++)
+        s += (double)base[(long)r * D + 4 * p + i] * (double)b2[(long)r * D + 4 * p + j];
+    if (r1 > r0) atomicAdd(&mom[id], s);
+}
+
+__global__ void pca_kernel(const double* __restrict__ mom, float* __restrict__ out_rp) {
+    const int p = threadIdx.x;
+    if (p >= NP) return;
+    float a[16], v[16];
+    for (int i = 0; i < 16; i++) {
+        a[i] = (float)mom[p * 16 + i];
+        v[i] = (i % 5 == 0) ? 1.0f : 0.0f;
+    }
+    for (int i = 0; i < 4; i++) a[i * 5] += 1e-3f;
+    const int P[6] = {0, 0, 0, 1, 1, 2}, Q[6] = {1, 2, 3, 2, 3, 3};
+    for (int sweep = 0; sweep < 5; sweep++) {
+        for (int k = 0; k < 6; k++) {
+            const int pi = P[k], qi = Q[k];
+            const float apq = a[pi * 4 + qi], app = a[pi * 5], aqq = a[qi * 5];
+            const float phi = 0.5f * atan2f(2.0f * apq, aqq - app);
+            const float c = cosf(phi), s = sinf(phi);
+            float cp[4], cq[4];
+            for (int i = 0; i < 4; i++) {
+                cp[i] = c * a[i * 4 + pi] - s * a[i * 4 + qi];
+                cq[i] = s * a[i * 4 + pi] + c * a[i * 4 + qi];
+            }
+            for (int i = 0; i < 4; i++) {
+                a[i * 4 + pi] = cp[i];
+                a[i * 4 + qi] = cq[i];
+                a[pi * 4 + i] = cp[i];
+                a[qi * 4 + i] = cq[i];
+            }
+            a[pi * 5] = c * c * app - 2.0f * s * c * apq + s * s * aqq;
+            a[qi * 5] = s * s * app + 2.0f * s * c * apq + c * c * aqq;
+            a[pi * 4 + qi] = 0.0f;
+            a[qi * 4 + pi] = 0.0f;
+            for (int i = 0; i < 4; i++) {
+                const float vp = v[i * 4 + pi], vq = v[i * 4 + qi];
+                v[i * 4 + pi] = c * vp - s * vq;
+                v[i * 4 + qi] = s * vp + c * vq;
+            }
+        }
+    }
+    int order[4] = {0, 1, 2, 3};
+    for (int i = 0; i < 4; i++)
+        for (int j = i + 1; j < 4; j++)
+            if (a[order[j] * 5] > a[order[i] * 5]) {
+                const int t = order[i];
+                order[i] = order[j];
+                order[j] = t;
+            }
+    const int sel[4] = {1, 2, 3, 0};
+    for (int c = 0; c < 4; c++)
+        for (int i = 0; i < 4; i++) out_rp[p * 16 + i * 4 + c] = v[i * 4 + order[sel[c]]];
+}
+
+// ------------------------------------------------------------------ op 5
+// k-means with 4 centroids per dim (ref .cu:3147-3183): initial centroids
+// (mn + (mx - mn) k / 3) * 0.8 from the dim's range, 20 Lloyd iterations,
+// first minimum wins, an empty cluster's centroid becomes 0.
+__global__ __launch_bounds__(256) void colrange_kernel(const float* __restrict__ x, int rows,
+                                                       float* __restrict__ mn,
+                                                       float* __restrict__ mx) {
+    const int d = threadIdx.x;
+    const int per = (rows + gridDim.x - 1) / gridDim.x;
+    const int r0 = blockIdx.x * per, r1 = min(rows, r0 + per);
+    if (r1 <= r0) return;
+    float lo = x[(long)r0 * D + d], hi = lo;
+    for (int r = r0 + 1; r < r1; r++) {
+        const float v = x[(long)r * D + d];
+        lo = fminf(lo, v);
+        hi = fmaxf(hi, v);
+    }
+    // float min / max through ordered-int atomics
+    auto key = [](float f) {
+        const int i = __float_as_int(f);
+        return i >= 0 ? i : (int)(0x80000000u - (unsigned)i) ;
+    };
+    atomicMin(reinterpret_cast<int*>(mn) + d, key(lo));
+    atomicMax(reinterpret_cast<int*>(mx) + d, key(hi));
+}
+__device__ __forceinline__ float unkey(int k) {
+    return __int_as_float(k >= 0 ? k : (int)(0x80000000u - (unsigned)k));
+}
+__global__ void km4_init_kernel(const float* __restrict__ mn, const float* __restrict__ mx,
+                                float* __restrict__ c) {
+    const int d = threadIdx.x;
+    const float lo = unkey(reinterpret_cast<const int*>(mn)[d]);
+    const float hi = unkey(reinterpret_cast<const int*>(mx)[d]);
+    for (int k = 0; k < 4; k++) c[k * D + d] = (lo + (hi - lo) * ((float)k / 3.0f)) * 0.8f;
+}
+__global__ __launch_bounds__(256) void km4_assign_kernel(const float* __restrict__ x, int rows,
+                                                         const float* __restrict__ c,
+                                                         double* __restrict__ acc) {
+    const int d = threadIdx.x;
+    const int per = (rows + gridDim.x - 1) / gridDim.x;
+    const int r0 = blockIdx.x * per, r1 = min(rows, r0 + per);
+    const float c0 = c[d], c1 = c[D + d], c2 = c[2 * D + d], c3 = c[3 * D + d];
+    double s[4] = {0, 0, 0, 0}, n[4] = {0, 0, 0, 0};
+    for (int r = r0; r < r1; r++) {
+        const float v = x[(long)r * D + d];
+        int bk = 0;
+        float bd = (v - c0) * (v - c0);
+        const float dd1 = (v - c1) * (v - c1), dd2 = (v - c2) * (v - c2), dd3 = (v - c3) * (v - c3);
+        if (dd1 < bd) { bd = dd1; bk = 1; }
+        if (dd2 < bd) { bd = dd2; bk = 2; }
+        if (dd3 < bd) { bd = dd3; bk = 3; }
+        s[bk] += v;
+        n[bk] += 1.0;
+    }
+    if (r1 > r0)
+        for (int k = 0; k < 4; k++) {
+            atomicAdd(&acc[k * D + d], s[k]);
+            atomicAdd(&acc[(4 + k) * D + d], n[k]);
+        }
+}
+__global__ void km4_update_kernel(float* __restrict__ c, double* __restrict__ acc) {
+    const int d = threadIdx.x;
+    for (int k = 0; k < 4; k++) {
+        c[k * D + d] = (float)(acc[k * D + d] / fmax(acc[(4 + k) * D + d], 1.0));
+        acc[k * D + d] = 0.0;
+        acc[(4 + k) * D + d] = 0.0;
+    }
+}
+
+// ------------------------------------------------------------------ op 6
+// k-means VQ, 256 codewords of dims 0..2 per patch (ref .cu:3185-3249):
+// codeword (p, k) starts as row idx of a per-entry xorshift draw, 30
+// iterations, first minimum wins, an empty cluster keeps its codeword.
+__global__ void vq_init_kernel(const float* __restrict__ data, float* __restrict__ C,
+                               unsigned seed, int rows) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= NP * 256) return;
+    const int p = i >> 8, k = i & 255;
+    unsigned s = seed ^ ((unsigned)i * 2654435761u + 1u);
+    s ^= s << 13;
+    s ^= s >> 17;
+    s ^= s << 5;
+    int idx = (int)((float)(s & 0xFFFFFFu) / 16777216.0f * (float)rows);
+    if (idx >= rows) idx = rows - 1;
+    for (int c = 0; c < 3; c++) C[p * 768 + k * 3 + c] = data[(long)idx * D + p * 4 + c];
+}
+// nearest codeword of (row, patch): first minimum wins
+__device__ __forceinline__ int nearest(const float* __restrict__ cb, float v0, float v1, float v2,
+                                       float* best) {
+    int bk = 0;
+    float bd = 1e30f;
+    for (int k = 0; k < 256; k++) {
+        const float d0 = v0 - cb[k * 3], d1 = v1 - cb[k * 3 + 1], d2 = v2 - cb[k * 3 + 2];
+        const float dd = d0 * d0 + d1 * d1 + d2 * d2;
+        if (dd < bd) {
+            bd = dd;
+            bk = k;
+        }
+    }
+    if (best) *best = bd;
+    return bk;
+}
+// block = 256 threads of one patch's rows; codebook of the patch in LDS
+__global__ __launch_bounds__(256) void vq_assign_kernel(const float* __restrict__ data,
+                                                        const float* __restrict__ C, int rows,
+                                                        double* __restrict__ sums) {
+    __shared__ float s_cb[768];
+    const int p = blockIdx.y;
+    for (int i = threadIdx.x; i < 768; i += 256) s_cb[i] = C[p * 768 + i];
+    __syncthreads();
+    for (long r = (long)blockIdx.x * 256 + threadIdx.x; r < rows; r += (long)gridDim.x * 256) {
+        const float* v = data + r * D + p * 4;
+        const int bk = nearest(s_cb, v[0], v[1], v[2], nullptr);
+        double* sp = sums + ((long)p * 256 + bk) * 4;
+        atomicAdd(&sp[0], (double)v[0]);
+        atomicAdd(&sp[1], (double)v[1]);
+        atomicAdd(&sp[2], (double)v[2]);
+        atomicAdd(&sp[3], 1.0);
+    }
+}
+__global__ void vq_update_kernel(float* __restrict__ C, double* __restrict__ sums) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= NP * 256) return;
+    double* sp = sums + (long)i * 4;
+    if (sp[3] > 0.0)
+        for (int c = 0; c < 3; c++) C[i * 3 + c] = (float)(sp[c] / sp[3]);
+    sp[0] = sp[1] = sp[2] = sp[3] = 0.0;
+}
+
+// ------------------------------------------------------------------ op 7
+// Procrustes-Lloyd step (ref .cu:3266-3349): target = nearest codeword on
+// dims 0..2 of the rotated row, its own dim 3; M = base^T target per patch;
+// rotor = orthogonal polar factor of M by 12 Newton-Schulz iterations from
+// M / |M|_F (kept unchanged if that produced a NaN).
+__global__ __launch_bounds__(256) void procrustes_target_kernel(const float* __restrict__ rot,
+                                                                const float* __restrict__ vq,
+                                                                float* __restrict__ tgt, int rows) {
+    __shared__ float s_cb[768];
+    const int p = blockIdx.y;
+    for (int i = threadIdx.x; i < 768; i += 256) s_cb[i] = vq[p * 768 + i];
+    __syncthreads();
+    for (long r = (long)blockIdx.x * 256 + threadIdx.x; r < rows; r += (long)gridDim.x * 256) {
+        const float* v = rot + r * D + p * 4;
+        const int bk = nearest(s_cb, v[0], v[1], v[2], nullptr);
+        float* t = tgt + r * D + p * 4;
+        t[0] = s_cb[bk * 3];
+        t[1] = s_cb[bk * 3 + 1];
+        t[2] = s_cb[bk * 3 + 2];
+        t[3] = v[3];
+    }
+}
+__global__ void polar_ns_kernel(const double* __restrict__ mom, float* __restrict__ rp) {
+    const int p = threadIdx.x;
+    if (p >= NP) return;
+    float X[16], G[16], Y[16];
+    float fro = 0.0f;
+    for (int i = 0; i < 16; i++) {
+        X[i] = (float)mom[p * 16 + i];
+        fro += X[i] * X[i];
+    }
+    fro = sqrtf(fro + 1e-8f);
+    for (int i = 0; i < 16; i++) X[i] /= fro;
+    for (int it = 0; it < 12; it++) {
+        for (int i = 0; i < 4; i++)
+            for (int j = 0; j < 4; j++) {
+                float s = 0.0f;
+                for (int k = 0; k < 4; k++) s += X[k * 4 + i] * X[k * 4 + j];
+                G[i * 4 + j] = (i == j ? 3.0f : 0.0f) - s;
+            }
+        for (int i = 0; i < 4; i++)
+            for (int j = 0; j < 4; j++) {
+                float s = 0.0f;
+                for (int k = 0; k < 4; k++) s += X[i * 4 + k] * G[k * 4 + j];
+                Y[i * 4 + j] = 0.5f * s;
+            }
+        for (int i = 0; i < 16; i++) X[i] = Y[i];
+    }
+    bool ok = true;
+    for (int i = 0; i < 16; i++) ok = ok && (X[i] == X[i]);
+    if (ok)
+        for (int i = 0; i < 16; i++) rp[p * 16 + i] = X[i];
+}
+
+// ----------------------------------------------------------------- op 10
+// head-major reorder: out[(h n + t)][i] = in[(t heads + h)][i]
+__global__ void headmajor_kernel(const float* __restrict__ in, float* __restrict__ out,
+                                 int n_tok, int heads) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)n_tok * heads * D) return;
+    const long r = i >> 8;
+    const int h = (int)(r / n_tok), t = (int)(r % n_tok);
+    out[i] = in[((long)t * heads + h) * D + (i & 255)];
+}
+
+// ---------------------------------------------------------- ops 8 / 9
+// Round trips of the SmartK / SmartV tournaments (ref .cu:2722-3025), one
+// wavefront per row.  K follows the calibration's own compressor, which
+// differs from the runtime one (reproduced, not fixed): an outlier candidate
+// (|p| > 1.6 f_s) is stored as code 1 / 2 by its sign, never as code 3, and
+// counts in the c_base_mult sums, so its residual never reaches the decoder
+// and the round trip is sign * cents_k[2][i] * mult for codes 1, 2.  The K
+// rotor is the identity here.  V: VQ and dim-3 codes with the fixed codebook
+// and dim-3 centroids, energy correction rounded to fp16.
+__global__ __launch_bounds__(256) void roundtrip_k_kernel(const float* __restrict__ proj,
+                                                          const float* __restrict__ norms,
+                                                          const float* __restrict__ cents,
+                                                          const float* __restrict__ rp,
+                                                          const float* __restrict__ d,
+                                                          float alpha, float* __restrict__ rec,
+                                                          int rows) {
+    const int lane = threadIdx.x & 63;
+    const long r = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float4 pv4 = *reinterpret_cast<const float4*>(proj + r * D + 4 * lane);
+    const float pv[4] = {pv4.x, pv4.y, pv4.z, pv4.w};
+    const float* cb = cents + 2 * D;
+    int sg[4];
+    float sn = 0.0f, sc = 0.0f;
+    for (int j = 0; j < 4; j++) {
+        const float a = fabsf(pv[j]);
+        sg[j] = a > 1.60f * FS ? (pv[j] > 0.0f ? 1 : -1)
+                               : (pv[j] > 0.47f * FS ? 1 : (pv[j] < -0.47f * FS ? -1 : 0));
+        if (sg[j] != 0) {
+            sn += a;
+            sc += fp16r(cb[4 * lane + j]);
+        }
+    }
+    sn = wsum(sn);
+    sc = wsum(sc);
+    float mult = sc > 1e-5f ? sn / sc : 1.0f;
+    if (mult < 0.1f || mult > 10.0f || mult != mult) mult = 1.0f;
+    // the decoder reads (u32)(mult * 1000) / 1000 with the same clamp
+    float m2 = (float)(unsigned)(mult * 1000.0f) / 1000.0f;
+    if (m2 < 0.1f || m2 > 10.0f) m2 = 1.0f;
+    const float nrm = norms[r];
+    float kv[4];
+    for (int j = 0; j < 4; j++) kv[j] = (float)sg[j] * (cb[4 * lane + j] * m2) * alpha * nrm;
+    // inverse rotor (patch = lane), FWHT, / (256 d)
+    const float* R = rp + lane * 16;
+    float q[4];
+    for (int c = 0; c < 4; c++)
+        q[c] = kv[0] * R[c * 4] + kv[1] * R[c * 4 + 1] + kv[2] * R[c * 4 + 2] + kv[3] * R[c * 4 + 3];
+    fwht_row(q, lane);
+    float4 o;
+    o.x = q[0] / (256.0f * d[4 * lane]);
+    o.y = q[1] / (256.0f * d[4 * lane + 1]);
+    o.z = q[2] / (256.0f * d[4 * lane + 2]);
+    o.w = q[3] / (256.0f * d[4 * lane + 3]);
+    *reinterpret_cast<float4*>(rec + r * D + 4 * lane) = o;
+}
+
+__global__ __launch_bounds__(256) void roundtrip_v_kernel(const float* __restrict__ proj,
+                                                          const float* __restrict__ norms,
+                                                          const float* __restrict__ cents,
+                                                          const float* __restrict__ vq,
+                                                          const float* __restrict__ rp,
+                                                          const float* __restrict__ d, float alpha,
+                                                          float* __restrict__ rec, int rows) {
+    const int lane = threadIdx.x & 63;  // = patch
+    const long r = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float4 pv4 = *reinterpret_cast<const float4*>(proj + r * D + 4 * lane);
+    const float* cbp = vq + lane * 768;
+    int bk = 0;
+    float bd = 1e30f;
+    for (int k = 0; k < 256; k++) {
+        const float d0 = pv4.x - fp16r(cbp[k * 3]) * alpha;
+        const float d1 = pv4.y - fp16r(cbp[k * 3 + 1]) * alpha;
+        const float d2 = pv4.z - fp16r(cbp[k * 3 + 2]) * alpha;
+        const float dd = d0 * d0 + d1 * d1 + d2 * d2;
+        if (dd < bd) {
+            bd = dd;
+            bk = k;
+        }
+    }
+    const float c0 = fp16r(cbp[bk * 3]) * alpha, c1 = fp16r(cbp[bk * 3 + 1]) * alpha,
+                c2 = fp16r(cbp[bk * 3 + 2]) * alpha;
+    const float te = wsum(pv4.x * pv4.x + pv4.y * pv4.y + pv4.z * pv4.z);
+    const float ve = wsum(c0 * c0 + c1 * c1 + c2 * c2);
+    const float cv0 = fp16r(cents[4 * lane + 3]) * alpha, cv1 = fp16r(cents[D + 4 * lane + 3]) * alpha;
+    const int d3 = fabsf(pv4.w - cv0) < fabsf(pv4.w - cv1) ? 0 : 1;
+    const float pres = pv4.w - (d3 ? cv1 : cv0);
+    const float gmax = wmax(fabsf(pres));
+    const float rsc = fmaxf(gmax, 1e-4f);
+    const int dump = (int)fminf(15.0f, fmaxf(0.0f, roundf(pres / rsc * 7.0f + 8.0f)));
+    const float rn = fp16r(sqrtf(te / (ve + 1e-8f)));
+    const float nrm = norms[r];
+    // decode (ref .cu:2962-3024): the decoder reads the unrounded table values
+    float vr[4];
+    vr[0] = cbp[bk * 3] * alpha * nrm * rn;
+    vr[1] = cbp[bk * 3 + 1] * alpha * nrm * rn;
+    vr[2] = cbp[bk * 3 + 2] * alpha * nrm * rn;
+    vr[3] = cents[d3 * D + 4 * lane + 3] * alpha * nrm + (((float)dump - 8.0f) / 7.0f) * gmax * nrm;
+    const float* R = rp + lane * 16;
+    float q[4];
+    for (int c = 0; c < 4; c++)
+        q[c] = vr[0] * R[c * 4] + vr[1] * R[c * 4 + 1] + vr[2] * R[c * 4 + 2] + vr[3] * R[c * 4 + 3];
+    fwht_row(q, lane);
+    float4 o;
+    o.x = q[0] / (16.0f * d[4 * lane]);
+    o.y = q[1] / (16.0f * d[4 * lane + 1]);
+    o.z = q[2] / (16.0f * d[4 * lane + 2]);
+    o.w = q[3] / (16.0f * d[4 * lane + 3]);
+    *reinterpret_cast<float4*>(rec + r * D + 4 * lane) = o;
+}
+
+// sums of (x - rec)^2 plain, weighted by dim_mag and by dim_var, and max |x - rec|
+__global__ __launch_bounds__(256) void mse_kernel(const float* __restrict__ x,
+                                                  const float* __restrict__ rec,
+                                                  const float* __restrict__ wmag,
+                                                  const float* __restrict__ wvar, long n,
+                                                  double* __restrict__ out) {
+    __shared__ double s[3][256];
+    __shared__ float smx[256];
+    double a = 0, b = 0, c = 0;
+    float m = 0.0f;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+        const float df = x[i] - rec[i];
+        const double sq = (double)df * df;
+        a += sq;
+        b += wmag[i & 255] * sq;
+        c += wvar[i & 255] * sq;
+        m = fmaxf(m, fabsf(df));
+    }
+    s[0][threadIdx.x] = a;
+    s[1][threadIdx.x] = b;
+    s[2][threadIdx.x] = c;
+    smx[threadIdx.x] = m;
+    __syncthreads();
+    for (int o = 128; o >= 1; o >>= 1) {
+        if (threadIdx.x < o) {
+            for (int k = 0; k < 3; k++) s[k][threadIdx.x] += s[k][threadIdx.x + o];
+            smx[threadIdx.x] = fmaxf(smx[threadIdx.x], smx[threadIdx.x + o]);
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        for (int k = 0; k < 3; k++) atomicAdd(&out[k], s[k][0]);
+        atomicMax(reinterpret_cast<unsigned long long*>(&out[3]),
+                  (unsigned long long)__double_as_longlong((double)smx[0]));
+    }
+}
+
+__global__ void round_fp16_kernel(float* __restrict__ p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = fp16r(p[i]);
+}
+
+// ============================================================== SmartVQ
+// Attention-aware VQ training (ref .cu:2089-2625, 4434-4596; the reference's
+// train_smartvq.py port): per seed, Adam on the 64 x 256 x 3 codebook and a
+// rank-8 output transform W = I + A B, with a straight-through VQ (hard
+// nearest codeword forward, softmax(-dist / temp) weights backward).  Rows are
+// head-major V projections (row = kv_head * T + t).
+
+// per (row, patch): nearest codeword (first minimum), rec dims 0..2 = that
+// codeword, soft weights w[k] = softmax(-|v - c_k|^2 / temp), dict term
+// |c_best - v|^2.  One thread per (row, patch); the patch's codebook in LDS.
+__global__ __launch_bounds__(256) void vq_ste_kernel(const float* __restrict__ rot,
+                                                     const float* __restrict__ cb,
+                                                     float* __restrict__ rec,
+                                                     float* __restrict__ wbuf,
+                                                     int* __restrict__ idx,
+                                                     float* __restrict__ dict, int rows,
+                                                     float temp, int need_w) {
+    __shared__ float s_cb[768];
+    const int p = blockIdx.y;
+    for (int i = threadIdx.x; i < 768; i += 256) s_cb[i] = cb[p * 768 + i];
+    __syncthreads();
+    const long n = (long)blockIdx.x * 256 + threadIdx.x;
+    if (n >= rows) return;
+    const float* v = rot + n * D + p * 4;
+    const float v0 = v[0], v1 = v[1], v2 = v[2];
+    float bd;
+    const int bk = nearest(s_cb, v0, v1, v2, &bd);
+    idx[n * NP + p] = bk;
+    float dd = 0.0f;
+    for (int c = 0; c < 3; c++) {
+        const float df = s_cb[bk * 3 + c] - v[c];
+        dd += df * df;
+        rec[n * D + p * 4 + c] = s_cb[bk * 3 + c];
+    }
+    dict[n * NP + p] = dd;
+    if (need_w) {
+        // max of -dist / temp is -bd / temp (bd is the minimum distance)
+        const float zmax = -bd / temp;
+        float* w = wbuf + (n * NP + p) * 256;
+        float z = 0.0f;
+        for (int k = 0; k < 256; k++) {
+            const float d0 = v0 - s_cb[k * 3], d1 = v1 - s_cb[k * 3 + 1], d2 = v2 - s_cb[k * 3 + 2];
+            const float e = expf(-(d0 * d0 + d1 * d1 + d2 * d2) / temp - zmax);
+            w[k] = e;
+            z += e;
+        }
+        const float zi = 1.0f / z;
+        for (int k = 0; k < 256; k++) w[k] *= zi;
+    }
+}
+
+// dim 3 of rec: round half to even of rot * 16, / 16
+__global__ void dim3_kernel(const float* __restrict__ rot, float* __restrict__ rec, int rows) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)rows * NP) return;
+    rec[i * 4 + 3] = rintf(rot[i * 4 + 3] * 16.0f) / 16.0f;
+}
+
+// va = rec A (N x 8); dlt = rec + va B - v.  One wavefront per row.
+__global__ __launch_bounds__(256) void wtrm_fwd_kernel(const float* __restrict__ rec,
+                                                       const float* __restrict__ wa,
+                                                       const float* __restrict__ wb,
+                                                       const float* __restrict__ v,
+                                                       float* __restrict__ dlt, int rows) {
+    const int lane = threadIdx.x & 63;
+    const long n = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= rows) return;
+    const float4 x = *reinterpret_cast<const float4*>(rec + n * D + 4 * lane);
+    const float xs[4] = {x.x, x.y, x.z, x.w};
+    float va[8];
+    for (int r = 0; r < 8; r++) {
+        float s = 0.0f;
+        for (int j = 0; j < 4; j++) s += xs[j] * wa[(4 * lane + j) * 8 + r];
+        va[r] = wsum(s);
+    }
+    const float4 vv = *reinterpret_cast<const float4*>(v + n * D + 4 * lane);
+    const float vs[4] = {vv.x, vv.y, vv.z, vv.w};
+    float o[4];
+    for (int j = 0; j < 4; j++) {
+        float s = xs[j];
+        for (int r = 0; r < 8; r++) s += va[r] * wb[r * D + 4 * lane + j];
+        o[j] = s - vs[j];
+    }
+    *reinterpret_cast<float4*>(dlt + n * D + 4 * lane) = make_float4(o[0], o[1], o[2], o[3]);
+}
+
+// grec = g + (g B^T) A^T per row (g = gradient w.r.t. dlt).  One wavefront per row.
+__global__ __launch_bounds__(256) void wtrm_bwd_kernel(const float* __restrict__ g,
+                                                       const float* __restrict__ wa,
+                                                       const float* __restrict__ wb,
+                                                       float* __restrict__ grec, int rows) {
+    const int lane = threadIdx.x & 63;
+    const long n = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= rows) return;
+    const float4 x = *reinterpret_cast<const float4*>(g + n * D + 4 * lane);
+    const float xs[4] = {x.x, x.y, x.z, x.w};
+    float gb[8];
+    for (int r = 0; r < 8; r++) {
+        float s = 0.0f;
+        for (int j = 0; j < 4; j++) s += xs[j] * wb[r * D + 4 * lane + j];
+        gb[r] = wsum(s);
+    }
+    float o[4];
+    for (int j = 0; j < 4; j++) {
+        float s = xs[j];
+        for (int r = 0; r < 8; r++) s += gb[r] * wa[(4 * lane + j) * 8 + r];
+        o[j] = s;
+    }
+    *reinterpret_cast<float4*>(grec + n * D + 4 * lane) = make_float4(o[0], o[1], o[2], o[3]);
+}
+
+// C[b] (M x N) = alpha * op(A[b]) B[b] (+ C[b] when acc); row-major B (K x N,
+// ldb) and C (ldc); op(A) = A (M x K, lda) or A^T (A stored K x M, lda).
+// 64 x 64 tiles, 16-deep K slabs in LDS, 4 x 4 outputs per thread.
+__global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A,
+                                                   const float* __restrict__ B,
+                                                   float* __restrict__ C, int M, int N, int K,
+                                                   long lda, long ldb, long ldc, long sa, long sb,
+                                                   long sc, int trans_a, float alpha, int acc) {
+    __shared__ float sA[16][65];
+    __shared__ float sB[16][65];
+    const int b = blockIdx.z;
+    A += b * sa;
+    B += b * sb;
+    C += b * sc;
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    float c[4][4] = {};
+    for (int k0 = 0; k0 < K; k0 += 16) {
+        for (int i = threadIdx.x; i < 16 * 64; i += 256) {
+            const int kk = i >> 6, mm = i & 63;  // A slab: [k][m]
+            const int gm = m0 + mm, gk = k0 + kk;
+            float av = 0.0f;
+            if (gm < M && gk < K) av = trans_a ? A[(long)gk * lda + gm] : A[(long)gm * lda + gk];
+            sA[kk][mm] = av;
+            const int gn = n0 + mm;
+            sB[kk][mm] = (gn < N && gk < K) ? B[(long)gk * ldb + gn] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 16; kk++) {
+            float a4[4], b4[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                a4[i] = sA[kk][ty * 4 + i];
+                b4[i] = sB[kk][tx * 4 + i];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) c[i][j] = fmaf(a4[i], b4[j], c[i][j]);
+        }
+        __syncthreads();
+    }
+    for (int i = 0; i < 4; i++)
+        for (int j = 0; j < 4; j++) {
+            const int gm = m0 + ty * 4 + i, gn = n0 + tx * 4 + j;
+            if (gm < M && gn < N) {
+                float* cp = C + (long)gm * ldc + gn;
+                *cp = alpha * c[i][j] + (acc ? *cp : 0.0f);
+            }
+        }
+}
+
+// sum of squares (or of (a - b)^2, and the gradient 2 (a - b) / n) into a double
+__global__ __launch_bounds__(256) void sumsq_kernel(const float* __restrict__ a,
+                                                    const float* __restrict__ b,
+                                                    float* __restrict__ grad, long n, float gscale,
+                                                    double* __restrict__ out, int square) {
+    __shared__ double s[256];
+    double acc = 0.0;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+        const float df = b ? a[i] - b[i] : a[i];
+        acc += square ? (double)df * df : (double)df;
+        if (grad) grad[i] = gscale * df;
+    }
+    s[threadIdx.x] = acc;
+    __syncthreads();
+    for (int o = 128; o >= 1; o >>= 1) {
+        if (threadIdx.x < o) s[threadIdx.x] += s[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) atomicAdd(out, s[0]);
+}
+
+// gq[n][p][c] = sum_{d < 3} grec[n][4p + d] rp[16p + 4d + c], c < 3 (ref .cu:2300-2314)
+__global__ void rotbwd_kernel(const float* __restrict__ grec, const float* __restrict__ rp,
+                              float* __restrict__ gq, int rows) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)rows * NP) return;
+    const int p = (int)(i & 63);
+    const float* g = grec + i * 4;
+    for (int c = 0; c < 3; c++)
+        gq[i * 3 + c] = g[0] * rp[p * 16 + c] + g[1] * rp[p * 16 + 4 + c] + g[2] * rp[p * 16 + 8 + c];
+}
+
+// swg[n][p] = sum_k w[n][p][k] (gq . c_k).  One wavefront per (row, patch).
+__global__ __launch_bounds__(256) void swg_kernel(const float* __restrict__ gq,
+                                                  const float* __restrict__ cb,
+                                                  const float* __restrict__ wbuf,
+                                                  float* __restrict__ swg, int rows) {
+    const int lane = threadIdx.x & 63;
+    const long np = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (np >= (long)rows * NP) return;
+    const int p = (int)(np & 63);
+    const float g0 = gq[np * 3], g1 = gq[np * 3 + 1], g2 = gq[np * 3 + 2];
+    const float* w = wbuf + np * 256;
+    float s = 0.0f;
+    for (int k = lane; k < 256; k += 64) {
+        const float* c = cb + p * 768 + k * 3;
+        s += w[k] * (g0 * c[0] + g1 * c[1] + g2 * c[2]);
+    }
+    s = wsum(s);
+    if (lane == 0) swg[np] = s;
+}
+
+// Codebook gradient (ref .cu:2339-2371), summed over rows without atomics:
+// block = patch, thread = codeword k; for every row n
+//   gC[k] += w_k gq + (-w_k (gq . c_k - swg) / temp) * 2 (c_k - v)
+// plus, at the row's hard codeword, the dict term 2 / (N 64 3) (c_bk - v).
+__global__ __launch_bounds__(256) void cgrad_kernel(const float* __restrict__ wbuf,
+                                                    const float* __restrict__ swg,
+                                                    const float* __restrict__ gq,
+                                                    const float* __restrict__ rot,
+                                                    const float* __restrict__ cb,
+                                                    const int* __restrict__ idx,
+                                                    float* __restrict__ gcb, int rows, float temp) {
+    const int p = blockIdx.x, k = threadIdx.x;
+    const float c0 = cb[p * 768 + k * 3], c1 = cb[p * 768 + k * 3 + 1], c2 = cb[p * 768 + k * 3 + 2];
+    const float dn = 2.0f / (float)((long)rows * NP * 3);
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f;
+    for (int n = 0; n < rows; n++) {
+        const long np = (long)n * NP + p;
+        const float w = wbuf[np * 256 + k];
+        const float g0 = gq[np * 3], g1 = gq[np * 3 + 1], g2 = gq[np * 3 + 2];
+        const float* v = rot + (long)n * D + p * 4;
+        const float gd = -(w * ((g0 * c0 + g1 * c1 + g2 * c2) - swg[np])) / temp;
+        a0 += w * g0 + gd * 2.0f * (c0 - v[0]);
+        a1 += w * g1 + gd * 2.0f * (c1 - v[1]);
+        a2 += w * g2 + gd * 2.0f * (c2 - v[2]);
+        if (idx[np] == k) {
+            a0 += dn * (c0 - v[0]);
+            a1 += dn * (c1 - v[1]);
+            a2 += dn * (c2 - v[2]);
+        }
+    }
+    gcb[p * 768 + k * 3] = a0;
+    gcb[p * 768 + k * 3 + 1] = a1;
+    gcb[p * 768 + k * 3 + 2] = a2;
+}
+
+// gA = gW B^T (256 x 8), gB = A^T gW (8 x 256)
+__global__ void gwab_kernel(const float* __restrict__ gw, const float* __restrict__ wa,
+                            const float* __restrict__ wb, float* __restrict__ gwa,
+                            float* __restrict__ gwb) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < 2048) {
+        const int j = i >> 3, r = i & 7;
+        float s = 0.0f;
+        for (int d = 0; d < D; d++) s += gw[j * D + d] * wb[r * D + d];
+        gwa[i] = s;
+    } else if (i < 4096) {
+        const int r = (i - 2048) >> 8, d = (i - 2048) & 255;
+        float s = 0.0f;
+        for (int j = 0; j < D; j++) s += wa[j * 8 + r] * gw[j * D + d];
+        gwb[i - 2048] = s;
+    }
+}
+
+// Adam with bias correction (ref .cu:2373-2385)
+__global__ void adam_kernel(float* __restrict__ p, const float* __restrict__ g,
+                            float* __restrict__ m, float* __restrict__ v, float lr, float bc1,
+                            float bc2, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float gi = g[i];
+    m[i] = 0.9f * m[i] + 0.1f * gi;
+    v[i] = 0.999f * v[i] + 0.001f * gi * gi;
+    p[i] -= lr * (m[i] / bc1) / (sqrtf(v[i] / bc2) + 1e-8f);
+}
+
+// p = base + N(0,1) * scale, one Box-Muller draw from a per-entry xorshift
+// stream (ref .cu:2387-2401)
+__global__ void noise_kernel(const float* __restrict__ base, float* __restrict__ p, unsigned seed,
+                             float scale, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    unsigned s = seed ^ ((unsigned)i * 747796405u + 2891336453u);
+    s ^= s << 13;
+    s ^= s >> 17;
+    s ^= s << 5;
+    const float u1 = (float)(s & 0xFFFFFFu) / 16777216.0f + 1e-7f;
+    s ^= s << 13;
+    s ^= s >> 17;
+    s ^= s << 5;
+    const float u2 = (float)(s & 0xFFFFFFu) / 16777216.0f;
+    p[i] = base[i] + sqrtf(-2.0f * logf(u1)) * cosf(6.2831853f * u2) * scale;
+}
+
+// W = I + A B (256 x 256)
+__global__ void wtrm_compose_kernel(const float* __restrict__ wa, const float* __restrict__ wb,
+                                    float* __restrict__ out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= D * D) return;
+    const int j = i >> 8, d = i & 255;
+    float s = j == d ? 1.0f : 0.0f;
+    for (int r = 0; r < 8; r++) s += wa[j * 8 + r] * wb[r * D + d];
+    out[i] = s;
+}
+
+}  // namespace cal
+}  // namespace khq
+
+// ============================================================ host side
+namespace {
+
+using namespace khq::cal;
+
+struct Buf {  // device buffer that frees itself
+    void* p = nullptr;
+    hipError_t alloc(size_t bytes) { return hipMalloc(&p, bytes); }
+    template <typename T>
+    T* as() const { return static_cast<T*>(p); }
+    ~Buf() {
+        if (p) (void)hipFree(p);
+    }
+};
+
+#define CAL_TRY(x)                            \
+    do {                                      \
+        hipError_t e_ = (x);                  \
+        if (e_ != hipSuccess) return (int)e_; \
+    } while (0)
+
+int n_row_blocks(int rows) { return std::max(1, std::min(1024, (rows + 63) / 64)); }
+
+// per-dim mean |x| and variance, each normalised to sum 1 (ref .cu:2683-2720)
+int dim_weights(const float* x, int rows, float* wmag, float* wvar, hipStream_t st) {
+    Buf acc, mean;
+    CAL_TRY(acc.alloc(3 * D * sizeof(double)));
+    CAL_TRY(mean.alloc(D * sizeof(double)));
+    CAL_TRY(hipMemsetAsync(acc.p, 0, 3 * D * sizeof(double), st));
+    const int nb = n_row_blocks(rows);
+    hipLaunchKernelGGL(colsum_kernel, dim3(nb), dim3(D), 0, st, x, rows, nullptr, acc.as<double>());
+    hipLaunchKernelGGL(colmean_kernel, dim3(1), dim3(D), 0, st, acc.as<double>(), mean.as<double>(),
+                       rows);
+    hipLaunchKernelGGL(colsum_kernel, dim3(nb), dim3(D), 0, st, x, rows, mean.as<double>(),
+                       acc.as<double>());
+    std::vector<double> h(3 * D);
+    CAL_TRY(hipMemcpyAsync(h.data(), acc.p, 3 * D * sizeof(double), hipMemcpyDeviceToHost, st));
+    CAL_TRY(hipStreamSynchronize(st));
+    std::vector<float> m(D), v(D);
+    float sm = 0.0f, sv = 0.0f;
+    for (int i = 0; i < D; i++) {
+        m[i] = (float)(h[D + i] / rows);
+        v[i] = (float)(h[2 * D + i] / rows);
+        sm += m[i];
+        sv += v[i];
+    }
+    sm += 1e-8f;
+    sv += 1e-8f;
+    for (int i = 0; i < D; i++) {
+        m[i] /= sm;
+        v[i] /= sv;
+    }
+    CAL_TRY(hipMemcpyAsync(wmag, m.data(), D * 4, hipMemcpyHostToDevice, st));
+    CAL_TRY(hipMemcpyAsync(wvar, v.data(), D * 4, hipMemcpyHostToDevice, st));
+    return (int)hipStreamSynchronize(st);
+}
+
+// SmartK (is_k) / SmartV tournament (ref .cu:4720-4806): 4 phases of an 8 x 8
+// grid over (alpha, ts multiplier); each phase keeps the best by plain,
+// magnitude-weighted and variance-weighted MSE; the winner is the one of the
+// three with the smallest max error.
+int tournament(bool is_k, const float* x32, const float* x16, const float* dv, const float* rp,
+               const float* cents_in, const float* vq_in, float* cents_out, float* g_out,
+               float ts0, int rows, hipStream_t st) {
+    Buf wmag, wvar, proj, rec, norms, cents, acc;
+    CAL_TRY(wmag.alloc(D * 4));
+    CAL_TRY(wvar.alloc(D * 4));
+    CAL_TRY(proj.alloc((size_t)rows * D * 4));
+    CAL_TRY(rec.alloc((size_t)rows * D * 4));
+    CAL_TRY(norms.alloc((size_t)rows * 4));
+    CAL_TRY(cents.alloc(1024 * 4));
+    CAL_TRY(acc.alloc(4 * sizeof(double)));
+    int rc = dim_weights(x32, rows, wmag.as<float>(), wvar.as<float>(), st);
+    if (rc) return rc;
+    // the projection of the fp16 rows does not depend on the grid point
+    hipLaunchKernelGGL(fwht_base_kernel, dim3(blocks(rows, 4)), dim3(256), 0, st, x16, dv,
+                       norms.as<float>(), proj.as<float>(), rows);
+    hipLaunchKernelGGL(round_fp16_kernel, dim3(blocks(rows, 256)), dim3(256), 0, st,
+                       norms.as<float>(), rows);
+    std::vector<float> base(1024), cur(1024);
+    if (is_k) {
+        CAL_TRY(hipMemcpyAsync(base.data(), cents_in, 1024 * 4, hipMemcpyDeviceToHost, st));
+        CAL_TRY(hipStreamSynchronize(st));
+        for (float& b : base) b /= ts0;
+    }
+    struct Best {
+        float a, ts, e, me;
+    };
+    Best bf{1.0f, ts0, 1e30f, 1e30f}, bm = bf, bv = bf;
+    const float deltas[8] = {-0.03f, -0.02f, -0.01f, 0.0f, 0.01f, 0.02f, 0.03f, 0.04f};
+    for (int phase = 0; phase < 4; phase++) {
+        const Best& c = phase == 1 ? bf : (phase == 2 ? bm : bv);
+        const float ac = phase ? c.a : 1.0f, mc = phase ? c.ts / ts0 : 1.0f;
+        for (int ia = 0; ia < 8; ia++)
+            for (int it = 0; it < 8; it++) {
+                const float a = phase == 0 ? 0.80f + 0.05f * ia : ac + deltas[ia];
+                const float m = phase == 0 ? 0.80f + 0.05f * it : mc + deltas[it];
+                const float ts = ts0 * m;
+                if (is_k) {
+                    for (int i = 0; i < 1024; i++)
+                        cur[i] = __half2float(__float2half(base[i] * ts));
+                    CAL_TRY(hipMemcpyAsync(cents.p, cur.data(), 1024 * 4, hipMemcpyHostToDevice, st));
+                    hipLaunchKernelGGL(roundtrip_k_kernel, dim3(blocks(rows, 4)), dim3(256), 0, st,
+                                       proj.as<float>(), norms.as<float>(), cents.as<float>(), rp,
+                                       dv, a, rec.as<float>(), rows);
+                } else {
+                    // V: the threshold scale only sets the unused V code plan;
+                    // alpha scales the codebook and dim-3 centroids
+                    hipLaunchKernelGGL(roundtrip_v_kernel, dim3(blocks(rows, 4)), dim3(256), 0, st,
+                                       proj.as<float>(), norms.as<float>(), cents_in, vq_in, rp,
+                                       dv, a, rec.as<float>(), rows);
+                }
+                CAL_TRY(hipMemsetAsync(acc.p, 0, 4 * sizeof(double), st));
+                hipLaunchKernelGGL(mse_kernel, dim3(256), dim3(256), 0, st, x32, rec.as<float>(),
+                                   wmag.as<float>(), wvar.as<float>(), (long)rows * D,
+                                   acc.as<double>());
+                double h[4];
+                CAL_TRY(hipMemcpyAsync(h, acc.p, sizeof(h), hipMemcpyDeviceToHost, st));
+                CAL_TRY(hipStreamSynchronize(st));
+                const float e_flat = (float)(h[0] / ((double)rows * D));
+                const float e_mag = (float)(h[1] / rows), e_var = (float)(h[2] / rows);
+                const float me = (float)h[3];
+                if (e_flat < bf.e) bf = Best{a, ts, e_flat, me};
+                if (e_mag < bm.e) bm = Best{a, ts, e_mag, me};
+                if (e_var < bv.e) bv = Best{a, ts, e_var, me};
+            }
+    }
+    Best w = bf;
+    if (bm.me < w.me) w = bm;
+    if (bv.me < w.me) w = bv;
+    if (is_k) {
+        for (int i = 0; i < 1024; i++) cur[i] = __half2float(__float2half(base[i] * w.ts));
+        CAL_TRY(hipMemcpyAsync(cents_out, cur.data(), 1024 * 4, hipMemcpyHostToDevice, st));
+    }
+    const float g[2] = {w.ts, w.a};
+    CAL_TRY(hipMemcpyAsync(g_out, g, 8, hipMemcpyHostToDevice, st));
+    return (int)hipStreamSynchronize(st);
+}
+
+
+// ---------------------------------------------------------- SmartVQ host
+struct Seed {
+    Buf cb, wa, wb, mcb, vcb, mwa, vwa, mwb, vwb, bcb, bwa, bwb;
+    float best = 0.0f, lr_mult = 1.0f;
+    int stagnant = 0, step = 0;
+    unsigned seed = 0;
+    int init(const float* init_cb, unsigned sd, hipStream_t st) {
+        for (Buf* b : {&cb, &mcb, &vcb, &bcb}) CAL_TRY(b->alloc(CB * 4));
+        for (Buf* b : {&wa, &wb, &mwa, &vwa, &mwb, &vwb, &bwa, &bwb}) CAL_TRY(b->alloc(2048 * 4));
+        for (Buf* b : {&mcb, &vcb}) CAL_TRY(hipMemsetAsync(b->p, 0, CB * 4, st));
+        for (Buf* b : {&wa, &wb, &mwa, &vwa, &mwb, &vwb}) CAL_TRY(hipMemsetAsync(b->p, 0, 2048 * 4, st));
+        // A ~ N(0, 1) / 16, B = 0 (ref .cu:4503-4505)
+        hipLaunchKernelGGL(noise_kernel, dim3(8), dim3(256), 0, st, wa.as<float>(), wa.as<float>(),
+                           sd * 2654435761u + 1u, 1.0f / 16.0f, 2048);
+        CAL_TRY(hipMemcpyAsync(cb.p, init_cb, CB * 4, hipMemcpyDeviceToDevice, st));
+        return keep_best(st);
+    }
+    int keep_best(hipStream_t st) {
+        CAL_TRY(hipMemcpyAsync(bcb.p, cb.p, CB * 4, hipMemcpyDeviceToDevice, st));
+        CAL_TRY(hipMemcpyAsync(bwa.p, wa.p, 2048 * 4, hipMemcpyDeviceToDevice, st));
+        CAL_TRY(hipMemcpyAsync(bwb.p, wb.p, 2048 * 4, hipMemcpyDeviceToDevice, st));
+        return 0;
+    }
+    int restore_best(hipStream_t st) {
+        CAL_TRY(hipMemcpyAsync(cb.p, bcb.p, CB * 4, hipMemcpyDeviceToDevice, st));
+        CAL_TRY(hipMemcpyAsync(wa.p, bwa.p, 2048 * 4, hipMemcpyDeviceToDevice, st));
+        CAL_TRY(hipMemcpyAsync(wb.p, bwb.p, 2048 * 4, hipMemcpyDeviceToDevice, st));
+        return 0;
+    }
+};
+
+struct Svq {
+    const float* v;     // [N][256] head-major FWHT-domain V rows
+    const float* attn;  // [H_q][T][T] or NULL (reconstruction loss)
+    const float* rp;    // [64][16]
+    int N, T, H_q, H_kv;
+    hipStream_t st;
+    Buf rot, rec, recf, dlt, wbuf, idx, dict, y, gdl, grec, gw, gq, swg, gcb, gwa, gwb, loss;
+    int init() {
+        const size_t nd = (size_t)N * D * 4;
+        for (Buf* b : {&rot, &rec, &recf, &dlt, &grec, &gdl}) CAL_TRY(b->alloc(nd));
+        CAL_TRY(wbuf.alloc((size_t)N * NP * 256 * 4));
+        CAL_TRY(idx.alloc((size_t)N * NP * 4));
+        CAL_TRY(dict.alloc((size_t)N * NP * 4));
+        CAL_TRY(gq.alloc((size_t)N * NP * 3 * 4));
+        CAL_TRY(swg.alloc((size_t)N * NP * 4));
+        CAL_TRY(gw.alloc(D * D * 4));
+        CAL_TRY(gcb.alloc(CB * 4));
+        CAL_TRY(gwa.alloc(2048 * 4));
+        CAL_TRY(gwb.alloc(2048 * 4));
+        CAL_TRY(loss.alloc(2 * sizeof(double)));
+        if (attn) CAL_TRY(y.alloc((size_t)H_q * T * D * 4));
+        return 0;
+    }
+    void gemm(const float* A, const float* B, float* C, int M, int Nn, int K, long lda, long ldb,
+              long ldc, long sa, long sb, long sc, int batch, int ta, float alpha) {
+        hipLaunchKernelGGL(gemm_kernel, dim3((Nn + 63) / 64, (M + 63) / 64, batch), dim3(256), 0,
+                           st, A, B, C, M, Nn, K, lda, ldb, ldc, sa, sb, sc, ta, alpha, 0);
+    }
+    // One pass at temperature temp (ref .cu:2436-2467 forward, :2470-2530
+    // with gradients): losses[0] = reconstruction (attention-weighted MSE of
+    // the transformed residual, or plain MSE), losses[1] = dict term.
+    int pass(Seed& s, float temp, bool grad, double* losses) {
+        const int n_rep = H_q / H_kv;
+        CAL_TRY(hipMemsetAsync(loss.p, 0, 2 * sizeof(double), st));
+        hipLaunchKernelGGL(rotate_kernel, dim3(blocks((long)N * NP, 256)), dim3(256), 0, st, v, rp,
+                           rot.as<float>(), N);
+        hipLaunchKernelGGL(vq_ste_kernel, dim3(blocks(N, 256), NP), dim3(256), 0, st,
+                           rot.as<float>(), s.cb.as<float>(), rec.as<float>(), wbuf.as<float>(),
+                           idx.as<int>(), dict.as<float>(), N, temp, grad ? 1 : 0);
+        hipLaunchKernelGGL(dim3_kernel, dim3(blocks((long)N * NP, 256)), dim3(256), 0, st,
+                           rot.as<float>(), rec.as<float>(), N);
+        hipLaunchKernelGGL(invrot_kernel, dim3(blocks((long)N * NP, 256)), dim3(256), 0, st,
+                           rec.as<float>(), rp, recf.as<float>(), N);
+        const long nd = (long)N * D;
+        double denom = (double)nd;
+        if (attn) {
+            hipLaunchKernelGGL(wtrm_fwd_kernel, dim3(blocks(N, 4)), dim3(256), 0, st,
+                               recf.as<float>(), s.wa.as<float>(), s.wb.as<float>(), v,
+                               dlt.as<float>(), N);
+            for (int kv = 0; kv < H_kv; kv++)  // y_h = A_h dlt_kv for the group's heads
+                gemm(attn + (long)kv * n_rep * T * T, dlt.as<float>() + (long)kv * T * D,
+                     y.as<float>() + (long)kv * n_rep * T * D, T, D, T, T, D, D, (long)T * T, 0,
+                     (long)T * D, n_rep, 0, 1.0f);
+            const long ny = (long)H_q * T * D;
+            denom = (double)ny;
+            hipLaunchKernelGGL(sumsq_kernel, dim3(256), dim3(256), 0, st, y.as<float>(), nullptr,
+                               nullptr, ny, 0.0f, loss.as<double>(), 1);
+            if (grad) {
+                const float g = 2.0f / (float)ny;
+                for (int kv = 0; kv < H_kv; kv++)  // gdlt_kv = g sum_h A_h^T y_h
+                    gemm(attn + (long)kv * n_rep * T * T, y.as<float>() + (long)kv * n_rep * T * D,
+                         gdl.as<float>() + (long)kv * T * D, T, D, n_rep * T, T, D, D, 0, 0, 0, 1,
+                         1, g);
+                hipLaunchKernelGGL(wtrm_bwd_kernel, dim3(blocks(N, 4)), dim3(256), 0, st,
+                                   gdl.as<float>(), s.wa.as<float>(), s.wb.as<float>(),
+                                   grec.as<float>(), N);
+                gemm(recf.as<float>(), gdl.as<float>(), gw.as<float>(), D, D, N, D, D, D, 0, 0, 0,
+                     1, 1, 1.0f);  // gW = recf^T gdlt
+                hipLaunchKernelGGL(gwab_kernel, dim3(16), dim3(256), 0, st, gw.as<float>(),
+                                   s.wa.as<float>(), s.wb.as<float>(), gwa.as<float>(),
+                                   gwb.as<float>());
+            }
+        } else {
+            hipLaunchKernelGGL(sumsq_kernel, dim3(256), dim3(256), 0, st, recf.as<float>(), v,
+                               grad ? grec.as<float>() : nullptr, nd, 2.0f / (float)nd,
+                               loss.as<double>(), 1);
+        }
+        hipLaunchKernelGGL(sumsq_kernel, dim3(64), dim3(256), 0, st, dict.as<float>(), nullptr,
+                           nullptr, (long)N * NP, 0.0f, loss.as<double>() + 1, 0);
+        if (grad) {
+            hipLaunchKernelGGL(rotbwd_kernel, dim3(blocks((long)N * NP, 256)), dim3(256), 0, st,
+                               grec.as<float>(), rp, gq.as<float>(), N);
+            hipLaunchKernelGGL(swg_kernel, dim3(blocks((long)N * NP, 4)), dim3(256), 0, st,
+                               gq.as<float>(), s.cb.as<float>(), wbuf.as<float>(),
+                               swg.as<float>(), N);
+            hipLaunchKernelGGL(cgrad_kernel, dim3(NP), dim3(256), 0, st, wbuf.as<float>(),
+                               swg.as<float>(), gq.as<float>(), rot.as<float>(), s.cb.as<float>(),
+                               idx.as<int>(), gcb.as<float>(), N, temp);
+        }
+        double h[2];
+        CAL_TRY(hipMemcpyAsync(h, loss.p, sizeof(h), hipMemcpyDeviceToHost, st));
+        CAL_TRY(hipStreamSynchronize(st));
+        losses[0] = h[0] / denom;
+        losses[1] = h[1] / ((double)N * NP * 3);
+        return 0;
+    }
+    // iters steps of one seed from step start (ref .cu:2470-2590): temperature
+    // 1.5 -> 0.1 geometric, linear lr decay to 10 %, Adam (transform at 5 %
+    // of the codebook rate), best-state tracking, patience 15 (halve the rate
+    // to 0.1, then a warm restart from the best state with decaying noise)
+    int run(Seed& s, int iters, int start, float lr) {
+        const int total = start + iters;
+        const int max_it = std::max(1, total - 1);
+        for (int i = start; i < total; i++) {
+            const float temp = 1.5f * expf((logf(0.1f) - logf(1.5f)) * (float)i / (float)max_it);
+            const float cur = lr * fmaxf(0.1f, 1.0f - (float)i / (float)total) * s.lr_mult;
+            double l[2];
+            int rc = pass(s, temp, true, l);
+            if (rc) return rc;
+            if (!attn) {  // no transform gradient without the attention loss
+                CAL_TRY(hipMemsetAsync(gwa.p, 0, 2048 * 4, st));
+                CAL_TRY(hipMemsetAsync(gwb.p, 0, 2048 * 4, st));
+            }
+            s.step++;
+            const float bc1 = 1.0f - powf(0.9f, (float)s.step), bc2 = 1.0f - powf(0.999f, (float)s.step);
+            hipLaunchKernelGGL(adam_kernel, dim3(blocks(CB, 256)), dim3(256), 0, st, s.cb.as<float>(),
+                               gcb.as<float>(), s.mcb.as<float>(), s.vcb.as<float>(), cur, bc1, bc2,
+                               CB);
+            hipLaunchKernelGGL(adam_kernel, dim3(8), dim3(256), 0, st, s.wa.as<float>(),
+                               gwa.as<float>(), s.mwa.as<float>(), s.vwa.as<float>(), cur * 0.05f,
+                               bc1, bc2, 2048);
+            hipLaunchKernelGGL(adam_kernel, dim3(8), dim3(256), 0, st, s.wb.as<float>(),
+                               gwb.as<float>(), s.mwb.as<float>(), s.vwb.as<float>(), cur * 0.05f,
+                               bc1, bc2, 2048);
+            // the loss of this step's forward pass (before the update), as the reference
+            const float loss = (float)(l[0] + l[1]);
+            if (loss < s.best - 1e-7f) {
+                s.best = loss;
+                rc = s.keep_best(st);
+                if (rc) return rc;
+                s.stagnant = 0;
+            } else {
+                s.stagnant++;
+            }
+            if (s.stagnant >= 15) {
+                if (s.lr_mult > 0.1f) {
+                    s.lr_mult *= 0.5f;
+                } else {
+                    s.lr_mult = 3.0f;
+                    const float ns = 1e-3f * expf(logf(0.01f) * (float)i / (float)max_it);
+                    hipLaunchKernelGGL(noise_kernel, dim3(blocks(CB, 256)), dim3(256), 0, st,
+                                       s.bcb.as<float>(), s.cb.as<float>(), s.seed ^ (unsigned)i, ns,
+                                       CB);
+                    CAL_TRY(hipMemcpyAsync(s.wa.p, s.bwa.p, 2048 * 4, hipMemcpyDeviceToDevice, st));
+                    CAL_TRY(hipMemcpyAsync(s.wb.p, s.bwb.p, 2048 * 4, hipMemcpyDeviceToDevice, st));
+                }
+                s.stagnant = 0;
+            }
+        }
+        return (int)hipStreamSynchronize(st);
+    }
+    // attention-MSE proxy of a state: the loss at temperature 0.05 without
+    // the dict term (ref .cu:4540-4545)
+    int proxy(Seed& s, float* out) {
+        double l[2];
+        int rc = pass(s, 0.05f, false, l);
+        *out = (float)l[0];
+        return rc;
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+int launch_cal_op(int op, const void* a_, const void* b_, const void* c_, const void* d_, void* e_,
+                  void* f_, void* g_, float f1, float f2, int i1, int i2, int i3, int i4,
+                  hipStream_t st) {
+    (void)f2;
+    (void)i3;
+    (void)i4;
+    const float* a = static_cast<const float*>(a_);
+    const float* b = static_cast<const float*>(b_);
+    const float* c = static_cast<const float*>(c_);
+    const float* d = static_cast<const float*>(d_);
+    float* e = static_cast<float*>(e_);
+    float* f = static_cast<float*>(f_);
+    float* g = static_cast<float*>(g_);
+    const int rows = i1;
+    if (rows <= 0) return -100;
+    switch (op) {
+        case 1:  // base = FWHT(x d / norm) / 16, norms out
+            if (!a || !b || !e || !f) return -100;
+            hipLaunchKernelGGL(fwht_base_kernel, dim3(blocks(rows, 4)), dim3(256), 0, st, a, b, e,
+                               f, rows);
+            return (int)hipGetLastError();
+        case 2: {  // K static: cents (f) and ts (g) from the projection a
+            if (!a || !f || !g) return -100;
+            Buf acc, mean;
+            CAL_TRY(acc.alloc(3 * D * sizeof(double)));
+            CAL_TRY(mean.alloc(D * sizeof(double)));
+            CAL_TRY(hipMemsetAsync(acc.p, 0, 3 * D * sizeof(double), st));
+            const int nb = n_row_blocks(rows);
+            hipLaunchKernelGGL(colsum_kernel, dim3(nb), dim3(D), 0, st, a, rows, nullptr,
+                               acc.as<double>());
+            hipLaunchKernelGGL(colmean_kernel, dim3(1), dim3(D), 0, st, acc.as<double>(),
+                               mean.as<double>(), rows);
+            hipLaunchKernelGGL(colsum_kernel, dim3(nb), dim3(D), 0, st, a, rows, mean.as<double>(),
+                               acc.as<double>());
+            hipLaunchKernelGGL(kstatic_kernel, dim3(1), dim3(D), 0, st, acc.as<double>(), rows, f, g);
+            return (int)hipStreamSynchronize(st);
+        }
+        case 3:  // rotate
+            if (!a || !b || !e) return -100;
+            hipLaunchKernelGGL(rotate_kernel, dim3(blocks((long)rows * NP, 256)), dim3(256), 0, st,
+                               a, b, e, rows);
+            return (int)hipGetLastError();
+        case 4: {  // PCA rotors (e) from the FWHT-domain rows a
+            if (!a || !e) return -100;
+            Buf mom;
+            CAL_TRY(mom.alloc(1024 * sizeof(double)));
+            CAL_TRY(hipMemsetAsync(mom.p, 0, 1024 * sizeof(double), st));
+            hipLaunchKernelGGL(patch_moment_kernel, dim3(4, n_row_blocks(rows)), dim3(256), 0, st,
+                               a, nullptr, rows, mom.as<double>());
+            hipLaunchKernelGGL(pca_kernel, dim3(1), dim3(64), 0, st, mom.as<double>(), e);
+            return (int)hipStreamSynchronize(st);
+        }
+        case 5: {  // 4-centroid k-means per dim -> e [4][256]
+            if (!a || !e) return -100;
+            Buf mn, mx, acc;
+            CAL_TRY(mn.alloc(D * 4));
+            CAL_TRY(mx.alloc(D * 4));
+            CAL_TRY(acc.alloc(8 * D * sizeof(double)));
+            std::vector<int> lo(D, 0x7FFFFFFF), hi(D, (int)0x80000000);
+            CAL_TRY(hipMemcpyAsync(mn.p, lo.data(), D * 4, hipMemcpyHostToDevice, st));
+            CAL_TRY(hipMemcpyAsync(mx.p, hi.data(), D * 4, hipMemcpyHostToDevice, st));
+            CAL_TRY(hipMemsetAsync(acc.p, 0, 8 * D * sizeof(double), st));
+            const int nb = n_row_blocks(rows);
+            hipLaunchKernelGGL(colrange_kernel, dim3(nb), dim3(D), 0, st, a, rows, mn.as<float>(),
+                               mx.as<float>());
+            hipLaunchKernelGGL(km4_init_kernel, dim3(1), dim3(D), 0, st, mn.as<float>(),
+                               mx.as<float>(), e);
+            for (int it = 0; it < 20; it++) {
+                hipLaunchKernelGGL(km4_assign_kernel, dim3(nb), dim3(D), 0, st, a, rows, e,
+                                   acc.as<double>());
+                hipLaunchKernelGGL(km4_update_kernel, dim3(1), dim3(D), 0, st, e, acc.as<double>());
+            }
+            return (int)hipStreamSynchronize(st);
+        }
+        case 6: {  // VQ codebooks (e [64][256][3]) by k-means, seed i2
+            if (!a || !e) return -100;
+            Buf sums;
+            CAL_TRY(sums.alloc((size_t)NP * 256 * 4 * sizeof(double)));
+            CAL_TRY(hipMemsetAsync(sums.p, 0, (size_t)NP * 256 * 4 * sizeof(double), st));
+            hipLaunchKernelGGL(vq_init_kernel, dim3(NP), dim3(256), 0, st, a, e, (unsigned)i2, rows);
+            const int gx = std::max(1, std::min(64, (rows + 255) / 256));
+            for (int it = 0; it < 30; it++) {
+                hipLaunchKernelGGL(vq_assign_kernel, dim3(gx, NP), dim3(256), 0, st, a, e, rows,
+                                   sums.as<double>());
+                hipLaunchKernelGGL(vq_update_kernel, dim3(NP), dim3(256), 0, st, e,
+                                   sums.as<double>());
+            }
+            return (int)hipStreamSynchronize(st);
+        }
+        case 7: {  // i2 Procrustes-Lloyd iterations on rotors e (in/out)
+            if (!a || !b || !e || i2 < 0) return -100;
+            Buf rot, tgt, mom;
+            CAL_TRY(rot.alloc((size_t)rows * D * 4));
+            CAL_TRY(tgt.alloc((size_t)rows * D * 4));
+            CAL_TRY(mom.alloc(1024 * sizeof(double)));
+            const int gx = std::max(1, std::min(64, (rows + 255) / 256));
+            for (int it = 0; it < i2; it++) {
+                hipLaunchKernelGGL(rotate_kernel, dim3(blocks((long)rows * NP, 256)), dim3(256), 0,
+                                   st, a, e, rot.as<float>(), rows);
+                hipLaunchKernelGGL(procrustes_target_kernel, dim3(gx, NP), dim3(256), 0, st,
+                                   rot.as<float>(), b, tgt.as<float>(), rows);
+                CAL_TRY(hipMemsetAsync(mom.p, 0, 1024 * sizeof(double), st));
+                hipLaunchKernelGGL(patch_moment_kernel, dim3(4, n_row_blocks(rows)), dim3(256), 0,
+                                   st, a, tgt.as<float>(), rows, mom.as<double>());
+                hipLaunchKernelGGL(polar_ns_kernel, dim3(1), dim3(64), 0, st, mom.as<double>(), e);
+            }
+            return (int)hipStreamSynchronize(st);
+        }
+        case 8:  // SmartK: a x32, b x16, c d, d rotor, e cents in, f cents out, g (ts, alpha)
+            if (!a || !b || !c || !d || !e || !f || !g || !(f1 > 0.0f)) return -100;
+            return tournament(true, a, b, c, d, e, nullptr, f, g, f1, rows, st);
+        case 9:  // SmartV: f is the VQ codebook (input)
+            if (!a || !b || !c || !d || !e || !f || !g || !(f1 > 0.0f)) return -100;
+            return tournament(false, a, b, c, d, e, f, nullptr, g, f1, rows, st);
+        case 10:  // head-major reorder: a -> e, i1 tokens, i2 heads
+            if (!a || !e || i2 <= 0) return -100;
+            hipLaunchKernelGGL(headmajor_kernel, dim3(blocks((long)rows * i2 * D, 256)), dim3(256),
+                               0, st, a, e, rows, i2);
+            return (int)hipGetLastError();
+        default:
+            return -1;
+    }
+}
+
+int launch_cal_svq_train(const void* v, const void* attn, const void* init_cb, const void* rp,
+                         void* out_cb, void* out_wtrm, int N, int T, int H_q, int H_kv,
+                         int iterations, int n_seeds, float lr, hipStream_t st) {
+    if (!v || !init_cb || !rp || !out_cb || N <= 0 || iterations < 0) return -100;
+    if (attn && (T <= 0 || H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || (long)H_kv * T != N))
+        return -100;
+    n_seeds = std::max(1, std::min(3, n_seeds));
+    Svq t{static_cast<const float*>(v), static_cast<const float*>(attn),
+          static_cast<const float*>(rp), N, T, H_q, H_kv, st};
+    int rc = t.init();
+    if (rc) return rc;
+    const unsigned seeds[3] = {42u, 137u, 271u};
+    Seed sd[3];
+    for (int i = 0; i < n_seeds; i++) {
+        rc = sd[i].init(static_cast<const float*>(init_cb), seeds[i], st);
+        if (rc) return rc;
+        sd[i].seed = seeds[i];
+        double l[2];
+        rc = t.pass(sd[i], 1.5f, false, l);
+        if (rc) return rc;
+        sd[i].best = (float)(l[0] + l[1]);
+    }
+    // round 1: up to 30 steps per seed; states restored to their best
+    const int r1 = std::min(iterations, 30), r2 = iterations - r1;
+    float prox[3];
+    for (int i = 0; i < n_seeds; i++) {
+        if ((rc = t.run(sd[i], r1, 0, lr))) return rc;
+        if ((rc = sd[i].restore_best(st))) return rc;
+        if ((rc = t.proxy(sd[i], &prox[i]))) return rc;
+    }
+    int order[3] = {0, 1, 2};
+    for (int i = 0; i < n_seeds; i++)
+        for (int j = i + 1; j < n_seeds; j++)
+            if (prox[order[j]] < prox[order[i]]) std::swap(order[i], order[j]);
+    // round 2: the remaining steps for every seed, best proxy first
+    if (r2 > 0)
+        for (int k = 0; k < n_seeds; k++) {
+            Seed& s = sd[order[k]];
+            if ((rc = t.run(s, r2, r1, lr))) return rc;
+            if ((rc = t.proxy(s, &prox[order[k]]))) return rc;
+        }
+    int win = order[0];
+    for (int k = 0; k < n_seeds; k++)
+        if (prox[order[k]] < prox[win]) win = order[k];
+    CAL_TRY(hipMemcpyAsync(out_cb, sd[win].bcb.p, CB * 4, hipMemcpyDeviceToDevice, st));
+    if (out_wtrm)
+        hipLaunchKernelGGL(wtrm_compose_kernel, dim3(256), dim3(256), 0, st, sd[win].bwa.as<float>(),
+                           sd[win].bwb.as<float>(), static_cast<float*>(out_wtrm));
+    return (int)hipStreamSynchronize(st);
+}
+
+}  // extern "C"

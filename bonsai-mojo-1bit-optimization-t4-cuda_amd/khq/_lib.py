@@ -59,6 +59,9 @@ SIGNATURES = {
     "khq_dump_attn": [P, I, P, P, I, I, I, I, F, P],
     "khq_dump_flush": [P],
     "khq_layer_set_dump": [P, P, I],
+    # calibration
+    "launch_cal_op": [I] + [P] * 7 + [F, F, I, I, I, I, P],
+    "launch_cal_svq_train": [P] * 6 + [I, I, I, I, I, I, F, P],
     "khq_layer_attention_step": [P] * 6 + [F, I, P, F, P],
 }
 # return types other than int

@@ -12,7 +12,7 @@ CSRC = os.path.join(ROOT, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 LIB_NAME = "libkhq_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["khq_kernels.hip", "khq_attn_ws.hip", "khq_finish.hip", "khq_prefill.hip", "khq_dump.hip",
+SOURCES = ["khq_kernels.hip", "khq_attn_ws.hip", "khq_finish.hip", "khq_prefill.hip", "khq_dump.hip", "khq_calib.hip",
            "khq_capi.cpp", "khq_layer.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -331,6 +331,40 @@ int khq_dump_attn(khq_dump* dump, int layer, const void* q_gate, const void* k_r
  * KHQD recording.  Synchronises the device. */
 int khq_dump_flush(khq_dump* dump);
 
+/* ---- calibration (replaces the calibration entry points of
+ * ref:src/csrc/qmv_sm75_kernel.cu:4434-4810, driven by
+ * ref:src/khq/calib.mojo:285-566; host driver: khq/calib.py) ----
+ * All pointers are f32 device buffers; rows = i1.  Synchronous for ops
+ * 2 and 4..9.  Returns 0, -100 on bad arguments, -1 for an unknown op, else a
+ * hipError_t.  Ops (argument roles as in the reference):
+ *   1 FWHT base     a x[rows][256], b d[256] -> e norms[rows],
+ *                   f base = FWHT(x fp16(d) / norm) / 16
+ *   2 K static      a proj -> f cents[4][256] = [0, -c, c, c], g ts
+ *                   (c = 0.935 sigma ts, ts = 16 / sqrt(sum 0.528756 c0^2 + 0.464545 sigma^2))
+ *   3 rotate        a rows, b rotor[64][16] -> e rows R^T per patch
+ *   4 PCA           a FWHT-domain rows -> e rotor (columns: eigenvectors 2, 3, 4, 1
+ *                   by decreasing eigenvalue)
+ *   5 k-means 4     a rows -> e cents[4][256] (20 Lloyd iterations per dim)
+ *   6 k-means VQ    a rotated rows -> e codebook[64][256][3] (30 iterations, seed i2)
+ *   7 Procrustes    a rows, b codebook, e rotor in/out (i2 Lloyd iterations)
+ *   8 SmartK        a x32, b x16, c d_k, d rotor, e cents, f1 ts -> f cents, g (ts, alpha)
+ *   9 SmartV        a x32, b x16, c d_v, d rotor, e cents, f codebook, f1 ts -> g (ts, alpha)
+ *  10 head-major    a rows [i1 tokens][i2 heads][256] -> e [i2][i1][256] */
+int launch_cal_op(int op, const void* a, const void* b, const void* c, const void* d, void* e,
+                  void* f, void* g, float f1, float f2, int i1, int i2, int i3, int i4,
+                  hipStream_t stream);
+
+/* SmartVQ tournament (replaces launch_cal_svq_train, ref .cu:4434-4596):
+ * v f32 [N][256] head-major FWHT-domain V rows (N = H_kv * T), attn f32
+ * [H_q][T][T] softmax scores (NULL: plain reconstruction loss), init_cb and
+ * out_cb f32 [64][256][3], rp f32 [64][16]; out_wtrm f32 [256][256] = I + A B
+ * of the winner (may be NULL).  Seeds 42, 137, 271 (n_seeds <= 3): 30 steps
+ * each, then the remaining iterations for each, best attention-MSE proxy
+ * first; the winner has the smallest proxy.  Synchronous. */
+int launch_cal_svq_train(const void* v, const void* attn, const void* init_cb, const void* rp,
+                         void* out_cb, void* out_wtrm, int N, int T, int H_q, int H_kv,
+                         int iterations, int n_seeds, float lr, hipStream_t stream);
+
 /* Attaches a dump recorder to a layer (NULL detaches): its
  * khq_layer_attention_step then records the token under `layer_id`
  * (ref attention.mojo:340-341, 355-356).  The recorder is not owned. */

@@ -1,0 +1,235 @@
+"""CPU restatement of the KHQ calibration steps (test infrastructure only).
+
+numpy versions of launch_cal_op ops 1-7 and 10 and of the SmartK / SmartV
+round trips (ref:src/csrc/qmv_sm75_kernel.cu:2019-2085, 2645-2681,
+2722-3025, 3071-3349, 4598-4810), written from the reference's algorithm in
+float64 so they can check the GPU steps (tests/test_gpu_calib.py); each is
+itself pinned in tests/test_calib_ref.py against closed forms (explicit
+Hadamard matrix, numpy eigh, SVD polar factor, Lloyd fixed points, the
+independent format decoders of tests/npref.py).  Nothing in the product
+imports this file.
+"""
+from __future__ import annotations
+
+import numpy as np
+from scipy.linalg import hadamard
+
+D, NP = 256, 64
+FS = 0.0625
+H256 = hadamard(D).astype(np.float64)
+
+
+def f16(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float64)
+
+
+def fwht_base(x, d):
+    """op 1 (.cu:2019-2070): norms, FWHT(x fp16(d) / (norm + 1e-8)) / 16."""
+    x = np.asarray(x, np.float64)
+    n = np.sqrt((x * x).sum(1) + 1e-8)
+    r = x * f16(d)[None, :] / (n[:, None] + 1e-8)
+    return n, (r @ H256.T) * FS
+
+
+def rotate(x, rp):
+    """op 3 (.cu:2073-2085): out[p][c] = sum_k x[p][k] rp[16p + 4k + c]."""
+    R = np.asarray(rp, np.float64).reshape(NP, 4, 4)
+    return np.einsum("npk,pkc->npc", np.asarray(x, np.float64).reshape(-1, NP, 4), R).reshape(-1, D)
+
+
+def k_static(proj):
+    """op 2 (.cu:2645-2681)."""
+    sg = np.asarray(proj, np.float64).std(0)
+    c0 = 0.935 * sg
+    ts = 16.0 / np.sqrt((0.528756 * c0 * c0 + 0.464545 * sg * sg).sum())
+    c = 0.935 * sg * ts
+    return np.stack([np.zeros(D), -c, c, c]), ts
+
+
+def pca_rotors(base):
+    """op 4 (.cu:3071-3145) by eigh: rotor column c = eigenvector of rank
+    {1, 2, 3, 0}[c] by decreasing eigenvalue of the uncentred moment + 1e-3 I."""
+    b = np.asarray(base, np.float64).reshape(-1, NP, 4)
+    out = np.zeros((NP, 4, 4))
+    for p in range(NP):
+        m = b[:, p].T @ b[:, p] + 1e-3 * np.eye(4)
+        w, v = np.linalg.eigh(m)
+        order = np.argsort(-w)
+        for c, s in enumerate((1, 2, 3, 0)):
+            out[p, :, c] = v[:, order[s]]
+    return out.reshape(NP, 16)
+
+
+def kmeans4(data, iters=20):
+    """op 5 (.cu:3147-3183): per dim, init (mn + (mx - mn) k / 3) * 0.8,
+    Lloyd, first minimum wins, empty cluster -> 0."""
+    x = np.asarray(data, np.float64)
+    mn, mx = x.min(0), x.max(0)
+    c = np.stack([(mn + (mx - mn) * (k / 3.0)) * 0.8 for k in range(4)])  # [4, D]
+    for _ in range(iters):
+        dist = (x[None, :, :] - c[:, None, :]) ** 2       # [4, rows, D]
+        a = np.argmin(dist, 0)                             # first minimum
+        new = np.zeros_like(c)
+        for k in range(4):
+            m = a == k
+            cnt = m.sum(0)
+            new[k] = np.where(cnt > 0, (x * m).sum(0) / np.maximum(cnt, 1), 0.0)
+        c = new
+    return c
+
+
+def xorshift_rows(seed, rows):
+    """op 6 initial codeword rows: per entry i = 256 p + k, s = seed ^ (i *
+    2654435761 + 1) (u32), one xorshift, idx = (s & 0xFFFFFF) / 2^24 * rows."""
+    i = np.arange(NP * 256, dtype=np.uint64)
+    s = (np.uint64(seed) ^ ((i * np.uint64(2654435761) + np.uint64(1)) & np.uint64(0xFFFFFFFF)))
+    s &= np.uint64(0xFFFFFFFF)
+    s ^= (s << np.uint64(13)) & np.uint64(0xFFFFFFFF)
+    s ^= s >> np.uint64(17)
+    s ^= (s << np.uint64(5)) & np.uint64(0xFFFFFFFF)
+    u = (s & np.uint64(0xFFFFFF)).astype(np.float32) / np.float32(16777216.0)
+    idx = (u * np.float32(rows)).astype(np.int64)
+    return np.minimum(idx, rows - 1).reshape(NP, 256)
+
+
+def nearest(v3, cb):
+    """first-minimum nearest codeword: v3 [n, 3], cb [256, 3]."""
+    d = ((v3[:, None, :] - cb[None, :, :]) ** 2).sum(-1)
+    return np.argmin(d, 1)
+
+
+def kmeans_vq(rot, seed, iters=30):
+    """op 6 (.cu:3185-3249)."""
+    x = np.asarray(rot, np.float64).reshape(-1, NP, 4)
+    idx = xorshift_rows(seed, x.shape[0])
+    C = np.stack([x[idx[p], p, :3] for p in range(NP)])  # [NP, 256, 3]
+    for _ in range(iters):
+        for p in range(NP):
+            a = nearest(x[:, p, :3], C[p])
+            cnt = np.bincount(a, minlength=256)
+            for c in range(3):
+                s = np.bincount(a, weights=x[:, p, c], minlength=256)
+                C[p, :, c] = np.where(cnt > 0, s / np.maximum(cnt, 1), C[p, :, c])
+    return C
+
+
+def polar_ns(M, iters=12):
+    """Newton-Schulz polar iteration of ref .cu:3308-3349: X = M / |M|_F,
+    X <- X (3 I - X^T X) / 2; kept as M's orthogonal polar factor's
+    approximation (tests pin it against the SVD polar factor)."""
+    X = np.asarray(M, np.float64) / np.sqrt((np.asarray(M, np.float64) ** 2).sum() + 1e-8)
+    for _ in range(iters):
+        X = 0.5 * X @ (3.0 * np.eye(4) - X.T @ X)
+    return X
+
+
+def procrustes(base, vq, rp, iters):
+    """op 7 (.cu:3266-3349): target = nearest codeword (dims 0..2) of the
+    rotated row plus its own dim 3, M = base^T target per patch, rotor =
+    polar_ns(M)."""
+    b = np.asarray(base, np.float64)
+    R = np.asarray(rp, np.float64).reshape(NP, 16).copy()
+    vq = np.asarray(vq, np.float64).reshape(NP, 256, 3)
+    for _ in range(iters):
+        rot = rotate(b, R).reshape(-1, NP, 4)
+        tgt = rot.copy()
+        for p in range(NP):
+            tgt[:, p, :3] = vq[p][nearest(rot[:, p, :3], vq[p])]
+        bb = b.reshape(-1, NP, 4)
+        for p in range(NP):
+            R[p] = polar_ns(bb[:, p].T @ tgt[:, p]).reshape(16)
+    return R
+
+
+def roundtrip_k(proj, norms, cents, rp, d, alpha):
+    """SmartK round trip (.cu:2722-2862 as the tournament runs it): codes
+    from |p| > 1.6 f_s (sign) or +-0.47 f_s, never code 3; mult over codes
+    1, 2; decode sign * cents[2] * mult * alpha * norm -> R -> H -> / (256 d)."""
+    p = np.asarray(proj, np.float64)
+    cb = np.asarray(cents, np.float64).reshape(4, D)[2]
+    a = np.abs(p)
+    sg = np.where(a > 1.6 * FS, np.sign(p), np.where(p > 0.47 * FS, 1.0, np.where(p < -0.47 * FS, -1.0, 0.0)))
+    nz = sg != 0
+    sn = (a * nz).sum(1)
+    sc = (f16(cb)[None, :] * nz).sum(1)
+    mult = np.where(sc > 1e-5, sn / np.where(sc > 0, sc, 1), 1.0)
+    mult = np.where((mult < 0.1) | (mult > 10), 1.0, mult)
+    m2 = np.floor(mult.astype(np.float32) * np.float32(1000.0)).astype(np.float64) / 1000.0
+    m2 = np.where((m2 < 0.1) | (m2 > 10), 1.0, m2)
+    kv = sg * cb[None, :] * m2[:, None] * alpha * np.asarray(norms, np.float64)[:, None]
+    R = np.asarray(rp, np.float64).reshape(NP, 4, 4)  # [p][k][c]
+    y = np.einsum("pck,npk->npc", R, kv.reshape(-1, NP, 4)).reshape(-1, D)
+    return (y @ H256.T) / (256.0 * np.asarray(d, np.float64)[None, :])
+
+
+def dim_weights(x):
+    x = np.asarray(x, np.float64)
+    m = np.abs(x).mean(0)
+    v = x.var(0)
+    return m / (m.sum() + 1e-8), v / (v.sum() + 1e-8)
+
+
+def roundtrip_v(proj, norms, cents, vq, rp, d, alpha):
+    """SmartV round trip (.cu:2863-3025): per patch the nearest fp16(vq) *
+    alpha codeword (first minimum), dim-3 code by |p3 - a c| (ties to 1),
+    dump = clamp(round(res / max(g, 1e-4) * 7 + 8)), energy correction
+    rounded to fp16; decode with the unrounded tables -> R -> H -> / (16 d)."""
+    p = np.asarray(proj, np.float64).reshape(-1, NP, 4)
+    n = p.shape[0]
+    cbf = np.asarray(vq, np.float64).reshape(NP, 256, 3)
+    cb16 = f16(cbf) * alpha
+    cv = np.asarray(cents, np.float64).reshape(4, D)[:2, np.arange(NP) * 4 + 3]  # [2, NP]
+    out = np.zeros((n, NP, 4))
+    te = (p[:, :, :3] ** 2).sum((1, 2))
+    code = np.stack([nearest(p[:, q, :3], cb16[q]) for q in range(NP)], 1)  # [n, NP]
+    sel16 = cb16[np.arange(NP)[None, :], code]
+    ve = (sel16 ** 2).sum((1, 2))
+    rn = f16(np.sqrt(te / (ve + 1e-8)))
+    c0, c1 = f16(cv[0]) * alpha, f16(cv[1]) * alpha
+    d3 = np.where(np.abs(p[:, :, 3] - c0) < np.abs(p[:, :, 3] - c1), 0, 1)
+    res = p[:, :, 3] - np.where(d3 == 0, c0, c1)
+    g = np.abs(res).max(1)
+    rsc = np.maximum(g, 1e-4)
+    x = res / rsc[:, None] * 7.0 + 8.0
+    dump = np.clip(np.where(x >= 0, np.floor(x + 0.5), -np.floor(-x + 0.5)), 0, 15)
+    nr = np.asarray(norms, np.float64)
+    out[:, :, :3] = cbf[np.arange(NP)[None, :], code] * alpha * (nr * rn)[:, None, None]
+    cvd = np.where(d3 == 0, cv[0][None, :], cv[1][None, :]) * alpha
+    out[:, :, 3] = cvd * nr[:, None] + (dump - 8.0) / 7.0 * (g * nr)[:, None]
+    R = np.asarray(rp, np.float64).reshape(NP, 4, 4)
+    y = np.einsum("pck,npk->npc", R, out).reshape(n, D)
+    return (y @ H256.T) / (16.0 * np.asarray(d, np.float64)[None, :])
+
+
+def tournament(x32, x16, d, rp, cents, ts0, vq=None):
+    """ops 8 (vq None: K) and 9 (V) in float64: returns (ts, alpha)."""
+    wm, wv = dim_weights(x32)
+    norms, proj = fwht_base(np.asarray(x16, np.float32).astype(np.float64), d)
+    norms = f16(norms)
+    base = np.asarray(cents, np.float64).reshape(4, D) / ts0
+    best = {k: [1.0, ts0, 1e30, 1e30] for k in ("f", "m", "v")}
+    deltas = [-0.03, -0.02, -0.01, 0.0, 0.01, 0.02, 0.03, 0.04]
+    x32 = np.asarray(x32, np.float64)
+    for phase in range(4):
+        c = best[{1: "f", 2: "m", 3: "v"}.get(phase, "f")]
+        ac, mc = (c[0], c[1] / ts0) if phase else (1.0, 1.0)
+        for ia in range(8):
+            for it in range(8):
+                a = 0.80 + 0.05 * ia if phase == 0 else ac + deltas[ia]
+                m = 0.80 + 0.05 * it if phase == 0 else mc + deltas[it]
+                ts = ts0 * m
+                if vq is None:
+                    rec = roundtrip_k(proj, norms, f16(base * ts), rp, d, a)
+                else:
+                    rec = roundtrip_v(proj, norms, cents, vq, rp, d, a)
+                sq = (x32 - rec) ** 2
+                e = {"f": sq.mean(), "m": (sq * wm).sum() / len(sq), "v": (sq * wv).sum() / len(sq)}
+                me = np.sqrt(sq.max())
+                for k in ("f", "m", "v"):
+                    if e[k] < best[k][2]:
+                        best[k] = [a, ts, e[k], me]
+    w = best["f"]
+    for k in ("m", "v"):
+        if best[k][3] < w[3]:
+            w = best[k]
+    return w[1], w[0]

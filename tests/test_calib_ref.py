@@ -1,0 +1,162 @@
+"""Pins the CPU restatement of the calibration steps (oracle/calib_ref.py)
+against closed forms and independent implementations (no GPU)."""
+import numpy as np
+
+import calib_ref as R
+import npref
+
+
+def test_fwht_base_is_an_isometry_and_involution():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((8, 256))
+    d = np.where(rng.random(256) < 0.5, -1.0, 1.0)
+    n, base = R.fwht_base(x, d)
+    np.testing.assert_allclose(n, np.sqrt((x ** 2).sum(1) + 1e-8))
+    # H/16 is orthogonal: |base| = |x d / n| = 1, and applying it again restores x d / n
+    np.testing.assert_allclose(np.linalg.norm(base, axis=1), 1.0, rtol=1e-6)
+    back = (base @ R.H256.T) / 16.0
+    np.testing.assert_allclose(back, x * d / (n[:, None] + 1e-8), atol=1e-12)
+
+
+def test_k_static_closed_form():
+    # sigma = s in every dim: ts = 16 / sqrt(256 s^2 (0.528756 * 0.935^2 + 0.464545))
+    rng = np.random.default_rng(1)
+    s = 0.05
+    x = np.sign(rng.standard_normal((4000, 256))) * s  # population std exactly s
+    x -= x.mean(0)
+    sg = x.std(0)
+    cents, ts = R.k_static(x)
+    want_ts = 16.0 / np.sqrt((sg ** 2 * (0.528756 * 0.935 ** 2 + 0.464545)).sum())
+    assert abs(ts - want_ts) < 1e-12
+    assert np.allclose(cents[0], 0) and np.allclose(cents[2], 0.935 * sg * ts)
+    assert np.allclose(cents[1], -cents[2]) and np.allclose(cents[3], cents[2])
+
+
+def test_pca_rotors_diagonalise_and_order():
+    rng = np.random.default_rng(2)
+    A = rng.standard_normal((64, 4, 4))
+    base = np.einsum("npk,pkc->npc", rng.standard_normal((3000, 64, 4)), A).reshape(-1, 256)
+    rp = R.pca_rotors(base).reshape(64, 4, 4)
+    b = base.reshape(-1, 64, 4)
+    for p in range(64):
+        Q = rp[p]
+        np.testing.assert_allclose(Q.T @ Q, np.eye(4), atol=1e-10)
+        m = b[:, p].T @ b[:, p] + 1e-3 * np.eye(4)
+        lam = np.diag(Q.T @ m @ Q)
+        off = Q.T @ m @ Q - np.diag(lam)
+        assert np.abs(off).max() < 1e-8 * np.abs(lam).max()
+        # column 3 holds the largest eigenvalue, columns 0..2 the rest descending
+        assert lam[3] >= lam[0] >= lam[1] >= lam[2]
+
+
+def _kmeans4_loops(x, iters=20):
+    rows, dims = x.shape
+    out = np.zeros((4, dims))
+    for dcol in range(dims):
+        col = [float(v) for v in x[:, dcol]]
+        mn, mx = min(col), max(col)
+        c = [(mn + (mx - mn) * (k / 3.0)) * 0.8 for k in range(4)]
+        for _ in range(iters):
+            s, n = [0.0] * 4, [0] * 4
+            for v in col:
+                bk, bd = 0, (v - c[0]) ** 2
+                for k in range(1, 4):
+                    if (v - c[k]) ** 2 < bd:
+                        bd, bk = (v - c[k]) ** 2, k
+                s[bk] += v
+                n[bk] += 1
+            c = [s[k] / max(n[k], 1) for k in range(4)]
+        out[:, dcol] = c
+    return out
+
+
+def test_kmeans4_matches_plain_loops():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((200, 6)) * rng.uniform(0.5, 2, 6)
+    x = np.concatenate([x, np.zeros((200, 250))], 1)  # a constant dim: three empty clusters
+    got = R.kmeans4(x)
+    np.testing.assert_allclose(got[:, :6], _kmeans4_loops(x[:, :6]), atol=1e-12)
+    np.testing.assert_allclose(got[:, 6], [0.0, 0.0, 0.0, 0.0])
+
+
+def test_xorshift_rows_matches_u32_loop():
+    seed, rows = 3 * 7919 + 13, 1000
+    got = R.xorshift_rows(seed, rows)
+    for i in (0, 1, 255, 256, 9999, 16383):
+        s = (seed ^ ((i * 2654435761 + 1) & 0xFFFFFFFF)) & 0xFFFFFFFF
+        s ^= (s << 13) & 0xFFFFFFFF
+        s ^= s >> 17
+        s ^= (s << 5) & 0xFFFFFFFF
+        u = np.float32(s & 0xFFFFFF) / np.float32(16777216.0)
+        assert got.reshape(-1)[i] == min(int(u * np.float32(rows)), rows - 1)
+
+
+def test_kmeans_vq_is_a_lloyd_fixed_point_on_separated_data():
+    rng = np.random.default_rng(4)
+    centers = rng.standard_normal((64, 256, 3)) * 10
+    lab = rng.integers(0, 256, (400, 64))
+    pts = centers[np.arange(64)[None, :], lab] + rng.standard_normal((400, 64, 3)) * 0.01
+    rot = np.concatenate([pts, np.zeros((400, 64, 1))], 2).reshape(400, 256)
+    C = R.kmeans_vq(rot, seed=7, iters=10)
+    x = rot.reshape(-1, 64, 4)
+    for p in range(0, 64, 9):
+        a = R.nearest(x[:, p, :3], C[p])
+        for k in np.unique(a):
+            np.testing.assert_allclose(C[p, k], x[a == k, p, :3].mean(0), atol=1e-12)
+
+
+def test_polar_ns_converges_to_the_svd_polar_factor():
+    rng = np.random.default_rng(8)
+    for _ in range(20):
+        Q, _ = np.linalg.qr(rng.standard_normal((4, 4)))
+        M = Q @ np.diag(rng.uniform(0.5, 2.0, 4)) @ np.linalg.qr(rng.standard_normal((4, 4)))[0]
+        u, _, vt = np.linalg.svd(M)
+        np.testing.assert_allclose(R.polar_ns(M), u @ vt, atol=1e-9)
+
+
+def test_procrustes_polar_factor_is_orthogonal_and_optimal():
+    rng = np.random.default_rng(5)
+    base = rng.standard_normal((800, 256))
+    # codebooks fitted to the rows themselves: M is well conditioned
+    vq = R.kmeans_vq(base, seed=3, iters=2)
+    rp = np.tile(np.eye(4).reshape(16), (64, 1))
+    out = R.procrustes(base, vq, rp, iters=1).reshape(64, 4, 4)
+    rot = base.reshape(-1, 64, 4)
+    tgt = rot.copy()
+    for p in range(64):
+        tgt[:, p, :3] = vq[p][R.nearest(rot[:, p, :3], vq[p])]
+    for p in (0, 17, 63):
+        Q = out[p]
+        np.testing.assert_allclose(Q.T @ Q, np.eye(4), atol=1e-10)
+        M = rot[:, p].T @ tgt[:, p]
+        best = np.trace(Q.T @ M)
+        for _ in range(50):  # no random orthogonal matrix does better
+            Z, _ = np.linalg.qr(rng.standard_normal((4, 4)))
+            assert np.trace(Z.T @ M) <= best + 1e-9
+
+
+def test_roundtrip_k_matches_the_independent_decoder():
+    """The tournament's K decode equals tests/npref.decode_k on the same codes
+    written as a mask with no code 3 and the (u32)(mult * 1000) word."""
+    rng = np.random.default_rng(6)
+    proj = rng.standard_normal((16, 256)) * 0.08
+    norms = rng.uniform(0.5, 2.0, 16)
+    cents = np.zeros((4, 256))
+    cents[2] = np.abs(rng.standard_normal(256)) * 0.06 + 0.01
+    rp = np.tile(np.eye(4).reshape(16), (64, 1))
+    d = np.where(rng.random(256) < 0.5, -1.0, 1.0)
+    got = R.roundtrip_k(proj, norms, cents, rp, d, alpha=0.9)
+    a = np.abs(proj)
+    code = np.where(a > 1.6 * R.FS, np.where(proj > 0, 2, 1),
+                    np.where(proj > 0.47 * R.FS, 2, np.where(proj < -0.47 * R.FS, 1, 0)))
+    mask = (code.reshape(16, 16, 16).astype(np.uint64) << (2 * np.arange(16, dtype=np.uint64))).sum(2)
+    nz = code != 0
+    mult = (a * nz).sum(1) / (R.f16(cents[2])[None, :] * nz).sum(1)
+    kpay = np.zeros((16, 40), np.uint8)
+    kpay[:, 0:4] = np.floor(mult.astype(np.float32) * np.float32(1000)).astype(np.uint32).view(np.uint8).reshape(16, 4)
+    want = npref.decode_k(mask.astype(np.uint32), kpay, norms.astype(np.float16), np.zeros(16, np.float16),
+                          cents.astype(np.float16), rp.astype(np.float16), d, 0.9)
+    # npref reads fp16 norms and cents; compare with those rounded inputs
+    got16 = R.roundtrip_k(proj, R.f16(norms), R.f16(cents), rp, d, alpha=0.9)
+    np.testing.assert_allclose(got16, want, rtol=1e-6, atol=1e-9)
+    assert np.abs(got - want).max() < 1e-2 * np.abs(want).max()
