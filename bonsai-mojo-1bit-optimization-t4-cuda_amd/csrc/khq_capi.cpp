@@ -611,6 +611,12 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
                                float alpha_k, float alpha_v, float rope_base, hipStream_t stream) {
     if (!seqs || n_seq <= 0 || n_seq > 4096) return -100;
     if (H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || H_q / H_kv > 8) return -100;
+    // The per-call argument block goes to the device with a copy from host
+    // staging memory that the next call reuses: a captured copy would replay
+    // whatever a later call left there, so capture is refused.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess) return -100;
+    if (cap != hipStreamCaptureStatusNone) return -105;
     for (int i = 0; i < n_seq; i++) {
         const khq_seq& q = seqs[i];
         if (q.c_len < 0 || q.win_len < 0 || (q.c_len == 0 && q.win_len == 0)) return -100;

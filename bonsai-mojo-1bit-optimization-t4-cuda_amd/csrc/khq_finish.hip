@@ -23,8 +23,11 @@ typedef float f2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ f2 ldg_f2(const float* p) {
     return *(const __attribute__((address_space(1))) f2*)p;
 }
+// Partial rows are 258 floats long, so a row's dims are only 8-byte aligned:
+// four floats are read as two 8-byte loads.
 __device__ __forceinline__ f4 ldg_f4(const float* p) {
-    return *(const __attribute__((address_space(1))) f4*)p;
+    const f2 a = ldg_f2(p), b = ldg_f2(p + 2);
+    return f4{a.x, a.y, b.x, b.y};
 }
 
 constexpr int DS = 32;         // dims per block

@@ -341,8 +341,16 @@ int khq_layer_prefill(khq_layer* L, const void* q_gate, const void* k_roped, con
         }
         // finite contents everywhere: padding keys of a launch get P = 0
         if (hipMemsetAsync(L->dk, 0, kb, stream) != hipSuccess ||
-            hipMemsetAsync(L->dvt, 0, vb, stream) != hipSuccess)
+            hipMemsetAsync(L->dvt, 0, vb, stream) != hipSuccess) {
+            // leave no half-initialised dense key space behind: the next
+            // call allocates and clears it again
+            (void)hipStreamSynchronize(stream);
+            (void)hipFree(L->dk);
+            (void)hipFree(L->dvt);
+            L->dk = nullptr;
+            L->dvt = nullptr;
             return -100;
+        }
         L->dec_hi = 0;
     }
     const __half* qg = static_cast<const __half*>(q_gate);

@@ -204,6 +204,9 @@ int khq_prefill_attn_fp16(const void* q_gate, const void* k, const void* vt, int
                           int n_q, int vis0, int H_q, int H_kv, float scale, void* out,
                           hipStream_t stream);
 
+/* khq_attn_step_batched_fp16 copies its per-sequence arguments from host
+ * staging memory on every call, so it returns -105 on a stream under HIP
+ * graph capture (a captured copy would replay stale arguments). */
 int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centroids_k,
                                const void* centroids_v, const void* vq_centroids,
                                const void* k_rotor, const void* v_rotor, const void* d_vec_k,

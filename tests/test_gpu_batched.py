@@ -131,3 +131,23 @@ def test_batched_c4_ragged_32(device):
                   ring_k=s["ring_k"].cpu().numpy(), ring_v=s["ring_v"].cpu().numpy(),
                   win_start=s["win_start"], win_len=s["win_len"])
         close(s["out"].cpu().numpy(), _oracle_out(st))
+
+
+def test_batched_refuses_graph_capture(device):
+    """Under HIP graph capture the batched call returns -105 and launches
+    nothing (its argument copy comes from host staging a later call reuses)."""
+    lc, h = layer_consts()
+    rng = np.random.default_rng(12)
+    st = _seq_state(rng, lc, h, 384, 128, 128, seed=300)
+    cents = ops.Centroids(lc, device)
+    n_rows = st["rows"]["kmask"].shape[0]
+    out = torch.zeros((H_Q, D), device=device, dtype=torch.float16)
+    seqs = [dict(q_gate=t(st["q_gate"]), pay=payload_from_rows(st["rows"], n_rows),
+                 ring_k=t(st["ring_k"]), ring_v=t(st["ring_v"]), out=out, c_len=384,
+                 win_start=128, win_len=128, ring_cap=256)]
+    ops.attn_step_batched(seqs, cents, H_q=H_Q, H_kv=H_KV, scale=SCALE)  # eager: fine
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = ops.attn_step_batched(seqs, cents, H_q=H_Q, H_kv=H_KV, scale=SCALE, check=False)
+    assert rc == -105
