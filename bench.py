@@ -234,6 +234,10 @@ def main():
             e0.elapsed_time(e1) * 1000.0 / args.steps, 3)
         del upay
 
+    # the same fused step replayed from a HIP graph (launch overhead off the
+    # host), checked bit for bit against the eager outputs
+    result["graph_layer_step_us"] = round(graph_us(step, args.steps, layers) / args.layers, 3)
+
     if not args.no_sweep:
         # the reference's launch sequence per layer (ref:src/khq/runtime.mojo:554-613):
         # launch_khq_attn_fp16 (split-K partials into out_partial + reduce),
@@ -254,21 +258,12 @@ def main():
                                     win_len=win_len, ring_cap=RING, H_q=H_Q, H_kv=H_KV,
                                     scale=scale)
                     ops.merge_gate(ac, aw, L["q"], L["out"], H_q=H_Q, has_w=True)
-            ref_step()
-            torch.cuda.synchronize()
-            e0.record(stream)
-            for _ in range(args.steps):
-                ref_step()
-            e1.record(stream)
-            torch.cuda.synchronize()
-            sweep[f"splits_{sp}"] = round(e0.elapsed_time(e1) * 1000.0 / n_launch, 3)
+            sweep[f"splits_{sp}"] = round(graph_us(ref_step, args.steps, layers) / args.layers, 3)
             if sp > 1:
-                e0.record(stream)
-                for _ in range(n_launch):
-                    ops.attn_reduce(part, ac, num_queries=H_Q, num_splits=sp)
-                e1.record(stream)
-                torch.cuda.synchronize()
-                reduce_us[f"splits_{sp}"] = round(e0.elapsed_time(e1) * 1000.0 / n_launch, 3)
+                def red_step():
+                    for _ in layers:
+                        ops.attn_reduce(part, ac, num_queries=H_Q, num_splits=sp)
+                reduce_us[f"splits_{sp}"] = round(graph_us(red_step, args.steps) / args.layers, 3)
         result["reference_entry_us_per_layer_step"] = sweep
         result["split_reduce_us"] = reduce_us
 
@@ -276,6 +271,35 @@ def main():
         result["cpu_baseline"] = cpu_baseline(layers[0], c_len, win_len, win_start, scale,
                                               args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+def graph_us(step, reps, layers=None):
+    """GPU time of one call of step(), in us: step's launches captured once
+    into a HIP graph (after an eager call that sizes the library workspace)
+    and replayed reps times between HIP events, so host issue overhead is not
+    counted.  When layers is given, every layer's output after the last
+    replay must equal the eager call's bit for bit."""
+    import torch
+
+    step()
+    torch.cuda.synchronize()
+    want = [L["out"].clone() for L in layers] if layers else []
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    for L, w in zip(layers or [], want):
+        if not torch.equal(L["out"], w):
+            raise RuntimeError("graph replay differs from the eager step")
+    return e0.elapsed_time(e1) * 1000.0 / reps
 
 
 def counters_run(args):
@@ -517,6 +541,15 @@ def bench_small(args):
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": None,
     }
+    if not args.no_cpu:
+        if args.config == "c1":
+            q, k, v, _ = layers[0]
+            result["cpu_baseline"] = cpu_baseline_c1(q, k, v, scale, args.cpu_seconds)
+        else:
+            q, pay, cents, rk, rv, _ = layers[0]
+            L0 = dict(pay=pay, lc=synthetic_layer(0, seed=1234), q=q, ring_k=rk, ring_v=rv)
+            result["cpu_baseline"] = cpu_baseline(L0, 384, 128, 384 % RING, scale,
+                                                  args.cpu_seconds)
     print(json.dumps(result))
 
 
@@ -615,6 +648,34 @@ def bench_c4(args):
         "sequential_calls_us_per_layer_step": round(ms_s * 1000.0 / args.layers, 3),
     }
     print(json.dumps(result), flush=True)
+
+
+def cpu_baseline_c1(q, k, v, scale, budget_s):
+    """Config 1's CPU path: the oracle's restatement of the host attention of
+    ref:src/models/qwen3_5/attention.mojo:97-201 (fp32, softmax over 512
+    positions, sigmoid gate), timed single-threaded and with OpenMP over query
+    heads on the host's cores."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    qh, kh, vh = q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy()
+    res = {}
+    for threads in (1, max(1, min(16, os.cpu_count() or 1))):
+        oracle.set_num_threads(threads)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            oracle.gqa_host(qh, kh, vh, seq_len=512, H_q=H_Q, H_kv=H_KV, scale=scale)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s / 2 or reps >= 2000:
+                break
+        res[threads] = el / reps * 1e6
+    nt = max(res)
+    return {"value": round(res[nt], 1), "unit": "us/layer-step", "cores": nt,
+            "single_thread_us": round(res[1], 1), "host_nproc": os.cpu_count(),
+            "kind": "port",
+            "sample": "layer 0 of the same workload (512 positions, 24/4 heads), repeated; "
+                      "value with OpenMP over query heads, single_thread_us on one core"}
 
 
 def cpu_baseline(L, c_len, win_len, win_start, scale, budget_s):
