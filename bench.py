@@ -187,7 +187,7 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f16-mfma/f32-acc",
         "data": ("synthetic: N(0,1) K/V rows compressed by the library's KHQ compressor, "
                  "N(0,1) fp16 ring" if args.data == "compressed" else
                  "synthetic: seeded uniform-random packed codes, outlier count ~U[0,50], "
@@ -531,7 +531,7 @@ def bench_small(args):
         "metric": metric, "value": round(us_layer, 3), "unit": "us/layer-step", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f16-in/f32-acc" if args.config == "c1" else "f32",
+        "dtype": "f16-in/f32-acc" if args.config == "c1" else "f16-mfma/f32-acc",
         "data": "synthetic: N(0,1) fp16 K/V" if args.config == "c1" else
                 "synthetic: seeded uniform-random packed codes, N(0,1) fp16 ring",
         "config": {"workload": workload, "layers": args.layers, "parallelism": "1 GPU"},
@@ -633,7 +633,7 @@ def bench_c4(args):
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f16-mfma/f32-acc",
         "data": "synthetic: seeded uniform-random packed codes, outlier count ~U[0,50], "
                 "N(0,1) fp16 rings",
         "config": {
