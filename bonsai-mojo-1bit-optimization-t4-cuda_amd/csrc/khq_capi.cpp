@@ -16,34 +16,70 @@
 namespace {
 
 constexpr int kMaxDevices = 64;
-std::mutex g_ws_mu;
-void* g_ws[kMaxDevices] = {nullptr};
-size_t g_ws_bytes[kMaxDevices] = {0};
 
 int rc_of(hipError_t e) { return e == hipSuccess ? 0 : static_cast<int>(e); }
 
-// Device workspace for split partials, grown on demand (never shrunk).
-hipError_t workspace(size_t bytes, float** out) {
+// Device workspace for split partials, one per device, grown on demand
+// (never shrunk; growing waits for the device).  Launches on different
+// streams are ordered on the GPU: when a launch comes on another stream than
+// the previous user of the workspace, the library records an event on the
+// previous stream (all its work so far, the last use included) and makes the
+// new stream wait for it, so two streams never use the workspace at once.
+// A stream under graph capture is not ordered this way (a graph runs when it
+// is replayed, not when it is captured): replays of a captured graph and
+// eager launches on other streams must not overlap.
+struct Workspace {
+    void* p = nullptr;
+    size_t bytes = 0;
+    bool used = false;
+    hipStream_t last = nullptr;  // stream of the previous use
+    hipEvent_t ev = nullptr;     // handed from the previous stream to the next
+};
+std::mutex g_ws_mu;
+Workspace g_ws[kMaxDevices];
+
+bool capturing(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+// stream = the stream the caller launches on; reserve calls pass use = false
+hipError_t workspace(size_t bytes, hipStream_t stream, float** out, bool use = true) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    if (g_ws_bytes[dev] < bytes) {
+    Workspace& w = g_ws[dev];
+    if (w.bytes < bytes) {
         size_t want = std::max(bytes, (size_t)4 << 20);
-        if (g_ws[dev]) {
+        if (w.p) {
             e = hipDeviceSynchronize();
             if (e != hipSuccess) return e;
-            e = hipFree(g_ws[dev]);
+            e = hipFree(w.p);
             if (e != hipSuccess) return e;
-            g_ws[dev] = nullptr;
-            g_ws_bytes[dev] = 0;
+            w.p = nullptr;
+            w.bytes = 0;
         }
-        e = hipMalloc(&g_ws[dev], want);
+        e = hipMalloc(&w.p, want);
         if (e != hipSuccess) return e;
-        g_ws_bytes[dev] = want;
+        w.bytes = want;
     }
-    *out = static_cast<float*>(g_ws[dev]);
+    if (use) {
+        if (w.used && w.last != stream && !capturing(stream) && !capturing(w.last)) {
+            if (!w.ev) {
+                e = hipEventCreateWithFlags(&w.ev, hipEventDisableTiming);
+                if (e != hipSuccess) return e;
+            }
+            e = hipEventRecord(w.ev, w.last);
+            if (e != hipSuccess) return e;
+            e = hipStreamWaitEvent(stream, w.ev, 0);
+            if (e != hipSuccess) return e;
+        }
+        w.used = true;
+        w.last = stream;
+    }
+    *out = static_cast<float*>(w.p);
     return hipSuccess;
 }
 
@@ -162,7 +198,7 @@ int khq_set_spin_limit(int sleeps) {
 
 int khq_workspace_reserve(size_t bytes) {
     float* p = nullptr;
-    return rc_of(workspace(bytes, &p));
+    return rc_of(workspace(bytes, nullptr, &p, false));
 }
 
 int launch_khq_compress_fp16(const void* x, const void* d_vec, const void* rotor,
@@ -238,7 +274,7 @@ int launch_khq_attn_fp16(const void* q, const void* k_payload, const void* v_pay
         float* part = outp;
         if (subs > 1) {
             float* ws = nullptr;
-            e = workspace((size_t)num_queries * nch * 258 * sizeof(float), &ws);
+            e = workspace((size_t)num_queries * nch * 258 * sizeof(float), stream, &ws);
             if (e != hipSuccess) return rc_of(e);
             part = ws;
         }
@@ -260,7 +296,7 @@ int launch_khq_attn_fp16(const void* q, const void* k_payload, const void* v_pay
     // into out_attn (the reference computes the same triple in one pass)
     const int np = compressed_parts(L_q > 1 ? std::min(c_len, L_q) : c_len, n_rep, h_kv, L_q);
     float* ws = nullptr;
-    e = workspace((size_t)num_queries * np * 258 * sizeof(float), &ws);
+    e = workspace((size_t)num_queries * np * 258 * sizeof(float), stream, &ws);
     if (e != hipSuccess) return rc_of(e);
     a.part = ws;
     a.n_parts = np;
@@ -289,7 +325,7 @@ int launch_khq_window_attn_fp16(const void* q, const void* ring_k, const void* r
         return -100;
     const int np = window_parts(win_len);
     float* ws = nullptr;
-    hipError_t e = workspace((size_t)H_q * np * 258 * sizeof(float), &ws);
+    hipError_t e = workspace((size_t)H_q * np * 258 * sizeof(float), stream, &ws);
     if (e != hipSuccess) return rc_of(e);
     khq::WinArgs w{};
     w.q = static_cast<const __half*>(q);
@@ -362,7 +398,7 @@ int launch_khq_gqa_attn_fp16(const void* q_gate, const void* k_cache, const void
         return -100;
     const int np = std::max(1, std::min(256, (seq_len + 15) / 16));
     float* ws = nullptr;
-    hipError_t e = workspace((size_t)H_q * np * 258 * sizeof(float), &ws);
+    hipError_t e = workspace((size_t)H_q * np * 258 * sizeof(float), stream, &ws);
     if (e != hipSuccess) return rc_of(e);
     khq::WinArgs w{};
     w.q = static_cast<const __half*>(q_gate);
@@ -394,7 +430,7 @@ int khq_attn_partials_fp16(const void* q_gate, const void* k_payload, const void
     if (c_len <= 0 || H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || H_q / H_kv > 8) return -100;
     const int npc = compressed_parts(c_len, H_q / H_kv, H_kv, 1);
     float* ws = nullptr;
-    hipError_t e = workspace((size_t)H_q * npc * 258 * sizeof(float), &ws);
+    hipError_t e = workspace((size_t)H_q * npc * 258 * sizeof(float), stream, &ws);
     if (e != hipSuccess) return rc_of(e);
     khq::AttnArgs a = attn_args(q_gate, k_payload, v_payload, v_shared_meta, k_mask, k_norms,
                                 k_r_norms, v_norms, v_r_norms, centroids_k, centroids_v,
@@ -449,7 +485,7 @@ static int attn_step_impl(const void* q_gate, const void* k_payload, const void*
         if (ws_bytes > kScratchBytes) return -103;
         e = scratch_ptr(&ws);
     } else {
-        e = workspace(ws_bytes, &ws);
+        e = workspace(ws_bytes, stream, &ws);
     }
     if (e != hipSuccess) return rc_of(e);
     const int ring = ring_cap > 0 ? ring_cap : 1;
@@ -684,7 +720,7 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
     const size_t meta_bytes = n_seq * (sizeof(khq::AttnArgs) + sizeof(khq::FinishArgs)) +
                               n_blocks * sizeof(int2) + 512;
     float* ws = nullptr;
-    hipError_t e = workspace(meta_off + meta_bytes, &ws);
+    hipError_t e = workspace(meta_off + meta_bytes, stream, &ws);
     if (e != hipSuccess) return rc_of(e);
     // metadata block (device and host staging share the layout): the
     // attention arguments, the finishing arguments, then the block map
@@ -787,7 +823,7 @@ int prefill_attn_run(const __half* q_gate, const __half* k, const __half* vt, in
     int per = 0;
     const int ns = prefill_splits(n_q, n_rep, H_kv, n_tot, &per);
     float* ws = nullptr;
-    hipError_t e = workspace((size_t)n_q * H_q * ns * 258 * sizeof(float), &ws);
+    hipError_t e = workspace((size_t)n_q * H_q * ns * 258 * sizeof(float), stream, &ws);
     if (e != hipSuccess) return rc_of(e);
     PrefillArgs a{};
     a.q = q_gate;

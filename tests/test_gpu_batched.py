@@ -88,7 +88,7 @@ def test_batched_error_codes(device):
 def test_batched_c4_ragged_32(device):
     """32 ragged sequences, L ~ U[1024, 16384] compressed tokens each plus a
     raw window of L % 256 + 1 tokens, against one single-sequence step each;
-    then the oracle on the two shortest."""
+    then the oracle on the two shortest, a middle and the longest sequence."""
     lc, h = layer_consts()
     rng = np.random.default_rng(44)
     lens = rng.integers(1024, 16385, 32)
@@ -122,7 +122,9 @@ def test_batched_c4_ragged_32(device):
     ops.attn_step_batched(seqs, cents, H_q=H_Q, H_kv=H_KV, scale=SCALE)
     torch.cuda.synchronize()
     assert all(torch.equal(a, s["out"]) for a, s in zip(first, seqs))
-    for i in np.argsort(lens)[:2]:
+    # the oracle directly on the two shortest, a middle and the longest sequence
+    order = np.argsort(lens)
+    for i in (order[0], order[1], order[len(order) // 2], order[-1]):
         s = seqs[int(i)]
         rows = {k: getattr(s["pay"], k).cpu().numpy() for k in
                 ("kmask", "kpay", "knorm", "krn", "vpay", "vnorm", "vrn", "vsm")}
