@@ -522,10 +522,17 @@ __device__ __forceinline__ f32x16 mfma3232(h8 a, h8 b, f32x16 c) {
 constexpr int KS2_LD = 256 + 8;   // halves per LDS K row
 constexpr int VS2_LD = KT + 4;    // halves per LDS V^T row
 
+// Pipelined over tiles: K / V^T tiles in a three-slot LDS ring, and the
+// scores of tile t + 1 are computed on the matrix cores while the vector ALU
+// does the softmax of tile t (MFMA and VALU instructions interleaved in issue
+// order, so the one wavefront per SIMD keeps both units busy).
+constexpr int NKB = 3;            // LDS tile slots
+// Lazy-rescale gap of the 32-row form: weights stay <= e^10 (< fp16 max).
+constexpr float GAP32 = 10.0f;
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void prefill_attn32_kernel(PrefillArgs a) {
-    __shared__ __align__(16) _Float16 ks[2][KT][KS2_LD];
-    __shared__ __align__(16) _Float16 vs[2][256][VS2_LD];
+    __shared__ __align__(16) _Float16 ks[NKB][KT][KS2_LD];
+    __shared__ __align__(16) _Float16 vs[NKB][256][VS2_LD];
     const int h = blockIdx.y;
     const int tid = threadIdx.x;
     const int wv = tid >> 6, lane = tid & 63;
@@ -586,74 +593,111 @@ void prefill_attn32_kernel(PrefillArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             *reinterpret_cast<uint4*>(&ks[buf][ld_key][ld_off + 8 * i]) = pk[i];
-            uint4 v = pv[i];
-            if (nv < KT)
-                v = uint4{vmask(v.x, 4 * i, nv), vmask(v.y, 4 * i + 1, nv), vmask(v.z, 4 * i + 2, nv),
-                          vmask(v.w, 4 * i + 3, nv)};
-            *reinterpret_cast<uint2*>(&vs[buf][tid][8 * i]) = uint2{v.x, v.y};
-            *reinterpret_cast<uint2*>(&vs[buf][tid][8 * i + 4]) = uint2{v.z, v.w};
+            *reinterpret_cast<uint2*>(&vs[buf][tid][8 * i]) = uint2{pv[i].x, pv[i].y};
+            *reinterpret_cast<uint2*>(&vs[buf][tid][8 * i + 4]) = uint2{pv[i].z, pv[i].w};
         }
+        if (nv < KT) {  // the key space's last tile: V^T columns past n_tot cleared (uniform branch)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint4 v = pv[i];
+                *reinterpret_cast<uint2*>(&vs[buf][tid][8 * i]) =
+                    uint2{vmask(v.x, 4 * i, nv), vmask(v.y, 4 * i + 1, nv)};
+                *reinterpret_cast<uint2*>(&vs[buf][tid][8 * i + 4]) =
+                    uint2{vmask(v.z, 4 * i + 2, nv), vmask(v.w, 4 * i + 3, nv)};
+            }
+        }
+    };
+    // S^T of the tile in slot buf: 16 MFMAs in two accumulation chains
+    auto kread = [&](int buf, int half, h8 (&kop)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            kop[i] = *reinterpret_cast<const h8*>(&ks[buf][ln][16 * (8 * half + i) + 8 * hh]);
     };
 
     const int n_tiles = k_lo < kt_hi ? (kt_hi - k_lo + KT - 1) / KT : 0;
     if (n_tiles > 0) {
         gload(k_lo);
         lstore(0, k_lo);
-        if (n_tiles > 1) gload(k_lo + KT);
     }
+    if (n_tiles > 1) {
+        gload(k_lo + KT);
+        lstore(1, k_lo + KT);
+    }
+    if (n_tiles > 2) gload(k_lo + 2 * KT);
     __syncthreads();
-    for (int t = 0; t < n_tiles; t++) {
-        const int buf = t & 1;
-        const int k0 = k_lo + t * KT;
-        // ---- the tile's K operand reads first, then S^T (32 keys x 32 rows)
-        // in four accumulation chains
-        f32x16 sc4[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) sc4[c][e] = 0.0f;
+    const f32x16 zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    f32x16 s2[2];
+    {
+        h8 kop[8];
+        s2[0] = s2[1] = zero16;
 #pragma unroll
         for (int half = 0; half < 2; half++) {
-            h8 kop[8];
+            kread(0, half, kop);
 #pragma unroll
-            for (int i = 0; i < 8; i++)
-                kop[i] = *reinterpret_cast<const h8*>(&ks[buf][ln][16 * (8 * half + i) + 8 * hh]);
-#pragma unroll
-            for (int i = 0; i < 8; i++) sc4[i & 3] = mfma3232(kop[i], qb[8 * half + i], sc4[i & 3]);
+            for (int i = 0; i < 8; i++) s2[i & 1] = mfma3232(kop[i], qb[8 * half + i], s2[i & 1]);
         }
-        float sc[16], lmax = -INFINITY;
-        const uint32_t mb = vis.tile(k0) >> (4 * hh);
+    }
+    for (int t = 0; t < n_tiles; t++) {
+        const int cur = t % NKB, nxt = (t + 1) % NKB;
+        const int k0 = k_lo + t * KT;
+        // ---- the scores of tile t out of the accumulators, whose registers
+        // then take tile t + 1 (on the last tile: a slot's stale data, unused)
+        float sc[16];
 #pragma unroll
-        for (int e = 0; e < 16; e++) {  // key k0 + 8 (e / 4) + 4 hh + e % 4
-            const float x = (sc4[0][e] + sc4[1][e]) + (sc4[2][e] + sc4[3][e]);
-            sc[e] = (mb >> (8 * (e >> 2) + (e & 3))) & 1u ? x * a.sc : -INFINITY;
-            lmax = fmaxf(lmax, sc[e]);
+        for (int e = 0; e < 16; e++) sc[e] = s2[0][e] + s2[1][e];
+        h8 kop[8];
+        kread(nxt, 0, kop);
+        // ---- S(t + 1), first half, under the mask and row maximum of tile t
+        float lmax = -INFINITY;
+        {
+            const uint32_t mb = vis.tile(k0) >> (4 * hh);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                s2[i & 1] = mfma3232(kop[i], qb[i], i < 2 ? zero16 : s2[i & 1]);
+#pragma unroll
+                for (int e = 2 * i; e < 2 * i + 2; e++) {  // key k0 + 8 (e / 4) + 4 hh + e % 4
+                    sc[e] = (mb >> (8 * (e >> 2) + (e & 3))) & 1u ? sc[e] * a.sc : -INFINITY;
+                    lmax = fmaxf(lmax, sc[e]);
+                }
+            }
         }
+        kread(nxt, 1, kop);
         // ---- raise the row's reference maximum only when needed (the row's
         // keys sit in lanes l and l ^ 32)
-        if (__ballot(lmax > m_ref + GAP) != 0ull) {
+        if (__ballot(lmax > m_ref + GAP32) != 0ull) {
             const float rmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
             const float m_new = fmaxf(m_ref, rmax);
             if (m_new > m_ref) {
-                const float fac = __expf(m_ref - m_new);  // 0 when m_ref = -inf
+                // before the first visible key every accumulator is still zero
+                if (__ballot(m_ref != -INFINITY) != 0ull) {
+                    const float fac = __expf(m_ref - m_new);  // 0 when m_ref = -inf
 #pragma unroll
-                for (int t2 = 0; t2 < 8; t2++) acc[t2] *= fac;
-                l_part *= fac;
+                    for (int t2 = 0; t2 < 8; t2++) acc[t2] *= fac;
+                    l_part *= fac;
+                }
                 m_ref = m_new;
             }
         }
+        // ---- S(t + 1), second half, under the weights of tile t
         h8 pb[2];
-#pragma unroll
-        for (int sp = 0; sp < 2; sp++) {
-            float p[8];
+        {
+            float p[16];
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                const float x = sc[8 * sp + i];
-                p[i] = x == -INFINITY ? 0.0f : __expf(x - m_ref);
-                l_part += p[i];
+                s2[i & 1] = mfma3232(kop[i], qb[8 + i], s2[i & 1]);
+#pragma unroll
+                for (int e = 2 * i; e < 2 * i + 2; e++) {
+                    const float x = sc[e];
+                    p[e] = x == -INFINITY ? 0.0f : __expf(x - m_ref);
+                    l_part += p[e];
+                }
             }
-            pb[sp] = __builtin_bit_cast(h8, uint4{pk_rne(p[0], p[1]), pk_rne(p[2], p[3]),
-                                                  pk_rne(p[4], p[5]), pk_rne(p[6], p[7])});
+#pragma unroll
+            for (int sp = 0; sp < 2; sp++)
+                pb[sp] = __builtin_bit_cast(h8, uint4{pk_rne(p[8 * sp], p[8 * sp + 1]),
+                                                      pk_rne(p[8 * sp + 2], p[8 * sp + 3]),
+                                                      pk_rne(p[8 * sp + 4], p[8 * sp + 5]),
+                                                      pk_rne(p[8 * sp + 6], p[8 * sp + 7])});
         }
         // ---- O^T += V^T P^T: 8 tiles of 32 dims x 2 K-steps of 16 keys; each
         // K-step's 8 operand reads issued before its MFMAs
@@ -662,17 +706,17 @@ void prefill_attn32_kernel(PrefillArgs a) {
             h8 vop[8];
 #pragma unroll
             for (int t2 = 0; t2 < 8; t2++) {
-                const uint2 va = *reinterpret_cast<const uint2*>(&vs[buf][32 * t2 + ln][16 * sp + 4 * hh]);
-                const uint2 vb = *reinterpret_cast<const uint2*>(&vs[buf][32 * t2 + ln][16 * sp + 8 + 4 * hh]);
+                const uint2 va = *reinterpret_cast<const uint2*>(&vs[cur][32 * t2 + ln][16 * sp + 4 * hh]);
+                const uint2 vb = *reinterpret_cast<const uint2*>(&vs[cur][32 * t2 + ln][16 * sp + 8 + 4 * hh]);
                 vop[t2] = __builtin_bit_cast(h8, uint4{va.x, va.y, vb.x, vb.y});
             }
 #pragma unroll
             for (int t2 = 0; t2 < 8; t2++) acc[t2] = mfma3232(vop[t2], pb[sp], acc[t2]);
         }
-        // ---- stage the next tile, load the one after
-        if (t + 1 < n_tiles) {
-            lstore(buf ^ 1, k0 + KT);
-            if (t + 2 < n_tiles) gload(k0 + 2 * KT);
+        // ---- stage tile t + 2 (its slot last held tile t - 1), load t + 3
+        if (t + 2 < n_tiles) {
+            lstore((t + 2) % NKB, k0 + 2 * KT);
+            if (t + 3 < n_tiles) gload(k0 + 3 * KT);
         }
         __syncthreads();
     }
