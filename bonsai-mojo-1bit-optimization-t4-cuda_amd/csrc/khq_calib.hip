@@ -1415,4 +1415,36 @@ int launch_cal_svq_train(const void* v, const void* attn, const void* init_cb, c
     return (int)hipStreamSynchronize(st);
 }
 
+int launch_cal_svq_pass(const void* v, const void* attn, const void* cb, const void* wa,
+                        const void* wb, const void* rp, void* out_grad, void* out_loss, int N,
+                        int T, int H_q, int H_kv, float temp, hipStream_t st) {
+    if (!v || !cb || !wa || !wb || !rp || !out_grad || !out_loss || N <= 0 || !(temp > 0.0f))
+        return -100;
+    if (attn && (T <= 0 || H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || (long)H_kv * T != N))
+        return -100;
+    Svq t{static_cast<const float*>(v), static_cast<const float*>(attn),
+          static_cast<const float*>(rp), N, T, H_q, H_kv, st};
+    int rc = t.init();
+    if (rc) return rc;
+    Seed s;
+    CAL_TRY(s.cb.alloc(CB * 4));
+    CAL_TRY(s.wa.alloc(2048 * 4));
+    CAL_TRY(s.wb.alloc(2048 * 4));
+    CAL_TRY(hipMemcpyAsync(s.cb.p, cb, CB * 4, hipMemcpyDeviceToDevice, st));
+    CAL_TRY(hipMemcpyAsync(s.wa.p, wa, 2048 * 4, hipMemcpyDeviceToDevice, st));
+    CAL_TRY(hipMemcpyAsync(s.wb.p, wb, 2048 * 4, hipMemcpyDeviceToDevice, st));
+    // without the attention loss the pass leaves the transform gradients alone
+    CAL_TRY(hipMemsetAsync(t.gwa.p, 0, 2048 * 4, st));
+    CAL_TRY(hipMemsetAsync(t.gwb.p, 0, 2048 * 4, st));
+    double l[2];
+    if ((rc = t.pass(s, temp, true, l))) return rc;
+    float* g = static_cast<float*>(out_grad);
+    CAL_TRY(hipMemcpyAsync(g, t.gcb.p, CB * 4, hipMemcpyDeviceToDevice, st));
+    CAL_TRY(hipMemcpyAsync(g + CB, t.gwa.p, 2048 * 4, hipMemcpyDeviceToDevice, st));
+    CAL_TRY(hipMemcpyAsync(g + CB + 2048, t.gwb.p, 2048 * 4, hipMemcpyDeviceToDevice, st));
+    const float lf[2] = {(float)l[0], (float)l[1]};
+    CAL_TRY(hipMemcpyAsync(out_loss, lf, sizeof(lf), hipMemcpyHostToDevice, st));
+    return (int)hipStreamSynchronize(st);
+}
+
 }  // extern "C"

@@ -62,6 +62,7 @@ SIGNATURES = {
     # calibration
     "launch_cal_op": [I] + [P] * 7 + [F, F, I, I, I, I, P],
     "launch_cal_svq_train": [P] * 6 + [I, I, I, I, I, I, F, P],
+    "launch_cal_svq_pass": [P] * 8 + [I, I, I, I, F, P],
     "khq_layer_attention_step": [P] * 6 + [F, I, P, F, P],
 }
 # return types other than int

@@ -56,6 +56,16 @@ def svq_train(v, attn, init_cb, rp, out_cb, *, N, T, H_q, H_kv, iterations=SVQ_I
         raise _lib.KhqError("launch_cal_svq_train", rc)
 
 
+def svq_pass(v, attn, cb, wa, wb, rp, out_grad, out_loss, *, N, T, H_q, H_kv, temp,
+             stream=None):
+    """launch_cal_svq_pass: one SmartVQ forward + backward (for tests)."""
+    rc = _lib.lib().launch_cal_svq_pass(_p(v), _p(attn), _p(cb), _p(wa), _p(wb), _p(rp),
+                                        _p(out_grad), _p(out_loss), N, T, H_q, H_kv, temp,
+                                        _lib.stream_handle(stream))
+    if rc:
+        raise _lib.KhqError("launch_cal_svq_pass", rc)
+
+
 def calibrate_layer(layer_id: int, k: np.ndarray, v: np.ndarray, attn: np.ndarray | None,
                     *, device="cuda", iterations=SVQ_ITERS, log=print) -> C.LayerCentroids:
     """One layer from its dumped rows k, v f32 [n_tokens][H_kv * 256] and the

@@ -368,6 +368,17 @@ int launch_cal_svq_train(const void* v, const void* attn, const void* init_cb, c
                          void* out_cb, void* out_wtrm, int N, int T, int H_q, int H_kv,
                          int iterations, int n_seeds, float lr, hipStream_t stream);
 
+/* One SmartVQ pass (no counterpart in the reference: it exposes, for tests,
+ * the step that launch_cal_svq_train repeats, ref .cu:2470-2530): forward and
+ * gradients at codebook cb f32 [64][256][3] and transform factors wa f32
+ * [256][8], wb f32 [8][256], temperature temp.  out_grad f32 [49152 + 2048 +
+ * 2048] = d/d cb, d/d wa, d/d wb (the straight-through codebook gradient;
+ * zero transform gradients without attn); out_loss f32 [2] = reconstruction
+ * and dict losses.  Other arguments as launch_cal_svq_train.  Synchronous. */
+int launch_cal_svq_pass(const void* v, const void* attn, const void* cb, const void* wa,
+                        const void* wb, const void* rp, void* out_grad, void* out_loss, int N,
+                        int T, int H_q, int H_kv, float temp, hipStream_t stream);
+
 /* Attaches a dump recorder to a layer (NULL detaches): its
  * khq_layer_attention_step then records the token under `layer_id`
  * (ref attention.mojo:340-341, 355-356).  The recorder is not owned. */

@@ -1,13 +1,15 @@
 """CPU restatement of the KHQ calibration steps (test infrastructure only).
 
-numpy versions of launch_cal_op ops 1-7 and 10 and of the SmartK / SmartV
-round trips (ref:src/csrc/qmv_sm75_kernel.cu:2019-2085, 2645-2681,
-2722-3025, 3071-3349, 4598-4810), written from the reference's algorithm in
-float64 so they can check the GPU steps (tests/test_gpu_calib.py); each is
-itself pinned in tests/test_calib_ref.py against closed forms (explicit
-Hadamard matrix, numpy eigh, SVD polar factor, Lloyd fixed points, the
-independent format decoders of tests/npref.py).  Nothing in the product
-imports this file.
+numpy versions of launch_cal_op ops 1-7 and 10, of the SmartK / SmartV
+round trips and of the SmartVQ trainer (ref:src/csrc/qmv_sm75_kernel.cu:
+2019-2085, 2089-2600, 2645-2681, 2722-3025, 3071-3349, 4434-4810), written
+from the reference's algorithm in float64 so they can check the GPU steps
+(tests/test_gpu_calib.py); each is itself pinned in tests/test_calib_ref.py
+against closed forms (explicit Hadamard matrix, numpy eigh, SVD polar
+factor, Lloyd fixed points, the independent format decoders of
+tests/npref.py, central differences of the SmartVQ loss and of its
+straight-through surrogate, Adam's closed-form first steps).  Nothing in the
+product imports this file.
 """
 from __future__ import annotations
 
@@ -233,3 +235,182 @@ def tournament(x32, x16, d, rp, cents, ts0, vq=None):
         if best[k][3] < w[3]:
             w = best[k]
     return w[1], w[0]
+
+
+# ------------------------------------------------------------------ SmartVQ
+# The reference's SmartVQ trainer (ref:src/csrc/qmv_sm75_kernel.cu:2089-2600
+# kernels and schedule, :4434-4596 driver), restated in float64: a straight-
+# through VQ (hard nearest codeword forward, softmax(-dist / temp) weights
+# backward), a rank-8 output transform W = I + A B, Adam with bias correction,
+# best-state tracking, patience 15 with rate halving and warm restarts, three
+# seeds with an attention-MSE proxy tournament.
+
+def invrotate(x, rp):
+    """dst[n][4p + c] = sum_k src[n][4p + k] rp[16p + 4c + k] (.cu:2159-2172)."""
+    r = np.asarray(rp, np.float64).reshape(NP, 4, 4)
+    return np.einsum("npk,pck->npc", np.asarray(x, np.float64).reshape(-1, NP, 4), r).reshape(-1, D)
+
+
+def svq_noise(base, seed, scale):
+    """base + N(0, 1) scale, one Box-Muller draw per entry from a xorshift
+    stream seeded with seed ^ (i 747796405 + 2891336453) (.cu:2387-2401)."""
+    base = np.asarray(base, np.float64).ravel()
+    i = np.arange(base.size, dtype=np.uint64)
+    s = (np.uint64(seed) ^ ((i * np.uint64(747796405) + np.uint64(2891336453)) & np.uint64(0xFFFFFFFF)))
+    s = s & np.uint64(0xFFFFFFFF)
+
+    def xs(s):
+        s = (s ^ (s << np.uint64(13))) & np.uint64(0xFFFFFFFF)
+        s = s ^ (s >> np.uint64(17))
+        return (s ^ (s << np.uint64(5))) & np.uint64(0xFFFFFFFF)
+
+    s = xs(s)
+    u1 = (s & np.uint64(0xFFFFFF)).astype(np.float64) / 16777216.0 + 1e-7
+    s = xs(s)
+    u2 = (s & np.uint64(0xFFFFFF)).astype(np.float64) / 16777216.0
+    return base + np.sqrt(-2.0 * np.log(u1)) * np.cos(6.2831853 * u2) * scale
+
+
+def svq_schedule(i, total, lr, lr_mult=1.0):
+    """Temperature 1.5 -> 0.1 geometric over steps 0 .. total - 1 and the
+    codebook rate, decaying linearly to a floor of 10 % (.cu:2478-2482)."""
+    max_it = max(1, total - 1)
+    temp = 1.5 * np.exp((np.log(0.1) - np.log(1.5)) * i / max_it)
+    return temp, lr * max(0.1, 1.0 - i / total) * lr_mult
+
+
+def svq_pass(v, attn, cb, wa, wb, rp, T, H_q, H_kv, temp, grad=True, extras=False):
+    """One forward (+ backward) pass (.cu:2436-2530).  v f [N][256], attn
+    [H_q][T][T] or None, cb [64][256][3], wa [256][8], wb [8][256].  Returns
+    (recon loss, dict loss, gcb, gwa, gwb) (gradients None without grad), and
+    with extras a dict of the intermediates (rot, idx, recf, grec, gq)."""
+    v = np.asarray(v, np.float64)
+    cb = np.asarray(cb, np.float64).reshape(NP, 256, 3)
+    wa = np.asarray(wa, np.float64).reshape(D, 8)
+    wb = np.asarray(wb, np.float64).reshape(8, D)
+    N = v.shape[0]
+    rot = rotate(v, rp).reshape(N, NP, 4)
+    v3 = rot[:, :, :3]
+    dist = ((v3[:, :, None, :] - cb[None]) ** 2).sum(-1)  # [N][64][256]
+    idx = dist.argmin(-1)  # first minimum
+    rec = rot.copy()
+    rec[:, :, :3] = np.take_along_axis(cb[None], idx[:, :, None, None].repeat(3, -1), 2)[:, :, 0]
+    dict_loss = np.take_along_axis(dist, idx[..., None], -1).sum() / (N * NP * 3)
+    # dim 3: round half to even of rot * 16, / 16 (.cu:2139-2155)
+    rec[:, :, 3] = np.rint(rot[:, :, 3] * 16.0) / 16.0
+    recf = invrotate(rec, rp)
+    if attn is not None:
+        attn = np.asarray(attn, np.float64)
+        n_rep = H_q // H_kv
+        dlt = recf + (recf @ wa) @ wb - v
+        y = np.stack([attn[h] @ dlt[(h // n_rep) * T:(h // n_rep + 1) * T] for h in range(H_q)])
+        recon = (y ** 2).mean()
+    else:
+        recon = ((recf - v) ** 2).mean()
+    if not grad:
+        return recon, dict_loss, None, None, None
+    if attn is not None:
+        g = 2.0 / y.size
+        gdl = np.zeros_like(dlt)
+        for h in range(H_q):
+            kv = h // n_rep
+            gdl[kv * T:(kv + 1) * T] += g * attn[h].T @ y[h]
+        grec = gdl + (gdl @ wb.T) @ wa.T
+        gW = recf.T @ gdl
+        gwa, gwb = gW @ wb.T, wa.T @ gW
+    else:
+        grec = 2.0 * (recf - v) / recf.size
+        gwa, gwb = np.zeros_like(wa), np.zeros_like(wb)
+    # rotation backward over the first three rotated dims only (the
+    # reference drops d = 3, .cu:2300-2314)
+    r = np.asarray(rp, np.float64).reshape(NP, 4, 4)
+    gq = np.einsum("npd,pdc->npc", grec.reshape(N, NP, 4)[:, :, :3], r[:, :3, :3])
+    z = -dist / temp
+    w = np.exp(z - z.max(-1, keepdims=True))
+    w /= w.sum(-1, keepdims=True)
+    gk = np.einsum("npc,pkc->npk", gq, cb)  # gq . c_k
+    swg = (w * gk).sum(-1)
+    gd = -(w * (gk - swg[..., None])) / temp
+    gcb = np.einsum("npk,npc->pkc", w, gq) + 2.0 * np.einsum(
+        "npk,npkc->pkc", gd, cb[None] - v3[:, :, None, :])
+    dn = 2.0 / (N * NP * 3)
+    hard = np.zeros_like(dist)
+    np.put_along_axis(hard, idx[..., None], 1.0, -1)
+    gcb += dn * np.einsum("npk,npkc->pkc", hard, cb[None] - v3[:, :, None, :])
+    if extras:
+        return recon, dict_loss, gcb, gwa, gwb, dict(rot=rot, idx=idx, recf=recf, grec=grec, gq=gq)
+    return recon, dict_loss, gcb, gwa, gwb
+
+
+def _adam(p, g, m, s, lr, bc1, bc2):
+    m[:] = 0.9 * m + 0.1 * g
+    s[:] = 0.999 * s + 0.001 * g * g
+    p -= lr * (m / bc1) / (np.sqrt(s / bc2) + 1e-8)
+
+
+def svq_train(v, attn, init_cb, rp, T, H_q, H_kv, iterations, n_seeds, lr):
+    """The trainer (.cu:4434-4596): returns (codebook [64][256][3], W)."""
+    n_seeds = max(1, min(3, n_seeds))
+    seeds = [42, 137, 271]
+    st = []
+    for sd in seeds[:n_seeds]:
+        s = dict(cb=np.asarray(init_cb, np.float64).reshape(NP, 256, 3).copy(),
+                 wa=svq_noise(np.zeros(2048), (sd * 2654435761 + 1) & 0xFFFFFFFF, 1.0 / 16.0).reshape(D, 8),
+                 wb=np.zeros((8, D)), step=0, lr_mult=1.0, stagnant=0, seed=sd)
+        for k in ("cb", "wa", "wb"):
+            s["m" + k], s["v" + k] = np.zeros_like(s[k]), np.zeros_like(s[k])
+        l0, l1, *_ = svq_pass(v, attn, s["cb"], s["wa"], s["wb"], rp, T, H_q, H_kv, 1.5, False)
+        s["best"] = l0 + l1
+        s["bcb"], s["bwa"], s["bwb"] = s["cb"].copy(), s["wa"].copy(), s["wb"].copy()
+        st.append(s)
+
+    def run(s, iters, start):
+        total = start + iters
+        max_it = max(1, total - 1)
+        for i in range(start, total):
+            temp, cur = svq_schedule(i, total, lr, s["lr_mult"])
+            l0, l1, gcb, gwa, gwb = svq_pass(v, attn, s["cb"], s["wa"], s["wb"], rp, T, H_q, H_kv, temp)
+            s["step"] += 1
+            bc1, bc2 = 1.0 - 0.9 ** s["step"], 1.0 - 0.999 ** s["step"]
+            _adam(s["cb"], gcb, s["mcb"], s["vcb"], cur, bc1, bc2)
+            _adam(s["wa"], gwa, s["mwa"], s["vwa"], cur * 0.05, bc1, bc2)
+            _adam(s["wb"], gwb, s["mwb"], s["vwb"], cur * 0.05, bc1, bc2)
+            loss = l0 + l1  # this step's forward, before the update
+            if loss < s["best"] - 1e-7:
+                s["best"] = loss
+                s["bcb"], s["bwa"], s["bwb"] = s["cb"].copy(), s["wa"].copy(), s["wb"].copy()
+                s["stagnant"] = 0
+            else:
+                s["stagnant"] += 1
+            if s["stagnant"] >= 15:
+                if s["lr_mult"] > 0.1:
+                    s["lr_mult"] *= 0.5
+                else:
+                    s["lr_mult"] = 3.0
+                    ns = 1e-3 * np.exp(np.log(0.01) * i / max_it)
+                    s["cb"] = svq_noise(s["bcb"], (s["seed"] ^ i) & 0xFFFFFFFF, ns).reshape(NP, 256, 3)
+                    s["wa"], s["wb"] = s["bwa"].copy(), s["bwb"].copy()
+                s["stagnant"] = 0
+
+    def proxy(s):
+        l0, *_ = svq_pass(v, attn, s["cb"], s["wa"], s["wb"], rp, T, H_q, H_kv, 0.05, False)
+        return l0
+
+    r1 = min(iterations, 30)
+    r2 = iterations - r1
+    prox = []
+    for s in st:
+        run(s, r1, 0)
+        s["cb"], s["wa"], s["wb"] = s["bcb"].copy(), s["bwa"].copy(), s["bwb"].copy()
+        prox.append(proxy(s))
+    order = sorted(range(n_seeds), key=lambda i: prox[i])
+    if r2 > 0:
+        for k in order:
+            run(st[k], r2, r1)
+            prox[k] = proxy(st[k])
+    win = order[0]
+    for k in order:
+        if prox[k] < prox[win]:
+            win = k
+    w = st[win]
+    return w["bcb"], np.eye(D) + w["bwa"] @ w["bwb"]

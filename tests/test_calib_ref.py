@@ -160,3 +160,174 @@ def test_roundtrip_k_matches_the_independent_decoder():
     got16 = R.roundtrip_k(proj, R.f16(norms), R.f16(cents), rp, d, alpha=0.9)
     np.testing.assert_allclose(got16, want, rtol=1e-6, atol=1e-9)
     assert np.abs(got - want).max() < 1e-2 * np.abs(want).max()
+
+
+# ---------------------------------------------------------------- SmartVQ
+def _svq_small(seed=0, T=8, H_kv=2, H_q=4, temp=0.05):
+    rng = np.random.default_rng(seed)
+    N = T * H_kv
+    v = rng.standard_normal((N, 256)) * 0.06
+    rp = np.stack([np.linalg.qr(rng.standard_normal((4, 4)))[0] for _ in range(64)]).reshape(64, 16)
+    cb = rng.standard_normal((64, 256, 3)) * 0.06
+    wa = rng.standard_normal((256, 8)) / 16.0
+    wb = rng.standard_normal((8, 256)) / 16.0
+    s = rng.standard_normal((H_q, T, T))
+    attn = np.exp(s - s.max(-1, keepdims=True))
+    attn /= attn.sum(-1, keepdims=True)
+    return dict(v=v, rp=rp, cb=cb, wa=wa, wb=wb, attn=attn, T=T, H_q=H_q, H_kv=H_kv, temp=temp)
+
+
+def _loss_of_recf(c, recf):
+    """The reconstruction loss as a function of the inverse-rotated
+    reconstruction (attention mode: through W = I + A B and the scores)."""
+    v = c["v"]
+    if c["attn"] is None:
+        return ((recf - v) ** 2).mean()
+    dlt = recf + (recf @ c["wa"]) @ c["wb"] - v
+    n_rep = c["H_q"] // c["H_kv"]
+    T = c["T"]
+    y = np.stack([c["attn"][h] @ dlt[(h // n_rep) * T:(h // n_rep + 1) * T] for h in range(c["H_q"])])
+    return (y ** 2).mean()
+
+
+def _fd(f, x, idx, eps=1e-6):
+    out = []
+    for i in idx:
+        xp, xm = x.copy(), x.copy()
+        xp.flat[i] += eps
+        xm.flat[i] -= eps
+        out.append((f(xp) - f(xm)) / (2 * eps))
+    return np.array(out)
+
+
+def test_svq_recon_gradient_is_the_loss_gradient():
+    """grec = d loss / d recf, by central differences, in both modes."""
+    for attn in (True, False):
+        c = _svq_small(seed=1)
+        if not attn:
+            c["attn"] = None
+        *_, ex = R.svq_pass(c["v"], c["attn"], c["cb"], c["wa"], c["wb"], c["rp"], c["T"],
+                            c["H_q"], c["H_kv"], c["temp"], extras=True)
+        idx = np.random.default_rng(2).choice(ex["recf"].size, 40, replace=False)
+        fd = _fd(lambda r: _loss_of_recf(c, r), ex["recf"], idx)
+        np.testing.assert_allclose(ex["grec"].flat[idx], fd, rtol=1e-5, atol=1e-12)
+
+
+def test_svq_rotation_backward_drops_rotated_dim_3():
+    """gq is d loss / d rec[p][0..2] of a forward whose inverse rotation
+    leaves its output component 3 fixed (the reference sums d < 3 only)."""
+    c = _svq_small(seed=3)
+    *_, ex = R.svq_pass(c["v"], c["attn"], c["cb"], c["wa"], c["wb"], c["rp"], c["T"],
+                        c["H_q"], c["H_kv"], c["temp"], extras=True)
+    N = c["v"].shape[0]
+    rec = np.einsum("npc,pck->npk", ex["recf"].reshape(N, 64, 4),
+                    np.asarray(c["rp"]).reshape(64, 4, 4))  # back to the rotated domain
+    fixed3 = ex["recf"].reshape(N, 64, 4)[:, :, 3].copy()
+
+    def f(r3):
+        r = rec.copy()
+        r[:, :, :3] = r3.reshape(N, 64, 3)
+        recf = R.invrotate(r, c["rp"]).reshape(N, 64, 4)
+        recf[:, :, 3] = fixed3
+        return _loss_of_recf(c, recf.reshape(N, 256))
+
+    r3 = rec[:, :, :3].copy()
+    idx = np.random.default_rng(4).choice(r3.size, 40, replace=False)
+    np.testing.assert_allclose(ex["gq"].flat[idx], _fd(f, r3, idx), rtol=1e-5, atol=1e-12)
+
+
+def test_svq_codebook_gradient_is_the_straight_through_surrogate():
+    """gcb = d/dC of sum gq . (sum_k softmax(-|v - c_k|^2 / temp) c_k) plus
+    the dict term at the fixed hard codewords, gq held fixed."""
+    c = _svq_small(seed=5, temp=0.02)
+    _, _, gcb, _, _, ex = R.svq_pass(c["v"], c["attn"], c["cb"], c["wa"], c["wb"], c["rp"],
+                                     c["T"], c["H_q"], c["H_kv"], c["temp"], extras=True)
+    N = c["v"].shape[0]
+    v3 = ex["rot"][:, :, :3]
+    gq, hard, temp = ex["gq"], ex["idx"], c["temp"]
+
+    def S(cb):
+        cb = cb.reshape(64, 256, 3)
+        dist = ((v3[:, :, None, :] - cb[None]) ** 2).sum(-1)
+        z = -dist / temp
+        w = np.exp(z - z.max(-1, keepdims=True))
+        w /= w.sum(-1, keepdims=True)
+        soft = np.einsum("npk,pkc->npc", w, cb)
+        dict_fixed = np.take_along_axis(dist, hard[..., None], -1).sum() / (N * 64 * 3)
+        return (gq * soft).sum() + dict_fixed
+
+    cb = c["cb"].copy()
+    rng = np.random.default_rng(6)
+    # the hard codewords (largest terms) and random entries
+    p = rng.integers(0, 64, 20)
+    n = rng.integers(0, N, 20)
+    idx = list((p * 256 + hard[n, p]) * 3 + rng.integers(0, 3, 20)) + list(rng.choice(cb.size, 40))
+    np.testing.assert_allclose(gcb.flat[idx], _fd(S, cb, idx, eps=1e-7), rtol=2e-4,
+                               atol=1e-6 * np.abs(gcb).max())
+
+
+def test_svq_transform_gradients_are_the_loss_gradients():
+    c = _svq_small(seed=7)
+    _, _, _, gwa, gwb = R.svq_pass(c["v"], c["attn"], c["cb"], c["wa"], c["wb"], c["rp"],
+                                   c["T"], c["H_q"], c["H_kv"], c["temp"])
+
+    def loss(key):
+        def f(x):
+            cc = dict(c)
+            cc[key] = x
+            return R.svq_pass(cc["v"], cc["attn"], cc["cb"], cc["wa"], cc["wb"], cc["rp"], cc["T"],
+                              cc["H_q"], cc["H_kv"], cc["temp"], grad=False)[0]
+        return f
+
+    rng = np.random.default_rng(8)
+    for key, g in (("wa", gwa), ("wb", gwb)):
+        idx = rng.choice(g.size, 20, replace=False)
+        np.testing.assert_allclose(g.flat[idx], _fd(loss(key), c[key], idx), rtol=1e-5, atol=1e-12)
+
+
+def test_svq_adam_steps_closed_form():
+    """From zero state the bias-corrected Adam step is lr g / (|g| + 1e-8),
+    and again for a repeated gradient."""
+    g = np.array([3e-3, -2e-5, 1e-9, 0.0, -4.0])
+    p, m, s = np.zeros(5), np.zeros(5), np.zeros(5)
+    R._adam(p, g, m, s, 0.1, 1 - 0.9, 1 - 0.999)
+    np.testing.assert_allclose(p, -0.1 * g / (np.abs(g) + 1e-8), rtol=1e-9, atol=1e-15)
+    R._adam(p, g, m, s, 0.1, 1 - 0.9 ** 2, 1 - 0.999 ** 2)
+    np.testing.assert_allclose(p, -0.2 * g / (np.abs(g) + 1e-8), rtol=1e-9, atol=1e-15)
+
+
+def test_svq_noise_xorshift_and_moments():
+    seed = (42 * 2654435761 + 1) & 0xFFFFFFFF
+    got = R.svq_noise(np.zeros(5), seed, 1.0)
+    for i in range(5):
+        s = (seed ^ ((i * 747796405 + 2891336453) & 0xFFFFFFFF)) & 0xFFFFFFFF
+        st = []
+        for _ in range(2):
+            s ^= (s << 13) & 0xFFFFFFFF
+            s ^= s >> 17
+            s ^= (s << 5) & 0xFFFFFFFF
+            st.append(s)
+        u1 = (st[0] & 0xFFFFFF) / 16777216.0 + 1e-7
+        u2 = (st[1] & 0xFFFFFF) / 16777216.0
+        assert abs(got[i] - np.sqrt(-2 * np.log(u1)) * np.cos(6.2831853 * u2)) < 1e-12
+    big = R.svq_noise(np.zeros(200000), 7, 1.0)
+    assert abs(big.mean()) < 0.01 and abs(big.std() - 1.0) < 0.01
+
+
+def test_svq_schedule_endpoints():
+    assert R.svq_schedule(0, 60, 0.02) == (1.5, 0.02)
+    temp, lr = R.svq_schedule(59, 60, 0.02)
+    assert abs(temp - 0.1) < 1e-12 and abs(lr - 0.002) < 1e-12  # floor: 10 %
+    assert abs(R.svq_schedule(30, 60, 0.02, 0.5)[1] - 0.005) < 1e-12
+
+
+def test_svq_train_keeps_the_best_state():
+    """No rate: the state never moves, the loss never improves, so the
+    output is the initial codebook and W = I + A 0 = I; one step with a rate:
+    that step's (pre-update) loss equals the initial one, still no update."""
+    c = _svq_small(seed=9, T=8)
+    for lr, it in ((0.0, 20), (0.05, 1)):
+        cb, W = R.svq_train(c["v"], c["attn"], c["cb"], c["rp"], c["T"], c["H_q"], c["H_kv"],
+                            iterations=it, n_seeds=2, lr=lr)
+        np.testing.assert_array_equal(cb, c["cb"])
+        np.testing.assert_array_equal(W, np.eye(256))

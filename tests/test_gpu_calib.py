@@ -183,6 +183,76 @@ def test_svq_train_attention_mode(device):
     assert _recon_mse(v, rp, cb) < 1.05 * _recon_mse(v, rp, init)
 
 
+def _svq_margin_case(T=32, H_kv=2, H_q=4, seed=21, shift=0.0):
+    """Rows whose rotated dims 0..2 sit near one codeword each (offsets well
+    inside half the codebook spacing), so the GPU and the float64
+    restatement pick the same hard codewords; with shift, the rows of each
+    codeword share an offset of that length (training has something to
+    improve)."""
+    rng = np.random.default_rng(seed)
+    N = T * H_kv
+    cb = (rng.standard_normal((64, 256, 3)) * 0.06).astype(np.float32)
+    rp = C.quaternion_rotors(rng).astype(np.float32)
+    k = rng.integers(0, 256, (N, 64))
+    off = rng.standard_normal((64, 256, 3))
+    off *= shift / np.linalg.norm(off, axis=-1, keepdims=True)
+    rot = np.empty((N, 64, 4))
+    rot[:, :, :3] = (cb[np.arange(64)[None, :], k] + off[np.arange(64)[None, :], k]
+                     + rng.standard_normal((N, 64, 3)) * 2e-4)
+    rot[:, :, 3] = rng.standard_normal((N, 64)) * 0.06
+    # rot[p][c] = sum_k v[p][k] rp[16 p + 4 k + c]: v = rot M^T for the orthogonal M
+    M = rp.astype(np.float64).reshape(64, 4, 4)
+    v = np.einsum("npc,pkc->npk", rot, M).reshape(N, 256).astype(np.float32)
+    s = rng.standard_normal((H_q, T, T)) + np.triu(np.full((T, T), -1e9), 1)[None]
+    attn = np.exp(s - s.max(-1, keepdims=True))
+    attn = (attn / attn.sum(-1, keepdims=True)).astype(np.float32)
+    return v, rp, cb, attn, N, T, H_q, H_kv
+
+
+@pytest.mark.parametrize("mode", ["attention", "reconstruction"])
+def test_svq_pass_vs_restatement(device, mode):
+    """One SmartVQ pass (launch_cal_svq_pass) against the float64
+    restatement: losses, the straight-through codebook gradient and the
+    transform gradients."""
+    v, rp, cb, attn, N, Tn, H_q, H_kv = _svq_margin_case()
+    if mode == "reconstruction":
+        attn = None
+    rng = np.random.default_rng(22)
+    wa = (rng.standard_normal((256, 8)) / 16).astype(np.float32)
+    wb = (rng.standard_normal((8, 256)) / 64).astype(np.float32)
+    g, l = new(49152 + 4096), new(2)
+    calib.svq_pass(T(v), None if attn is None else T(attn), T(cb), T(wa), T(wb), T(rp), g, l,
+                   N=N, T=Tn, H_q=H_q, H_kv=H_kv, temp=0.3)
+    rl, dl, gcb, gwa, gwb = R.svq_pass(v, attn, cb, wa, wb, rp, Tn, H_q, H_kv, 0.3)
+    got_l, got = l.cpu().numpy(), g.cpu().numpy()
+    np.testing.assert_allclose(got_l, [rl, dl], rtol=1e-4)
+    for a, w in ((got[:49152], gcb.ravel()), (got[49152:51200], gwa.ravel()),
+                 (got[51200:], gwb.ravel())):
+        np.testing.assert_allclose(a, w, rtol=1e-3, atol=1e-4 * max(np.abs(w).max(), 1e-30))
+
+
+def test_svq_train_vs_restatement(device):
+    """The whole trainer (3 seeds, Adam steps, best tracking, the proxy
+    tournament) against the float64 restatement; with no rate the output
+    is the initial codebook and W = I."""
+    v, rp, cb, attn, N, Tn, H_q, H_kv = _svq_margin_case(seed=23, shift=4e-3)
+    out, wt = new(64, 256, 3), new(256, 256)
+    for it, lr in ((6, 1e-3), (20, 0.0)):
+        calib.svq_train(T(v), T(attn), T(cb), T(rp), out, N=N, T=Tn, H_q=H_q, H_kv=H_kv,
+                        iterations=it, n_seeds=3, lr=lr, out_wtrm=wt)
+        want_cb, want_w = R.svq_train(v, attn, cb, rp, Tn, H_q, H_kv, iterations=it, n_seeds=3,
+                                      lr=lr)
+        got_cb, got_w = out.cpu().numpy(), wt.cpu().numpy()
+        print(f"SmartVQ {it} steps lr {lr}: max |cb - ref| {np.abs(got_cb - want_cb).max():.3e}, "
+              f"max |W - ref| {np.abs(got_w - want_w).max():.3e}")
+        np.testing.assert_allclose(got_cb, want_cb, atol=max(1e-3 * lr, 1e-7))
+        np.testing.assert_allclose(got_w, want_w, atol=max(1e-3 * lr, 1e-7))
+        if lr == 0.0:
+            np.testing.assert_array_equal(got_cb, cb)
+        else:  # the winner's best state moved away from the start
+            assert np.abs(want_cb - cb).max() > 0.5 * lr
+
+
 def _write_attn(path, H_q, n, H_kv, rng):
     with open(path, "wb") as f:
         import struct
