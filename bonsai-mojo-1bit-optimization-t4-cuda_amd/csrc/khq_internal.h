@@ -219,6 +219,11 @@ hipError_t launch_decompress(const DecompArgs& a, hipStream_t st);
 hipError_t launch_ring_gather(const GatherArgs& a, hipStream_t st);
 // A decode and a gather whose outputs are disjoint, in one launch.
 hipError_t launch_decompress_gather(const DecompArgs& d, const GatherArgs& g, hipStream_t st);
+// A compression event (k, v: rows (token, KV head) of the chunk), the decode
+// of those rows (d: tok0 = key0, n_tok tokens, start_pos 0) and an optional
+// independent gather (chunk append or raw copy) in one launch.
+hipError_t launch_compress_decode(const CompressJob& k, const CompressJob& v, const DecompArgs& d,
+                                  const GatherArgs* g, hipStream_t st);
 int prefill_splits(int n_q, int n_rep, int h_kv, int n_k, int* keys_per_split);
 hipError_t launch_prefill_attn(const PrefillArgs& a, hipStream_t st);
 // Prefill attention plus merge and gate through the shared workspace; the

@@ -70,19 +70,24 @@ bool alloc_zero(T** p, size_t bytes) {
 
 // Compression event: ring slots [boundary % 256, + 128) -> payload rows of
 // tokens [boundary, boundary + 128) (ref runtime.mojo:494-552).
-int compress_event(khq_layer* L, hipStream_t stream) {
+void compress_jobs(const khq_layer* L, khq::CompressJob* kj, khq::CompressJob* vj) {
     const int kv = L->H_kv * kD;
     const int s0 = L->boundary % kRing;
     const size_t r0 = (size_t)L->boundary * L->H_kv;
     const int n = kChunk * L->H_kv;
-    // K and V rows in one launch (the two jobs write disjoint outputs)
     auto h = [](const void* p) { return static_cast<const __half*>(p); };
-    khq::CompressJob kj{L->ring_u + (size_t)s0 * kv, h(L->d_k), h(L->rotor_k), h(L->cents_k), h(L->cents_k),
-                        L->kmask + r0 * 16, L->knorm + r0, L->krn + r0, L->kpay + r0 * 40,
-                        nullptr, n, L->ts_k, L->alpha_k};
-    khq::CompressJob vj{L->ring_v + (size_t)s0 * kv, h(L->d_v), h(L->rotor_v), h(L->cents_v), h(L->vq),
-                        L->kmask + r0 * 16, L->vnorm + r0, L->vrn + r0, L->vpay + r0 * 104,
-                        L->vsm + r0 * 4, n, L->ts_v, L->alpha_v};
+    *kj = khq::CompressJob{L->ring_u + (size_t)s0 * kv, h(L->d_k), h(L->rotor_k), h(L->cents_k),
+                           h(L->cents_k), L->kmask + r0 * 16, L->knorm + r0, L->krn + r0,
+                           L->kpay + r0 * 40, nullptr, n, L->ts_k, L->alpha_k};
+    *vj = khq::CompressJob{L->ring_v + (size_t)s0 * kv, h(L->d_v), h(L->rotor_v), h(L->cents_v),
+                           h(L->vq), L->kmask + r0 * 16, L->vnorm + r0, L->vrn + r0,
+                           L->vpay + r0 * 104, L->vsm + r0 * 4, n, L->ts_v, L->alpha_v};
+}
+
+int compress_event(khq_layer* L, hipStream_t stream) {
+    // K and V rows in one launch (the two jobs write disjoint outputs)
+    khq::CompressJob kj, vj;
+    compress_jobs(L, &kj, &vj);
     const hipError_t e = khq::launch_compress_pair(kj, vj, stream);
     if (e != hipSuccess) return (int)e;
     L->boundary += kChunk;
@@ -122,6 +127,25 @@ void decomp_args(const khq_layer* L, int d0, int nd, khq::DecompArgs* a) {
     a->a_k = L->alpha_k;
     a->a_v = L->alpha_v;
     a->rope_base = L->rope_base;
+}
+
+// Compression event whose rows are also decoded into the dense key space
+// (which holds every earlier row: dec_hi = boundary), with an optional
+// independent gather (the chunk append) in the same launch.
+int compress_event_decoded(khq_layer* L, const khq::GatherArgs* g, hipStream_t stream) {
+    const int c_a = L->boundary;
+    khq::CompressJob kj, vj;
+    compress_jobs(L, &kj, &vj);
+    khq::DecompArgs da{};
+    decomp_args(L, c_a, kChunk, &da);
+    const hipError_t e = khq::launch_compress_decode(kj, vj, da, g, stream);
+    if (e != hipSuccess) return (int)e;
+    L->boundary += kChunk;
+    L->n_events += 1;
+    L->dec_hi = c_a + kChunk;
+    // V^T columns up to the decode's last 16-column block are rewritten
+    L->raw_lo = std::max(L->raw_lo, c_a + (kChunk + 15) / 16 * 16);
+    return 0;
 }
 
 int split_count(int c_len, int splits) {  // ref runtime.mojo:211-222
@@ -209,6 +233,15 @@ int khq_layer_payload(const khq_layer* L, void** ptrs) {
     void* p[] = {L->kmask, L->kpay, L->knorm, L->krn, L->vpay, L->vnorm, L->vrn, L->vsm,
                  L->ring_k, L->ring_v, L->ring_u};
     for (int i = 0; i < 11; i++) ptrs[i] = p[i];
+    return 0;
+}
+
+int khq_layer_dense(const khq_layer* L, void** k, void** vt, int* ld_vt, int* n_decoded) {
+    if (!L || !k || !vt || !ld_vt || !n_decoded) return -100;
+    *k = L->dk;
+    *vt = L->dvt;
+    *ld_vt = L->d_ld;
+    *n_decoded = L->dec_hi;
     return 0;
 }
 
@@ -456,11 +489,15 @@ int khq_layer_prefill(khq_layer* L, const void* q_gate, const void* k_roped, con
             return 0;
         };
         if (combine) {
-            int rc = compress_event(L, stream);
+            // steady state (every earlier row decoded): the event decodes its
+            // own rows, with the deferred append in the same launch
+            const bool fused = L->dec_hi == c_a;
+            int rc = fused ? compress_event_decoded(L, defer ? &cw : nullptr, stream)
+                           : compress_event(L, stream);
             if (rc) return rc;
             const int c_b = L->boundary;  // c_a + kChunk
             const int n_k = w0 + m;
-            rc = prepare(c_b, n_k, defer ? &cw : nullptr);
+            rc = prepare(c_b, n_k, defer && !fused ? &cw : nullptr);
             if (rc) return rc;
             rc = khq::prefill_attn_run(qg + (size_t)done * L->H_q * 2 * kD, L->dk, L->dvt,
                                        L->d_ld, n_k, m, w0 + 1, L->H_q, L->H_kv, scale,

@@ -24,6 +24,8 @@
 
 #include "khq_internal.h"
 #include "khq_mfma_util.h"
+#include "khq_decode_row.h"
+#include "khq_compress_row.h"
 
 namespace khq {
 namespace pf {
@@ -70,27 +72,8 @@ __device__ __forceinline__ void decompress_block(const DecompArgs& a, int bx, in
     __shared__ __align__(16) _Float16 sv[256][TOK_BLK + VT_PAD];
     const int wv = threadIdx.x >> 6, p = threadIdx.x & 63;
     const int t_blk = bx * TOK_BLK;
-    // per-lane constants
-    float cbk[4], ldk[4], ldv[4], rk[16], rv[16];
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        cbk[c] = __half2float(a.cents_k[512 + 4 * p + c]);
-        ldk[c] = (1.0f / 256.0f) / (__half2float(a.dk[4 * p + c]) + 1e-8f);
-        ldv[c] = (1.0f / 16.0f) / (__half2float(a.dv[4 * p + c]) + 1e-8f);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        rk[i] = __half2float(a.rotor_k[p * 16 + i]);
-        rv[i] = __half2float(a.rotor_v[p * 16 + i]);
-    }
-    const float cv0 = __half2float(a.cents_v[4 * p + 3]) * a.a_v;
-    const float cv1 = __half2float(a.cents_v[256 + 4 * p + 3]) * a.a_v;
-    // RoPE frequencies of dims 4 (p & 7) + c (lanes 0..15 rotate dims 0..63)
-    float fr[4];
-#pragma unroll
-    for (int c = 0; c < 4; c++) fr[c] = powf(a.rope_base, -2.0f * (float)(4 * (p & 7) + c) / 64.0f);
-    const uint64_t below = (p == 0) ? 0ull : (~0ull >> (64 - p));
-
+    dec::Consts cs;
+    dec::load_consts(a, p, cs);
     {
         const int tl = wv;           // token within the block
         const int tok = t_blk + tl;
@@ -100,73 +83,14 @@ __device__ __forceinline__ void decompress_block(const DecompArgs& a, int bx, in
             goto staged;
         }
         const size_t g = (size_t)(a.tok0 + tok) * a.h_kv + h;
-        // ---- K: codes, outlier ordinals (ballot prefix), values
-        const uint32_t mw = a.kmask[g * 16 + (p >> 2)];
-        const uint8_t* kb = a.kpay + g * 40;
-        const float nk = __half2float(a.knorm[g]);
-        const float rs = __half2float(a.krn[g]);
-        float mult = (float)rd32(kb) / 1000.0f;
-        if (mult < 0.1f || mult > 10.0f || isnan(mult)) mult = 1.0f;
-        uint32_t code[4];
-        int own = 0, ord = 0;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            code[k] = (mw >> (2 * (4 * (p & 3) + k))) & 3u;
-            const uint64_t b = __ballot(code[k] == 3u);
-            ord += __popcll(b & below);
-        }
-        float kf[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const float cbase = cbk[k] * mult;
-            float kv = 0.0f;
-            if (code[k] == 3u) {
-                const int jo = ord + own;
-                const float sign = (jo < 50 && ((kb[29 + jo / 8] >> (jo % 8)) & 1)) ? 1.0f : -1.0f;
-                const float r4 = (jo < 50) ? (float)((kb[4 + jo / 2] >> ((jo % 2) * 4)) & 0xF) : 0.0f;
-                kv = sign * fmaf(r4, rs, cbase);
-                own++;
-            } else if (code[k] == 2u) {
-                kv = cbase;
-            } else if (code[k] == 1u) {
-                kv = -cbase;
-            }
-            kf[k] = kv * a.a_k * nk;
-        }
         float y[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            float s = kf[0] * rk[c * 4 + 0];
-            s = fmaf(kf[1], rk[c * 4 + 1], s);
-            s = fmaf(kf[2], rk[c * 4 + 2], s);
-            s = fmaf(kf[3], rk[c * 4 + 3], s);
-            y[c] = s;
-        }
-        fwht256(y, p);
-#pragma unroll
-        for (int c = 0; c < 4; c++) y[c] *= ldk[c];
-        // RoPE on dims 0..63: lane p < 8 holds dim i, lane p + 8 dim i + 32
-        {
-            float xo[4];
-#pragma unroll
-            for (int c = 0; c < 4; c++) xo[c] = __shfl_xor(y[c], 8, 64);
-            if (p < 16) {
-                const float pos = (float)(a.start_pos + a.tok0 + tok);
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    float cs, sn;
-                    sincos_rev(pos * fr[c], cs, sn);
-                    y[c] = p < 8 ? fmaf(y[c], cs, -(xo[c] * sn)) : fmaf(xo[c], sn, y[c] * cs);
-                }
-            }
-        }
+        // ---- K: codes, outlier ordinals (ballot prefix), values, RoPE
+        dec::decode_k(a, cs, a.kmask[g * 16 + (p >> 2)], a.kpay + g * 40, __half2float(a.knorm[g]),
+                      __half2float(a.krn[g]), (float)(a.start_pos + a.tok0 + tok), p, y);
         *reinterpret_cast<uint2*>(a.out_k + ((size_t)(a.key0 + tok) * a.h_kv + h) * 256 + 4 * p) =
             uint2{pk_rne(y[0], y[1]), pk_rne(y[2], y[3])};
         // ---- V: patch fields, codebook, dim 3, inverse rotor, FWHT
         const uint8_t* vp = a.vpay + g * 104;
-        const float nv = __half2float(a.vnorm[g]);
-        const float ec = __half2float(a.vrn[g]);
-        const float smv = __uint_as_float(rd32(a.vsm + g * 4));
         const uint32_t grp = (uint32_t)p / 8, sub = (uint32_t)p % 8;
         const uint64_t w0 = rd32(vp + (grp * 3 + 0) * 4), w1 = rd32(vp + (grp * 3 + 1) * 4),
                        w2 = rd32(vp + (grp * 3 + 2) * 4);
@@ -174,24 +98,10 @@ __device__ __forceinline__ void decompress_block(const DecompArgs& a, int bx, in
         const uint32_t pvl = (sub < 4) ? (uint32_t)((low64 >> (sub * 12)) & 0xFFF)
                                        : (uint32_t)((high64 >> ((sub - 4) * 12 + 16)) & 0xFFF);
         const uint32_t hb = (p < 32) ? ((rd32(vp + 96) >> p) & 1u) : ((rd32(vp + 100) >> (p - 32)) & 1u);
-        const uint32_t vc = (pvl & 0x7Fu) | (hb << 7);
-        const float pre_v = (a.a_v * nv) * ec;
-        const float pre_r = smv * nv;
-        float vv[4];
+        dec::decode_v(a, cs, (pvl & 0x7Fu) | (hb << 7), pvl, __half2float(a.vnorm[g]),
+                      __half2float(a.vrn[g]), __uint_as_float(rd32(a.vsm + g * 4)), p, y);
 #pragma unroll
-        for (int k = 0; k < 3; k++) vv[k] = __half2float(a.vq[(size_t)p * 768 + vc * 3 + k]) * pre_v;
-        vv[3] = fmaf(((float)((pvl >> 8) & 0xFu) - 8.0f) / 7.0f, pre_r, (((pvl >> 7) & 1u) ? cv1 : cv0) * nv);
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            float s = vv[0] * rv[c * 4 + 0];
-            s = fmaf(vv[1], rv[c * 4 + 1], s);
-            s = fmaf(vv[2], rv[c * 4 + 2], s);
-            s = fmaf(vv[3], rv[c * 4 + 3], s);
-            y[c] = s;
-        }
-        fwht256(y, p);
-#pragma unroll
-        for (int c = 0; c < 4; c++) sv[4 * p + c][tl] = (_Float16)(y[c] * ldv[c]);
+        for (int c = 0; c < 4; c++) sv[4 * p + c][tl] = (_Float16)y[c];
     }
 staged:
     __syncthreads();
@@ -282,6 +192,34 @@ __global__ __launch_bounds__(BLK_THR) void decompress_gather_kernel(DecompArgs d
         return;
     }
     b -= nb_d;
+    const int per_plane = nx_g * g.h_kv;
+    const int bz = b / per_plane;
+    b -= bz * per_plane;
+    gather_block(g, b % nx_g, b / nx_g, bz);
+}
+
+// A compression event, the decode of its rows into the dense key space and
+// an independent gather (a chunk append or a raw copy, disjoint from the
+// rows compressed) in one launch: blocks [0, nb_v) compress and decode V rows
+// (one row per block, the longest blocks first), [nb_v, nb_v + nb_k) K rows
+// (four per block), the rest gather (x, then the KV head, then the job plane;
+// nx_g = 0: no gather).
+__global__ __launch_bounds__(BLK_THR) void compress_decode_kernel(CompressJob k, CompressJob v,
+                                                                  DecompArgs d, GatherArgs g,
+                                                                  int nb_k, int nx_g) {
+    int b = blockIdx.x;
+    if (b < v.n) {
+        compress_block<true>(v.x, v.d_vec, v.rotor, v.cents, v.vq, v.out_mask, v.out_norms,
+                             v.out_rn, v.out_pay, v.out_sm, v.n, v.ts, v.alpha, 1, b, &d);
+        return;
+    }
+    b -= v.n;
+    if (b < nb_k) {
+        compress_block<true>(k.x, k.d_vec, k.rotor, k.cents, k.vq, k.out_mask, k.out_norms,
+                             k.out_rn, k.out_pay, nullptr, k.n, k.ts, k.alpha, 0, b, &d);
+        return;
+    }
+    b -= nb_k;
     const int per_plane = nx_g * g.h_kv;
     const int bz = b / per_plane;
     b -= bz * per_plane;
@@ -805,6 +743,28 @@ hipError_t launch_decompress_gather(const DecompArgs& d, const GatherArgs& g, hi
     hipLaunchKernelGGL(pf::decompress_gather_kernel,
                        dim3(nx_d * d.h_kv + nx_g * g.h_kv * (1 + side)), dim3(pf::BLK_THR), 0, st,
                        d, g, nx_d, nx_g);
+    return hipGetLastError();
+}
+
+hipError_t launch_compress_decode(const CompressJob& k, const CompressJob& v, const DecompArgs& d,
+                                  const GatherArgs* g, hipStream_t st) {
+    // the decode covers exactly the compressed rows: token t, KV head h is row t h_kv + h
+    if (k.n != v.n || d.n_tok * d.h_kv != k.n || d.tok0 != d.key0 || d.start_pos != 0)
+        return hipErrorInvalidValue;
+    const int nb_k = (k.n + 3) / 4;
+    int nx_g = 0, planes = 0;
+    GatherArgs ga{};
+    if (g) {
+        const int side = g->src_k && g->side_n > 0 ? 1 : 0;
+        const int n_g = std::max(g->n, side ? g->side_n : 0);
+        if (n_g > 0) {
+            nx_g = (n_g + pf::TOK_BLK - 1) / pf::TOK_BLK;
+            planes = 1 + side;
+            ga = *g;
+        }
+    }
+    hipLaunchKernelGGL(pf::compress_decode_kernel, dim3(v.n + nb_k + nx_g * ga.h_kv * planes),
+                       dim3(pf::BLK_THR), 0, st, k, v, d, ga, nb_k, nx_g);
     return hipGetLastError();
 }
 

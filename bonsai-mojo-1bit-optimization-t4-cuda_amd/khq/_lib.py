@@ -48,6 +48,7 @@ SIGNATURES = {
     "khq_layer_reset": [P],
     "khq_layer_state": [P, P, P, P],
     "khq_layer_payload": [P, P],
+    "khq_layer_dense": [P, P, P, P, P],
     "khq_layer_capture_unroped": [P, P, P],
     "khq_layer_step": [P] * 6 + [F, P],
     "khq_layer_prefill": [P] * 6 + [I, F, P],

@@ -279,6 +279,15 @@ class NativeKhqLayer:
         self._lib.khq_layer_payload(self.handle, arr)
         return [int(p or 0) for p in arr]
 
+    def dense(self) -> tuple[int, int, int, int]:
+        """(K rows pointer, V^T pointer, V^T row stride, rows decoded) of the
+        prefill path's dense key space."""
+        k, vt = ctypes.c_void_p(), ctypes.c_void_p()
+        ld, nd = ctypes.c_int(), ctypes.c_int()
+        self._lib.khq_layer_dense(self.handle, ctypes.byref(k), ctypes.byref(vt),
+                                  ctypes.byref(ld), ctypes.byref(nd))
+        return int(k.value or 0), int(vt.value or 0), ld.value, nd.value
+
     def capture_unroped(self, k: torch.Tensor) -> None:
         from ._lib import KhqError, stream_handle
 

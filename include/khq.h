@@ -278,6 +278,12 @@ int khq_layer_state(const khq_layer* layer, int* boundary, int* write_pos, int* 
 /* Device pointers of kmask, kpay, knorm, krn, vpay, vnorm, vrn, vsm, ring_k,
  * ring_v, ring_u (11 entries), for inspection. */
 int khq_layer_payload(const khq_layer* layer, void** ptrs);
+/* The prefill path's dense key space, for inspection: roped K rows
+ * [keys][H_kv][256] (*k), V^T [H_kv][256][*ld_vt] (*vt), rows [0, *n_decoded)
+ * decoded from the compressed region (null pointers before the first
+ * prefill).  No counterpart in the reference (its prefill steps token by
+ * token). */
+int khq_layer_dense(const khq_layer* layer, void** k, void** vt, int* ld_vt, int* n_decoded);
 /* Post-norm, pre-RoPE K [H_kv][256] of the token about to be stepped into
  * ring_u[write_pos % 256] (ref runtime.mojo:432-451). */
 int khq_layer_capture_unroped(khq_layer* layer, const void* k_unroped, hipStream_t stream);

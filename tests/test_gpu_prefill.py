@@ -161,6 +161,47 @@ def test_layer_prefill_matches_steps(device):
         close(got[j], want[j])
 
 
+@pytest.mark.parametrize("chunks", [(128,) * 6, (1, 5, 250, 128, 100, 216)])
+def test_layer_prefill_decoded_rows_match_decode(device, chunks):
+    """The dense key space a layer's prefills build (compression events that
+    decode their own rows in the compressing launch, with the chunk append
+    beside them) holds, bit for bit, what khq_decompress_fp16 makes of the
+    layer's compressed rows."""
+    lc, _ = layer_consts(layer_id=5)
+    L = KL.NativeKhqLayer(lc, H_q=H_Q, H_kv=H_KV, cap=1024, device=device,
+                          options=KL.KhqOptions(splits=8, fused=True))
+    n = sum(chunks)
+    k, kr, v, q = _tokens(n, seed=37)
+    out = torch.empty((n, H_Q, D), device=device, dtype=torch.float16)
+    i = 0
+    for m in chunks:
+        assert L.prefill(t(q[i:i + m]), t(kr[i:i + m]), t(v[i:i + m]), t(k[i:i + m]),
+                         out[i:i + m], SCALE) == m
+        i += m
+    torch.cuda.synchronize()
+    boundary = L.state()[0]
+    kp, vtp, ld, n_dec = L.dense()
+    assert 384 <= n_dec <= boundary
+    got_k = torch.empty((n_dec * H_KV * D,), device=device, dtype=torch.float16)
+    assert _hip_d2d(got_k.data_ptr(), kp, got_k.numel() * 2) == 0
+    got_vt = torch.empty((H_KV * D * ld,), device=device, dtype=torch.float16)
+    assert _hip_d2d(got_vt.data_ptr(), vtp, got_vt.numel() * 2) == 0
+    rows, _ = _payload_np(L, n_dec)
+    pay = payload_from_rows(rows, n_dec * H_KV)
+    ld2 = ops.vt_ld(n_dec)
+    want_k = torch.zeros((n_dec * H_KV * D,), device=device, dtype=torch.float16)
+    want_vt = torch.zeros((H_KV * D * ld2,), device=device, dtype=torch.float16)
+    ops.decompress(pay, ops.Centroids(lc, device), want_k, want_vt, H_kv=H_KV, tok0=0,
+                   n_tok=n_dec, key0=0, ld_vt=ld2)
+    torch.cuda.synchronize()
+    gk = got_k.cpu().numpy().view(np.uint16)
+    wk = want_k.cpu().numpy().view(np.uint16)
+    assert np.array_equal(gk, wk)
+    gv = got_vt.cpu().numpy().view(np.uint16).reshape(H_KV * D, ld)[:, :n_dec]
+    wv = want_vt.cpu().numpy().view(np.uint16).reshape(H_KV * D, ld2)[:, :n_dec]
+    assert np.array_equal(gv, wv)
+
+
 def test_c5_chunk_vs_oracle(device):
     """Config 5: 8,192 tokens already appended (boundary 8,064, raw 8,064..
     8,191), then one chunk of 128 tokens at positions 8,192..8,319; the 128th
