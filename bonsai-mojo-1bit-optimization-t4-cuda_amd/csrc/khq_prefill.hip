@@ -677,52 +677,66 @@ void prefill_attn32_kernel(PrefillArgs a) {
     }
 }
 
-// Merge of the key splits, normalisation and gate: one block per (query,
-// head) row, thread = dim; every thread walks the row's n_split (m, l) pairs
-// (the same addresses for the whole block) and its own acc column.
+// Merge of the key splits, normalisation and gate: one wavefront per (query,
+// head) row, lane l owning dims 4 l .. 4 l + 3; lane s < n_split holds split
+// s's (m, l) pair.  Each group of up to 16 splits has every load in flight
+// before the first is used; the sums run in split order.
+constexpr int MG = 16;  // splits per load group
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part,
                                                             const __half* __restrict__ q_gate,
-                                                            __half* __restrict__ out, int n_split,
-                                                            float eps) {
-    __shared__ float s_w[64];  // split weights exp(m_s - M)
-    __shared__ float s_l[64];
-    const int row = blockIdx.x, d = threadIdx.x;
+                                                            __half* __restrict__ out, int n_rows,
+                                                            int n_split, float eps) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= n_rows) return;  // uniform per wavefront
     const float* base = part + (size_t)row * n_split * 258;
-    // the row's (m, l) pairs once per block, its acc column per thread, all
-    // loads issued before any is used (n_split <= 64)
-    float acc[64];
-#pragma unroll
-    for (int s = 0; s < 64; s++) acc[s] = s < n_split ? base[(size_t)s * 258 + d] : 0.0f;
     float m = -1e30f, l = 0.0f;
-    if (d < n_split) {
-        m = base[(size_t)d * 258 + 256];
-        l = base[(size_t)d * 258 + 257];
+    if (lane < n_split) {
+        const float2 ml = *reinterpret_cast<const float2*>(base + (size_t)lane * 258 + 256);
+        m = ml.x;
+        l = ml.y;
     }
-    float M = d < 64 ? m : -1e30f;
+    float M = m;
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    if (d < 64) {
-        const float w = d < n_split ? __expf(m - M) : 0.0f;
-        s_w[d] = w;
-        s_l[d] = l * w;
-    }
-    __syncthreads();
-    float num = 0.0f, den = 0.0f;
+    const float w = lane < n_split ? __expf(m - M) : 0.0f;
+    const float lw = l * w;
+    float num[4] = {0.f, 0.f, 0.f, 0.f}, den = 0.0f;
+    for (int s0 = 0; s0 < n_split; s0 += MG) {
+        float2 a[MG][2];
 #pragma unroll
-    for (int s = 0; s < 64; s++) {
-        num = fmaf(acc[s], s_w[s], num);
-        den += s_l[s];
+        for (int j = 0; j < MG; j++)
+            if (s0 + j < n_split) {
+                const float* pp = base + (size_t)(s0 + j) * 258 + 4 * lane;
+                a[j][0] = *reinterpret_cast<const float2*>(pp);
+                a[j][1] = *reinterpret_cast<const float2*>(pp + 2);
+            }
+#pragma unroll
+        for (int j = 0; j < MG; j++)
+            if (s0 + j < n_split) {
+                const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), s0 + j));
+                num[0] = fmaf(a[j][0].x, ws, num[0]);
+                num[1] = fmaf(a[j][0].y, ws, num[1]);
+                num[2] = fmaf(a[j][1].x, ws, num[2]);
+                num[3] = fmaf(a[j][1].y, ws, num[3]);
+                den += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lw), s0 + j));
+            }
     }
-    const float g = __half2float(q_gate[(size_t)row * 512 + 256 + d]);
-    out[(size_t)row * 256 + d] = __float2half(num / (den + eps) * (1.0f / (1.0f + expf(-g))));
+    const uint2 gw = *reinterpret_cast<const uint2*>(q_gate + (size_t)row * 512 + 256 + 4 * lane);
+    const h4 g = __builtin_bit_cast(h4, gw);
+    float o[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        o[c] = num[c] / (den + eps) * (1.0f / (1.0f + expf(-(float)g[c])));
+    *reinterpret_cast<uint2*>(out + (size_t)row * 256 + 4 * lane) =
+        uint2{pk_rne(o[0], o[1]), pk_rne(o[2], o[3])};
 }
 
 }  // namespace pf
 
 hipError_t launch_prefill_merge(const float* part, const __half* q_gate, __half* out, int n_rows,
                                 int n_split, float eps, hipStream_t st) {
-    hipLaunchKernelGGL(pf::prefill_merge_kernel, dim3(n_rows), dim3(256), 0, st, part, q_gate, out,
-                       n_split, eps);
+    hipLaunchKernelGGL(pf::prefill_merge_kernel, dim3((n_rows + 3) / 4), dim3(256), 0, st, part,
+                       q_gate, out, n_rows, n_split, eps);
     return hipGetLastError();
 }
 
