@@ -93,6 +93,17 @@ __device__ __forceinline__ void compress_block(
     const float f_s = 0.0625f;
     dec::Consts dcs;
     if constexpr (DEC) dec::load_consts(*da, lane, dcs);
+    // every per-lane constant is requested here, so the block waits for
+    // memory once instead of once per phase
+    float dv4[4], rot[16], cbk[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) dv4[c] = h2f(d_vec[lane * 4 + c]);
+#pragma unroll
+    for (int i = 0; i < 16; i++) rot[i] = h2f(rotor[lane * 16 + i]);
+    // K: the code-1/2 centroid of the lane's dims; V: the dim-3 centroids
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        cbk[c] = is_v ? h2f(cents[(c & 1) * 256 + lane * 4 + 3]) : h2f(cents[2 * 256 + lane * 4 + c]);
 
     float xv[4] = {0.f, 0.f, 0.f, 0.f};
     if (valid) {
@@ -117,18 +128,17 @@ __device__ __forceinline__ void compress_block(
 
     float r[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) r[c] = (xv[c] * h2f(d_vec[lane * 4 + c])) / (norm + 1e-8f);
+    for (int c = 0; c < 4; c++) r[c] = (xv[c] * dv4[c]) / (norm + 1e-8f);
     fwht256(r);
 
     float proj[4];
     {
-        const __half* R = rotor + lane * 16;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            float acc = r[0] * h2f(R[0 * 4 + c]);
-            acc = fmaf(r[1], h2f(R[1 * 4 + c]), acc);
-            acc = fmaf(r[2], h2f(R[2 * 4 + c]), acc);
-            acc = fmaf(r[3], h2f(R[3 * 4 + c]), acc);
+            float acc = r[0] * rot[0 * 4 + c];
+            acc = fmaf(r[1], rot[1 * 4 + c], acc);
+            acc = fmaf(r[2], rot[2 * 4 + c], acc);
+            acc = fmaf(r[3], rot[3 * 4 + c], acc);
             proj[c] = acc * f_s;
         }
     }
@@ -161,7 +171,7 @@ __device__ __forceinline__ void compress_block(
                 code[c] = proj[c] > 0.47f * f_s ? 2u : (proj[c] < -0.47f * f_s ? 1u : 0u);
                 if (code[c] != 0u) {
                     sa = fabsf(proj[c]);
-                    sb = h2f(cents[2 * 256 + lane * 4 + c]);
+                    sb = cbk[c];
                 }
             }
             s_a[wave][lane * 4 + c] = sa;
@@ -184,7 +194,7 @@ __device__ __forceinline__ void compress_block(
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             if (code[c] == 3u) {
-                const float cb = h2f(cents[2 * 256 + lane * 4 + c]);
+                const float cb = cbk[c];
                 res[c] = fmaxf(0.0f, fmaf(-cb, mult, fabsf(proj[c] * ts)));
                 my_max = fmaxf(my_max, res[c]);
             }
@@ -239,7 +249,6 @@ __device__ __forceinline__ void compress_block(
 
     // ---- V branch, ref .cu:1353-1428: lane p owns patch p
     const float v0 = proj[0], v1 = proj[1], v2 = proj[2], v3 = proj[3];
-    const __half* cb = vq + (size_t)lane * 768;
     float best_d = 1e20f;
     unsigned best = 0;
     // the lane's codebook quarter (codes 64 wave .. + 63) in two chunks of 32
@@ -247,7 +256,7 @@ __device__ __forceinline__ void compress_block(
     // is searched; codes in increasing order with a strict < (first minimum
     // wins), then the quarters in order through LDS, so the result is the
     // sequential search's
-    const uint4* cb4 = reinterpret_cast<const uint4*>(cb);
+    const uint4* cb4 = reinterpret_cast<const uint4*>(vq + (size_t)lane * 768);
     uint4 cur[12], nxt[12];
 #pragma unroll
     for (int k = 0; k < 12; k++) cur[k] = cb4[12 * (2 * wave) + k];
@@ -256,12 +265,12 @@ __device__ __forceinline__ void compress_block(
 #pragma unroll
             for (int k = 0; k < 12; k++) nxt[k] = cb4[12 * (ch + 1) + k];
         }
-        const __half* hv = reinterpret_cast<const __half*>(cur);
+        const uint16_t* hv = reinterpret_cast<const uint16_t*>(cur);
 #pragma unroll
         for (int j = 0; j < 32; j++) {
-            const float d0 = fmaf(-h2f(hv[3 * j + 0]), alpha, v0);
-            const float d1 = fmaf(-h2f(hv[3 * j + 1]), alpha, v1);
-            const float d2 = fmaf(-h2f(hv[3 * j + 2]), alpha, v2);
+            const float d0 = fmaf(-h2f(__ushort_as_half(hv[3 * j + 0])), alpha, v0);
+            const float d1 = fmaf(-h2f(__ushort_as_half(hv[3 * j + 1])), alpha, v1);
+            const float d2 = fmaf(-h2f(__ushort_as_half(hv[3 * j + 2])), alpha, v2);
             const float dist = fmaf(d2, d2, fmaf(d1, d1, d0 * d0));
             if (dist < best_d) { best_d = dist; best = 32u * ch + j; }
         }
@@ -283,13 +292,15 @@ __device__ __forceinline__ void compress_block(
                 best = s_bi[w][lane];
             }
     }
-    const float c0 = h2f(cb[best * 3 + 0]) * alpha;
-    const float c1 = h2f(cb[best * 3 + 1]) * alpha;
-    const float c2 = h2f(cb[best * 3 + 2]) * alpha;
+    const __half* cbp = vq + (size_t)lane * 768;
+    const float cbh[3] = {h2f(cbp[best * 3]), h2f(cbp[best * 3 + 1]), h2f(cbp[best * 3 + 2])};
+    const float c0 = cbh[0] * alpha;
+    const float c1 = cbh[1] * alpha;
+    const float c2 = cbh[2] * alpha;
     const float te = fmaf(v2, v2, fmaf(v1, v1, v0 * v0));
     const float ve = fmaf(c2, c2, fmaf(c1, c1, c0 * c0));
-    const float cv0 = h2f(cents[0 * 256 + lane * 4 + 3]);
-    const float cv1 = h2f(cents[1 * 256 + lane * 4 + 3]);
+    const float cv0 = cbk[0];
+    const float cv1 = cbk[1];
     const float dd0 = fabsf(fmaf(-cv0, alpha, v3));
     const float dd1 = fabsf(fmaf(-cv1, alpha, v3));
     unsigned bs = 0;
@@ -331,7 +342,7 @@ __device__ __forceinline__ void compress_block(
         const float ec = h2f(__float2half(sqrtf(st / (sv + 1e-8f))));
         const int tok = row / da->h_kv, h = row - tok * da->h_kv;
         float y[4];
-        dec::decode_v(*da, dcs, best, pv, h2f(__float2half(norm)), ec, max_res, lane, y);
+        dec::decode_v_cb(*da, dcs, cbh, pv, h2f(__float2half(norm)), ec, max_res, lane, y);
         _Float16* vt = reinterpret_cast<_Float16*>(da->out_vt);
 #pragma unroll
         for (int c = 0; c < 4; c++)

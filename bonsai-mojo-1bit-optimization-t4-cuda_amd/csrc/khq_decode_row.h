@@ -109,18 +109,19 @@ __device__ __forceinline__ void decode_k(const DecompArgs& a, const Consts& c, u
     }
 }
 
-// V row: vc = the patch's 8-bit codebook index, pvl = its 12-bit field
+// V row: vc (decode_v) = the patch's 8-bit codebook index, pvl = its 12-bit field
 // (bit 7 the dim-3 centroid, bits 8..11 the dim-3 residual), nv / ec / smv =
 // the row's fp16 norm, fp16 energy ratio (as floats) and fp32 shared meta.
 // y = the decoded dims, 1 / (16 d_v) applied.
-__device__ __forceinline__ void decode_v(const DecompArgs& a, const Consts& c, uint32_t vc,
-                                         uint32_t pvl, float nv, float ec, float smv, int p,
-                                         float (&y)[4]) {
+// cbv = the patch's codebook entry (three fp16 values as floats).
+__device__ __forceinline__ void decode_v_cb(const DecompArgs& a, const Consts& c, const float (&cbv)[3],
+                                            uint32_t pvl, float nv, float ec, float smv, int p,
+                                            float (&y)[4]) {
     const float pre_v = (a.a_v * nv) * ec;
     const float pre_r = smv * nv;
     float vv[4];
 #pragma unroll
-    for (int k = 0; k < 3; k++) vv[k] = __half2float(a.vq[(size_t)p * 768 + vc * 3 + k]) * pre_v;
+    for (int k = 0; k < 3; k++) vv[k] = cbv[k] * pre_v;
     vv[3] = fmaf(((float)((pvl >> 8) & 0xFu) - 8.0f) / 7.0f, pre_r,
                  (((pvl >> 7) & 1u) ? c.cv1 : c.cv0) * nv);
 #pragma unroll
@@ -134,6 +135,15 @@ __device__ __forceinline__ void decode_v(const DecompArgs& a, const Consts& c, u
     mu::fwht256(y, p);
 #pragma unroll
     for (int i = 0; i < 4; i++) y[i] *= c.ldv[i];
+}
+
+__device__ __forceinline__ void decode_v(const DecompArgs& a, const Consts& c, uint32_t vc,
+                                         uint32_t pvl, float nv, float ec, float smv, int p,
+                                         float (&y)[4]) {
+    float cbv[3];
+#pragma unroll
+    for (int k = 0; k < 3; k++) cbv[k] = __half2float(a.vq[(size_t)p * 768 + vc * 3 + k]);
+    decode_v_cb(a, c, cbv, pvl, nv, ec, smv, p, y);
 }
 
 }  // namespace dec

@@ -200,26 +200,26 @@ __global__ __launch_bounds__(BLK_THR) void decompress_gather_kernel(DecompArgs d
 
 // A compression event, the decode of its rows into the dense key space and
 // an independent gather (a chunk append or a raw copy, disjoint from the
-// rows compressed) in one launch: blocks [0, nb_v) compress and decode V rows
-// (one row per block, the longest blocks first), [nb_v, nb_v + nb_k) K rows
-// (four per block), the rest gather (x, then the KV head, then the job plane;
+// rows compressed) in one launch: blocks [0, nb_k) compress and decode K rows
+// (four per block, the longest blocks, first), [nb_k, nb_k + n_v) V rows (one
+// per block), the rest gather (x, then the KV head, then the job plane;
 // nx_g = 0: no gather).
 __global__ __launch_bounds__(BLK_THR) void compress_decode_kernel(CompressJob k, CompressJob v,
                                                                   DecompArgs d, GatherArgs g,
                                                                   int nb_k, int nx_g) {
     int b = blockIdx.x;
-    if (b < v.n) {
-        compress_block<true>(v.x, v.d_vec, v.rotor, v.cents, v.vq, v.out_mask, v.out_norms,
-                             v.out_rn, v.out_pay, v.out_sm, v.n, v.ts, v.alpha, 1, b, &d);
-        return;
-    }
-    b -= v.n;
     if (b < nb_k) {
         compress_block<true>(k.x, k.d_vec, k.rotor, k.cents, k.vq, k.out_mask, k.out_norms,
                              k.out_rn, k.out_pay, nullptr, k.n, k.ts, k.alpha, 0, b, &d);
         return;
     }
     b -= nb_k;
+    if (b < v.n) {
+        compress_block<true>(v.x, v.d_vec, v.rotor, v.cents, v.vq, v.out_mask, v.out_norms,
+                             v.out_rn, v.out_pay, v.out_sm, v.n, v.ts, v.alpha, 1, b, &d);
+        return;
+    }
+    b -= v.n;
     const int per_plane = nx_g * g.h_kv;
     const int bz = b / per_plane;
     b -= bz * per_plane;
