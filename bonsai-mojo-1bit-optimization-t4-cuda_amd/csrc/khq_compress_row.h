@@ -60,6 +60,47 @@ __device__ __forceinline__ void fwht256(float (&v)[4]) {
     }
 }
 
+// Sequential folds of LDS rows in index order (the reference's order), the
+// reads issued a batch at a time ahead of the batch's dependent chain (one
+// LDS round trip per batch instead of per element).
+__device__ __forceinline__ float fold_sq256(const float* v) {
+    float s = 0.0f;
+#pragma unroll 1
+    for (int i0 = 0; i0 < 256; i0 += 32) {
+        float4 t[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) t[j] = *reinterpret_cast<const float4*>(&v[i0 + 4 * j]);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            s = fmaf(t[j].x, t[j].x, s);
+            s = fmaf(t[j].y, t[j].y, s);
+            s = fmaf(t[j].z, t[j].z, s);
+            s = fmaf(t[j].w, t[j].w, s);
+        }
+    }
+    return s;
+}
+// sa = a[0] + a[1] + ..., sb likewise, over n (a multiple of 16) elements
+__device__ __forceinline__ void fold_sum2(const float* a, const float* b, int n, float& sa,
+                                          float& sb) {
+    sa = 0.0f;
+    sb = 0.0f;
+#pragma unroll 1
+    for (int i0 = 0; i0 < n; i0 += 16) {
+        float4 ta[4], tb[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            ta[j] = *reinterpret_cast<const float4*>(&a[i0 + 4 * j]);
+            tb[j] = *reinterpret_cast<const float4*>(&b[i0 + 4 * j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            sa += ta[j].x; sa += ta[j].y; sa += ta[j].z; sa += ta[j].w;
+            sb += tb[j].x; sb += tb[j].y; sb += tb[j].z; sb += tb[j].w;
+        }
+    }
+}
+
 // ---------------------------------------------------------------- compress
 // One wavefront per row, four rows per 256-thread block.  The reference
 // (ref:src/csrc/qmv_sm75_kernel.cu:1256-1467) runs one thread per row; the
@@ -115,14 +156,7 @@ __device__ __forceinline__ void compress_block(
     for (int c = 0; c < 4; c++) s_a[wave][lane * 4 + c] = xv[c];
     if (lane < 32) s_w[wave][lane] = 0u;
     __syncthreads();
-    float sum_sq = 0.0f;
-    for (int i = 0; i < 256; i += 4) {
-        float4 t = *reinterpret_cast<const float4*>(&s_a[wave][i]);
-        sum_sq = fmaf(t.x, t.x, sum_sq);
-        sum_sq = fmaf(t.y, t.y, sum_sq);
-        sum_sq = fmaf(t.z, t.z, sum_sq);
-        sum_sq = fmaf(t.w, t.w, sum_sq);
-    }
+    const float sum_sq = fold_sq256(s_a[wave]);
     const float norm = sqrtf(sum_sq + 1e-8f);
     if (live && lane == 0) out_norms[row] = __float2half(norm);
 
@@ -180,13 +214,8 @@ __device__ __forceinline__ void compress_block(
         unsigned byte = code[0] | (code[1] << 2) | (code[2] << 4) | (code[3] << 6);
         atomicOr(&s_w[wave][16 + (lane >> 2)], byte << (8 * (lane & 3)));
         __syncthreads();
-        float sum_normals = 0.0f, sum_cbase = 0.0f;
-        for (int i = 0; i < 256; i += 4) {
-            float4 ta = *reinterpret_cast<const float4*>(&s_a[wave][i]);
-            float4 tb = *reinterpret_cast<const float4*>(&s_b[wave][i]);
-            sum_normals += ta.x; sum_normals += ta.y; sum_normals += ta.z; sum_normals += ta.w;
-            sum_cbase += tb.x; sum_cbase += tb.y; sum_cbase += tb.z; sum_cbase += tb.w;
-        }
+        float sum_normals, sum_cbase;
+        fold_sum2(s_a[wave], s_b[wave], 256, sum_normals, sum_cbase);
         float mult = (sum_cbase > 1e-5f) ? (sum_normals / sum_cbase) : 1.0f;
         if (mult < 0.1f || mult > 10.0f || isnan(mult)) mult = 1.0f;
         float res[4] = {0.f, 0.f, 0.f, 0.f};
@@ -330,15 +359,15 @@ __device__ __forceinline__ void compress_block(
         op[24] = (uint32_t)(hi & 0xFFFFFFFFull);
         op[25] = (uint32_t)(hi >> 32);
     } else if (lane == 9) {
-        float st = 0.0f, sv = 0.0f;
-        for (int p = 0; p < 64; p++) { st += s_a[wave][p]; sv += s_b[wave][p]; }
+        float st, sv;
+        fold_sum2(s_a[wave], s_b[wave], 64, st, sv);
         out_rn[row] = __float2half(sqrtf(st / (sv + 1e-8f)));
         *reinterpret_cast<float*>(out_sm + (size_t)row * 4) = max_res;
     }
     if constexpr (DEC) {
         // the energy ratio as lane 9 folds it, on every lane
-        float st = 0.0f, sv = 0.0f;
-        for (int p = 0; p < 64; p++) { st += s_a[wave][p]; sv += s_b[wave][p]; }
+        float st, sv;
+        fold_sum2(s_a[wave], s_b[wave], 64, st, sv);
         const float ec = h2f(__float2half(sqrtf(st / (sv + 1e-8f))));
         const int tok = row / da->h_kv, h = row - tok * da->h_kv;
         float y[4];
