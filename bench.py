@@ -517,6 +517,29 @@ def bench_small(args):
     torch.cuda.synchronize()
     ms_step = e0.elapsed_time(e1) / args.steps
     us_layer = ms_step * 1000.0 / args.layers
+    # The same step captured once as a HIP graph and replayed (how a serving
+    # loop issues these launch-bound steps); the replayed outputs must equal
+    # the eager ones bit for bit before the figure is reported.
+    ops.workspace_reserve(64 << 20)
+    eager_out = [L[-1].clone() for L in layers]
+    for L in layers:
+        L[-1].zero_()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    graph.replay()
+    torch.cuda.synchronize()
+    same = all(torch.equal(a, L[-1]) for a, L in zip(eager_out, layers))
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us_layer_graph = e0.elapsed_time(e1) * 1000.0 / args.steps / args.layers if same else None
     if args.config == "c1":
         nbytes = 512 * H_KV * D * 2 * 2
         workload = f"C1: {args.layers} layers x 512 fp16 cached positions, H_q 24 / H_kv 4, D 256"
@@ -540,6 +563,11 @@ def bench_small(args):
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": None,
+        "graph_replay": {"us_per_layer_step": None if us_layer_graph is None else
+                         round(us_layer_graph, 3),
+                         "outputs_equal_eager": same,
+                         "note": "the 16-layer step captured as one HIP graph and replayed; "
+                                 "value is the eager launch loop"},
     }
     if not args.no_cpu:
         if args.config == "c1":
