@@ -1015,7 +1015,7 @@ __device__ __forceinline__ void window_block(const AttnArgs& a, Smem& S, int par
 //   scores q.k on MFMA (A = the 6 query rows of the group, B = K rows, both
 //   exact fp16, fp32 accumulate) into LDS;
 //   softmax per query head over the whole window in LDS;
-//   P x V on the vector ALUs, lane l holding dims 4 l .. 4 l + 3;
+//   P x V on the matrix cores (below);
 // then the two halves of each KV head are added into one partial triple.
 __device__ void window_block_all(const AttnArgs& a, Smem& S, int part_idx) {
     constexpr int WMAX = 256;
@@ -1091,50 +1091,98 @@ __device__ void window_block_all(const AttnArgs& a, Smem& S, int part_idx) {
         }
     }
     __syncthreads();
-    // ---- P x V over this half's rows
-    float acc[6][4];
-#pragma unroll
-    for (int i = 0; i < 6; i++)
-#pragma unroll
-        for (int c = 0; c < 4; c++) acc[i][c] = 0.0f;
-    for (int s0 = r_lo; s0 < r_hi; s0 += 16) {  // 16 rows' loads in flight at once
-        uint2 vr[16];
+    // ---- P x V on the matrix cores over this half's rows:
+    // O^T [dim][head] = V^T [dim][token] P^T [token][head] with 16x16x16
+    // MFMAs (M = 16 dims, N = the 6 query heads, K = 16 tokens); the weights
+    // enter as fp16 hi + lo (two MFMAs), V exact.  Each wavefront stages its
+    // 16-token V groups transposed in its own LDS region: lane l's dims
+    // 4 l .. 4 l + 3 become 4 rows of 16 tokens.  Group g + 1's rows load
+    // while group g is used.
+    constexpr int VT_LD = 20;  // halves per staged V^T row (16 tokens + pad; 8-byte rows)
+    _Float16* vts = reinterpret_cast<_Float16*>(sacc + 4 * 6 * 256) + wv * 256 * VT_LD;
+    const int n_g = (r_hi - r_lo + 15) / 16;  // 16-token groups of this half
+    auto load_v = [&](uint2 (&vr)[16], int s0) {
 #pragma unroll
         for (int u = 0; u < 16; u++) {
             const int slot = slot_of(min(s0 + u, r_hi - 1));
             vr[u] = ldg<uint2>(a.ring_v + ((size_t)slot * a.h_kv + hk) * 256 + 4 * lane);
         }
+    };
+    f4 o[16];
 #pragma unroll
-        for (int u = 0; u < 16; u++) {  // rows past r_hi weigh 0 (no early exit: vr stays in registers)
-            const bool ok = s0 + u < r_hi;
-            const int su = min(s0 + u, WMAX - 1);
-            const h4 vh = __builtin_bit_cast(h4, vr[u]);
+    for (int i = 0; i < 16; i++) o[i] = f4{0.f, 0.f, 0.f, 0.f};
+    const int n = li, kg = lg;  // B / C column: query head n; K group kg
+    auto group = [&](const uint2 (&vr)[16], int s0) {
+        // V^T rows 4 lane + c, tokens s0 .. s0 + 15
 #pragma unroll
-            for (int i = 0; i < 6; i++) {
-                const float p = ok ? sp[(hk * 6 + i) * WMAX + su] : 0.0f;
+        for (int c = 0; c < 4; c++) {
+            const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+            uint32_t wds[8];
 #pragma unroll
-                for (int c = 0; c < 4; c++) acc[i][c] = fmaf(p, (float)vh[c], acc[i][c]);
+            for (int u = 0; u < 8; u++) {
+                const uint32_t x0 = (c < 2) ? vr[2 * u].x : vr[2 * u].y;
+                const uint32_t x1 = (c < 2) ? vr[2 * u + 1].x : vr[2 * u + 1].y;
+                wds[u] = __builtin_amdgcn_perm(x1, x0, sel);
+            }
+            uint2* row = reinterpret_cast<uint2*>(vts + (4 * lane + c) * VT_LD);
+#pragma unroll
+            for (int q = 0; q < 4; q++) row[q] = uint2{wds[2 * q], wds[2 * q + 1]};
+        }
+        // P^T: tokens s0 + 4 kg .. + 3 of head n (rows past r_hi and heads
+        // past 5 weigh 0), split hi + lo
+        f4 pw = f4{0.f, 0.f, 0.f, 0.f};
+        if (n < 6) pw = *reinterpret_cast<const f4*>(&sp[(hk * 6 + n) * WMAX + min(s0 + 4 * kg, WMAX - 4)]);
+        h4 bh, bl;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float p = (s0 + 4 * kg + j < r_hi) ? pw[j] : 0.0f;
+            const _Float16 h = (_Float16)p;
+            bh[j] = h;
+            bl[j] = (_Float16)(p - (float)h);
+        }
+        wave_sync();  // this wavefront's V^T rows are in place
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const h4 av = *reinterpret_cast<const h4*>(vts + (16 * i + n) * VT_LD + 4 * kg);
+            o[i] = mfma16(av, bh, o[i]);
+            o[i] = mfma16(av, bl, o[i]);
+        }
+        wave_sync();  // the rows are read before the next group overwrites them
+    };
+    {
+        uint2 vrA[16], vrB[16];
+        if (n_g > 0) load_v(vrA, r_lo);
+        if (n_g > 1) load_v(vrB, r_lo + 16);
+        for (int g = 0; g < n_g; g += 2) {
+            group(vrA, r_lo + 16 * g);
+            if (g + 2 < n_g) load_v(vrA, r_lo + 16 * (g + 2));
+            if (g + 1 < n_g) {
+                group(vrB, r_lo + 16 * (g + 1));
+                if (g + 3 < n_g) load_v(vrB, r_lo + 16 * (g + 3));
             }
         }
     }
-    if (half == 1) {
+    // C layout: lane (n, kg) holds dims 16 i + 4 kg .. + 3 of head n
+    if (half == 1 && n < 6) {
 #pragma unroll
-        for (int i = 0; i < 6; i++)
-            *reinterpret_cast<f4*>(&sacc[(hk * 6 + i) * 256 + 4 * lane]) =
-                f4{acc[i][0], acc[i][1], acc[i][2], acc[i][3]};
+        for (int i = 0; i < 16; i++)
+            *reinterpret_cast<f4*>(&sacc[(hk * 6 + n) * 256 + 16 * i + 4 * kg]) = o[i];
     }
     __syncthreads();
-    if (half == 0) {
+    if (half == 0 && n < 6) {
+        const int hq = hk * 6 + n;
+        float* out = a.part + ((size_t)hq * a.part_stride + part_idx) * 258;
+        typedef float f2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-        for (int i = 0; i < 6; i++) {
-            const f4 o = *reinterpret_cast<const f4*>(&sacc[(hk * 6 + i) * 256 + 4 * lane]);
-            const int hq = hk * 6 + i;
-            float* out = a.part + ((size_t)hq * a.part_stride + part_idx) * 258;
-            stg<f4>(&out[4 * lane], f4{acc[i][0] + o[0], acc[i][1] + o[1], acc[i][2] + o[2], acc[i][3] + o[3]});
-            if (lane == 0) {
-                stg<float>(&out[256], sml[(hk * 6 + i) * 2 + 0]);
-                stg<float>(&out[257], sml[(hk * 6 + i) * 2 + 1]);
-            }
+        for (int i = 0; i < 16; i++) {
+            const f4 h1 = *reinterpret_cast<const f4*>(&sacc[(hk * 6 + n) * 256 + 16 * i + 4 * kg]);
+            const int d = 16 * i + 4 * kg;
+            stg<f2>(&out[d], f2{o[i][0] + h1[0], o[i][1] + h1[1]});
+            stg<f2>(&out[d + 2], f2{o[i][2] + h1[2], o[i][3] + h1[3]});
+        }
+        if (kg == 0) {
+            stg<float>(&out[256], sml[hq * 2 + 0]);
+            stg<float>(&out[257], sml[hq * 2 + 1]);
         }
     }
 }
@@ -1314,6 +1362,9 @@ __global__ __launch_bounds__(NTHR, 1) void attn_ws_batched_kernel(const AttnArgs
 
 }  // namespace ws
 
+static_assert((4 * 6 * 256 + 4 * 6 * 2 + 4 * 6 * 256) * sizeof(float) + 8 * 256 * 20 * 2 <=
+                  sizeof(ws::Smem),
+              "window block LDS: scores, sums, half-sums and V^T staging fit the block's LDS");
 size_t attn_ws_smem_bytes() { return sizeof(ws::Smem); }
 
 int g_spin_limit = 1 << 20;
