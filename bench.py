@@ -448,7 +448,7 @@ def bench_c5(args):
         "tflops_layer_step": round(flops / (us_layer * 1e-6) / 1e12, 2),
         "roofline": {
             "bound": "mfma",
-            "kernel": "prefill_attn_kernel (127 queries x 24 heads over 8,319 keys) + combine",
+            "kernel": "prefill_attn_rs_kernel (127 queries x 24 heads over 8,319 keys) + prefill_merge_kernel",
             "achieved": round(attn_flops / (attn_us * 1e-6) / 1e12, 2),
             "peak": 2500.0,
             "unit": "TFLOP/s",

@@ -1,7 +1,7 @@
 // khq_prefill.hip -- chunked prefill on matrix cores: many query tokens of one
 // layer attend to the compressed prefix and the raw ring window at once.
 //
-// Three kernels build one dense fp16 key space (key index = token position)
+// Kernels that build one dense fp16 key space (key index = token position)
 // and attend over it causally:
 //   decompress_kernel   compressed rows -> roped K rows [key][H_kv][256] and
 //                       V^T [H_kv][256][ld] (the decode of the compressed-
@@ -10,10 +10,12 @@
 //                       1776-1826 for V, applied per token instead of being
 //                       folded into the running sums);
 //   ring_gather_kernel  raw ring slots -> the same K rows / V^T columns;
-//   prefill_attn_kernel S^T = K Q^T and O^T = V^T P^T on MFMA (fp16 in, fp32
-//                       accumulate), online softmax, one split of the keys per
-//                       block, partial triples merged and gated by
-//                       combine_gate_kernel.
+//   compress_decode_kernel  a compression event that decodes the rows it
+//                       packs into the key space (and appends new tokens);
+//   prefill_attn_kernel, prefill_attn_rs_kernel  S^T = K Q^T and
+//                       O^T = V^T P^T on MFMA (fp16 in, fp32 accumulate),
+//                       online softmax, one split of the keys per block;
+//   prefill_merge_kernel  the splits' partial triples merged and gated.
 // Query j of a launch sees keys [0, vis0 + j): the sequential step semantics
 // (its own position included) when keys are positions.
 #include <hip/hip_runtime.h>
@@ -441,13 +443,11 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillArgs a) {
     }
 }
 
-// 32-row form: each wavefront owns 32 query rows and uses 32x32x16 MFMAs, so
-// every K / V^T operand read from LDS feeds twice the arithmetic of the
-// 16-row form.  One block (4 wavefronts, 128 rows) per CU: the O^T
-// accumulators (32 rows x 256 dims) and Q^T (32 x 256 fp16) stay in
-// registers.  Per tile every LDS operand read of the tile (16 K, 32 V^T) is
-// issued first, then the S^T MFMAs (four accumulation chains), the softmax
-// and the P x V MFMAs.  32x32 layouts (lane l, n = l % 32, hh = l / 32):
+// 32-row form: 32 query rows per wavefront pair on 32x32x16 MFMAs, so every
+// K / V^T operand read from LDS feeds twice the arithmetic of the 16-row
+// form; the O^T accumulators (32 rows x 256 dims) and Q^T (32 x 256 fp16)
+// stay in registers, split between the pair.  32x32 layouts (lane l,
+// n = l % 32, hh = l / 32):
 //   A[m][k]: lane m + 32 (k / 8) holds element k % 8;  B[k][n] likewise;
 //   C[m][n]: lane n + 32 hh, register r <-> m = 8 (r / 4) + 4 hh + r % 4.
 // S^T = K Q^T (keys x rows); its C registers 8 s' .. 8 s' + 7 are the B
@@ -460,244 +460,30 @@ __device__ __forceinline__ f32x16 mfma3232(h8 a, h8 b, f32x16 c) {
 constexpr int KS2_LD = 256 + 8;   // halves per LDS K row
 constexpr int VS2_LD = KT + 4;    // halves per LDS V^T row
 
-// Pipelined over tiles: K / V^T tiles in a three-slot LDS ring, and the
-// scores of tile t + 1 are computed on the matrix cores while the vector ALU
-// does the softmax of tile t (MFMA and VALU instructions interleaved in issue
-// order, so the one wavefront per SIMD keeps both units busy).
 constexpr int NKB = 3;            // LDS tile slots
 // Lazy-rescale gap of the 32-row form: weights stay <= e^10 (< fp16 max).
 constexpr float GAP32 = 10.0f;
-#ifndef KHQ_PF_RS
-#define KHQ_PF_RS 1
-#endif
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void prefill_attn32_kernel(PrefillArgs a) {
-    __shared__ __align__(16) _Float16 ks[NKB][KT][KS2_LD];
-    __shared__ __align__(16) _Float16 vs[NKB][256][VS2_LD];
-    const int h = blockIdx.y;
-    const int tid = threadIdx.x;
-    const int wv = tid >> 6, lane = tid & 63;
-    const int ln = lane & 31, hh = lane >> 5;
-    const int n_rows = a.n_q * a.n_rep;
-    const int row0 = (blockIdx.x * 4 + wv) * 32;
-    const int split = blockIdx.z;
-    const int k_lo = split * a.keys_per_split;
-    const int k_hi = min(a.n_tot, k_lo + a.keys_per_split);
-    const int H_q = a.h_kv * a.n_rep;
-    const int r = row0 + ln;
-    const bool r_ok = r < n_rows;
-    const int jq = r_ok ? r / a.n_rep : 0;
-    const int hq = h * a.n_rep + (r_ok ? r % a.n_rep : 0);
-    const RowKeys vis(a, r_ok, jq);
-    const int b_last = min((int)blockIdx.x * 128 + 127, n_rows - 1);
-    const int kt_hi = min(k_hi, block_key_end(a, blockIdx.x * 128, b_last));
 
-    h8 qb[16];
-    {
-        const __half* qrow = a.q + ((size_t)jq * H_q + hq) * 512;
-#pragma unroll
-        for (int st = 0; st < 16; st++) {
-            const uint4 v = *reinterpret_cast<const uint4*>(qrow + 16 * st + 8 * hh);
-            qb[st] = __builtin_bit_cast(h8, r_ok ? v : uint4{0u, 0u, 0u, 0u});
-        }
-    }
-    f32x16 acc[8];
-#pragma unroll
-    for (int t = 0; t < 8; t++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) acc[t][e] = 0.0f;
-    float m_ref = -INFINITY, l_part = 0.0f;
-
-    // cooperative tile loads: thread t -> K key t / 8, 64 B at (t % 8) * 32
-    // halves; V^T dim t, the tile's 32 keys (64 B)
-    const int ld_key = tid >> 3, ld_off = (tid & 7) * 32;
-    const __half* kg = a.k + (size_t)h * 256 + ld_off;
-    const __half* vg = a.vt + ((size_t)h * 256 + tid) * a.ld_vt;
-    uint4 pk[4], pv[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) pk[i] = pv[i] = uint4{0u, 0u, 0u, 0u};
-    auto gload = [&](int k0) {
-        const int key = min(k0 + ld_key, a.n_tot - 1);
-        const uint4* ksrc = reinterpret_cast<const uint4*>(kg + (size_t)key * a.h_kv * 256);
-        const uint4* vsrc = reinterpret_cast<const uint4*>(vg + k0);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            pk[i] = ksrc[i];
-            pv[i] = vsrc[i];
-        }
-    };
-    auto vmask = [](uint32_t w, int i, int nv) {
-        return 2 * i + 1 < nv ? w : (2 * i < nv ? (w & 0xFFFFu) : 0u);
-    };
-    auto lstore = [&](int buf, int k0) {
-        const int nv = a.n_tot - k0;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            *reinterpret_cast<uint4*>(&ks[buf][ld_key][ld_off + 8 * i]) = pk[i];
-            *reinterpret_cast<uint2*>(&vs[buf][tid][8 * i]) = uint2{pv[i].x, pv[i].y};
-            *reinterpret_cast<uint2*>(&vs[buf][tid][8 * i + 4]) = uint2{pv[i].z, pv[i].w};
-        }
-        if (nv < KT) {  // the key space's last tile: V^T columns past n_tot cleared (uniform branch)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint4 v = pv[i];
-                *reinterpret_cast<uint2*>(&vs[buf][tid][8 * i]) =
-                    uint2{vmask(v.x, 4 * i, nv), vmask(v.y, 4 * i + 1, nv)};
-                *reinterpret_cast<uint2*>(&vs[buf][tid][8 * i + 4]) =
-                    uint2{vmask(v.z, 4 * i + 2, nv), vmask(v.w, 4 * i + 3, nv)};
-            }
-        }
-    };
-    // S^T of the tile in slot buf: 16 MFMAs in two accumulation chains
-    auto kread = [&](int buf, int half, h8 (&kop)[8]) {
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            kop[i] = *reinterpret_cast<const h8*>(&ks[buf][ln][16 * (8 * half + i) + 8 * hh]);
-    };
-
-    const int n_tiles = k_lo < kt_hi ? (kt_hi - k_lo + KT - 1) / KT : 0;
-    if (n_tiles > 0) {
-        gload(k_lo);
-        lstore(0, k_lo);
-    }
-    if (n_tiles > 1) {
-        gload(k_lo + KT);
-        lstore(1, k_lo + KT);
-    }
-    if (n_tiles > 2) gload(k_lo + 2 * KT);
-    __syncthreads();
-    const f32x16 zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    f32x16 s2[2];
-    {
-        h8 kop[8];
-        s2[0] = s2[1] = zero16;
-#pragma unroll
-        for (int half = 0; half < 2; half++) {
-            kread(0, half, kop);
-#pragma unroll
-            for (int i = 0; i < 8; i++) s2[i & 1] = mfma3232(kop[i], qb[8 * half + i], s2[i & 1]);
-        }
-    }
-    for (int t = 0; t < n_tiles; t++) {
-        const int cur = t % NKB, nxt = (t + 1) % NKB;
-        const int k0 = k_lo + t * KT;
-        // ---- the scores of tile t out of the accumulators, whose registers
-        // then take tile t + 1 (on the last tile: a slot's stale data, unused)
-        float sc[16];
-#pragma unroll
-        for (int e = 0; e < 16; e++) sc[e] = s2[0][e] + s2[1][e];
-        h8 kop[8];
-        kread(nxt, 0, kop);
-        // ---- S(t + 1), first half, under the mask and row maximum of tile t
-        float lmax = -INFINITY;
-        {
-            const uint32_t mb = vis.tile(k0) >> (4 * hh);
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                s2[i & 1] = mfma3232(kop[i], qb[i], i < 2 ? zero16 : s2[i & 1]);
-#pragma unroll
-                for (int e = 2 * i; e < 2 * i + 2; e++) {  // key k0 + 8 (e / 4) + 4 hh + e % 4
-                    sc[e] = (mb >> (8 * (e >> 2) + (e & 3))) & 1u ? sc[e] * a.sc : -INFINITY;
-                    lmax = fmaxf(lmax, sc[e]);
-                }
-            }
-        }
-        kread(nxt, 1, kop);
-        // ---- raise the row's reference maximum only when needed (the row's
-        // keys sit in lanes l and l ^ 32)
-        if (__ballot(lmax > m_ref + GAP32) != 0ull) {
-            const float rmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
-            const float m_new = fmaxf(m_ref, rmax);
-            if (m_new > m_ref) {
-                // before the first visible key every accumulator is still zero
-                if (__ballot(m_ref != -INFINITY) != 0ull) {
-                    const float fac = __expf(m_ref - m_new);  // 0 when m_ref = -inf
-#pragma unroll
-                    for (int t2 = 0; t2 < 8; t2++) acc[t2] *= fac;
-                    l_part *= fac;
-                }
-                m_ref = m_new;
-            }
-        }
-        // ---- S(t + 1), second half, under the weights of tile t
-        h8 pb[2];
-        {
-            float p[16];
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                s2[i & 1] = mfma3232(kop[i], qb[8 + i], s2[i & 1]);
-#pragma unroll
-                for (int e = 2 * i; e < 2 * i + 2; e++) {
-                    const float x = sc[e];
-                    p[e] = x == -INFINITY ? 0.0f : __expf(x - m_ref);
-                    l_part += p[e];
-                }
-            }
-#pragma unroll
-            for (int sp = 0; sp < 2; sp++)
-                pb[sp] = __builtin_bit_cast(h8, uint4{pk_rne(p[8 * sp], p[8 * sp + 1]),
-                                                      pk_rne(p[8 * sp + 2], p[8 * sp + 3]),
-                                                      pk_rne(p[8 * sp + 4], p[8 * sp + 5]),
-                                                      pk_rne(p[8 * sp + 6], p[8 * sp + 7])});
-        }
-        // ---- O^T += V^T P^T: 8 tiles of 32 dims x 2 K-steps of 16 keys; each
-        // K-step's 8 operand reads issued before its MFMAs
-#pragma unroll
-        for (int sp = 0; sp < 2; sp++) {
-            h8 vop[8];
-#pragma unroll
-            for (int t2 = 0; t2 < 8; t2++) {
-                const uint2 va = *reinterpret_cast<const uint2*>(&vs[cur][32 * t2 + ln][16 * sp + 4 * hh]);
-                const uint2 vb = *reinterpret_cast<const uint2*>(&vs[cur][32 * t2 + ln][16 * sp + 8 + 4 * hh]);
-                vop[t2] = __builtin_bit_cast(h8, uint4{va.x, va.y, vb.x, vb.y});
-            }
-#pragma unroll
-            for (int t2 = 0; t2 < 8; t2++) acc[t2] = mfma3232(vop[t2], pb[sp], acc[t2]);
-        }
-        // ---- stage tile t + 2 (its slot last held tile t - 1), load t + 3
-        if (t + 2 < n_tiles) {
-            lstore((t + 2) % NKB, k0 + 2 * KT);
-            if (t + 3 < n_tiles) gload(k0 + 3 * KT);
-        }
-        __syncthreads();
-    }
-    // ---- partial triple of row ln (dims 32 t + 8 j + 4 hh + c)
-    const float l_row = l_part + __shfl_xor(l_part, 32, 64);
-    if (r_ok) {
-        float* out = a.part + ((size_t)(jq * H_q + hq) * a.n_split + split) * 258;
-        const bool empty = (m_ref == -INFINITY);
-#pragma unroll
-        for (int t2 = 0; t2 < 8; t2++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const f4 v = f4{acc[t2][4 * j], acc[t2][4 * j + 1], acc[t2][4 * j + 2], acc[t2][4 * j + 3]};
-                *reinterpret_cast<f4*>(&out[32 * t2 + 8 * j + 4 * hh]) = empty ? f4{0.f, 0.f, 0.f, 0.f} : v;
-            }
-        if (hh == 0) {
-            out[256] = empty ? -1e20f : m_ref;
-            out[257] = empty ? 0.0f : l_row;
-        }
-    }
-}
-
-// Role-specialised 32-row form: per SIMD a score wavefront and an output
-// wavefront (8 wavefronts per block, 128 rows of one KV head).  The score
-// wavefront of row group g computes S^T = K Q^T (tile t + 1 on the matrix
-// cores under tile t's softmax, as above), turns tile t into P^T (fp16, already
-// the B operand layout of O^T += V^T P^T) and the per-row rescale factor, and
-// leaves both in LDS; the output wavefront of g applies tile t one tile later
-// (rescale, then 16 MFMAs).  Each needs about half the registers of the
-// single-wavefront form, so the two share a SIMD and one's vector work runs
-// under the other's matrix work.  The score side stages the K tiles, the
-// output side the V^T tiles, in the three-slot ring; one block barrier per
-// tile orders all of it (every wavefront passes the same barriers).
+// Role-specialised 32-row attention: per SIMD a score wavefront and an
+// output wavefront (8 wavefronts per block, 128 rows of one KV head).  The
+// score wavefront of row group g computes S^T = K Q^T (tile t + 1 on the
+// matrix cores while tile t is masked, scaled and its row maximum taken),
+// decides whether the row's reference maximum rises (rescale factor fac) and
+// leaves tile t's masked scores with (max, fac) in LDS; the output wavefront
+// of g, one tile behind, rescales its accumulators and row sums by fac,
+// forms P = exp(s - max) as fp16 (the C layout of S^T is the B operand layout
+// of O^T += V^T P^T) and applies the tile with 16 MFMAs.  Each role needs
+// about half the registers of one wavefront doing both, so the two share a
+// SIMD and one's vector work runs under the other's matrix work.  The score
+// side stages the K tiles and the output side the V^T tiles in the
+// three-slot ring; one block barrier per tile orders all of it (every
+// wavefront passes the same barriers).
 __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_attn_rs_kernel(PrefillArgs a) {
     __shared__ __align__(16) _Float16 ks[NKB][KT][KS2_LD];
     __shared__ __align__(16) _Float16 vs[NKB][256][VS2_LD];
-    __shared__ __align__(16) uint4 psl[2][4][2][64];  // P^T operands (slot, row group, half, lane)
-    __shared__ float pfac[2][4][64];                   // rescale factor (slot, row group, lane)
-    __shared__ float2 pml[4][64];                      // final (max, sum) (row group, lane)
+    __shared__ __align__(16) f4 pss[2][4][4][64];     // masked scaled scores (slot, row group, quad, lane)
+    __shared__ float2 pmf[2][4][64];                   // (reference max, rescale factor) per slot
     const int h = blockIdx.y;
     const int tid = threadIdx.x;
     const int wv = tid >> 6, lane = tid & 63;
@@ -763,7 +549,7 @@ void prefill_attn_rs_kernel(PrefillArgs a) {
         }
         if (n_tiles > 2) gload(k_lo + 2 * KT);
         __syncthreads();  // prologue: K tiles 0, 1 and V^T tile 0 staged
-        float m_ref = -INFINITY, l_part = 0.0f;
+        float m_ref = -INFINITY;
         f32x16 s2[2];
         {
             h8 kop[8];
@@ -799,41 +585,23 @@ void prefill_attn_rs_kernel(PrefillArgs a) {
             }
             kread(nxt, 1, kop);
             // ---- raise the row's reference maximum only when needed; the
-            // output wavefront rescales its accumulators by fac first
+            // output wavefront rescales its accumulators and sums by fac
             float fac = 1.0f;
             if (__ballot(lmax > m_ref + GAP32) != 0ull) {
                 const float rmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
                 const float m_new = fmaxf(m_ref, rmax);
                 if (m_new > m_ref) {
                     fac = __expf(m_ref - m_new);  // 0 when m_ref = -inf (the sums are still 0)
-                    l_part *= fac;
                     m_ref = m_new;
                 }
             }
-            // ---- S(t + 1), second half, under the weights of tile t
-            h8 pb[2];
-            {
-                float p[16];
+            // ---- S(t + 1), second half; tile t's scores go to the output side
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    s2[i & 1] = mfma3232(kop[i], qb[8 + i], s2[i & 1]);
+            for (int i = 0; i < 8; i++) s2[i & 1] = mfma3232(kop[i], qb[8 + i], s2[i & 1]);
 #pragma unroll
-                    for (int e = 2 * i; e < 2 * i + 2; e++) {
-                        const float x = sc[e];
-                        p[e] = x == -INFINITY ? 0.0f : __expf(x - m_ref);
-                        l_part += p[e];
-                    }
-                }
-#pragma unroll
-                for (int sp = 0; sp < 2; sp++)
-                    pb[sp] = __builtin_bit_cast(h8, uint4{pk_rne(p[8 * sp], p[8 * sp + 1]),
-                                                          pk_rne(p[8 * sp + 2], p[8 * sp + 3]),
-                                                          pk_rne(p[8 * sp + 4], p[8 * sp + 5]),
-                                                          pk_rne(p[8 * sp + 6], p[8 * sp + 7])});
-            }
-            psl[t & 1][rg][0][lane] = __builtin_bit_cast(uint4, pb[0]);
-            psl[t & 1][rg][1][lane] = __builtin_bit_cast(uint4, pb[1]);
-            pfac[t & 1][rg][lane] = fac;
+            for (int q4 = 0; q4 < 4; q4++)
+                pss[t & 1][rg][q4][lane] = f4{sc[4 * q4], sc[4 * q4 + 1], sc[4 * q4 + 2], sc[4 * q4 + 3]};
+            pmf[t & 1][rg][lane] = float2{m_ref, fac};
             // ---- stage K tile t + 2 (its slot last held tile t - 1), load t + 3
             if (t + 2 < n_tiles) {
                 lstore((t + 2) % NKB);
@@ -842,9 +610,6 @@ void prefill_attn_rs_kernel(PrefillArgs a) {
             __syncthreads();  // tile t
         }
         __syncthreads();  // the output side's last tile
-        const float l_row = l_part + __shfl_xor(l_part, 32, 64);
-        pml[rg][lane] = float2{m_ref, l_row};
-        __syncthreads();  // (max, sum) in place
     } else {
         // ================= output wavefront
         f32x16 acc[8];
@@ -882,15 +647,34 @@ void prefill_attn_rs_kernel(PrefillArgs a) {
             }
         };
         // O^T += V^T P^T for tile u: 8 tiles of 32 dims x 2 K-steps of 16 keys
+        float l_part = 0.0f, m_last = -INFINITY;
         auto pv_tile = [&](int u) {
             const int cur = u % NKB;
-            const h8 pb0 = __builtin_bit_cast(h8, psl[u & 1][rg][0][lane]);
-            const h8 pb1 = __builtin_bit_cast(h8, psl[u & 1][rg][1][lane]);
-            const float fac = pfac[u & 1][rg][lane];
-            if (__ballot(fac != 1.0f) != 0ull) {
+            const float2 mf = pmf[u & 1][rg][lane];
+            const f4 s0 = pss[u & 1][rg][0][lane], s1 = pss[u & 1][rg][1][lane];
+            const f4 s2v = pss[u & 1][rg][2][lane], s3 = pss[u & 1][rg][3][lane];
+            const float sc[16] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3],
+                                  s2v[0], s2v[1], s2v[2], s2v[3], s3[0], s3[1], s3[2], s3[3]};
+            m_last = mf.x;
+            if (__ballot(mf.y != 1.0f) != 0ull) {
 #pragma unroll
-                for (int t2 = 0; t2 < 8; t2++) acc[t2] *= fac;
+                for (int t2 = 0; t2 < 8; t2++) acc[t2] *= mf.y;
+                l_part *= mf.y;
             }
+            float p[16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                p[e] = sc[e] == -INFINITY ? 0.0f : __expf(sc[e] - mf.x);
+                l_part += p[e];
+            }
+            h8 pbv[2];
+#pragma unroll
+            for (int sp = 0; sp < 2; sp++)
+                pbv[sp] = __builtin_bit_cast(h8, uint4{pk_rne(p[8 * sp], p[8 * sp + 1]),
+                                                       pk_rne(p[8 * sp + 2], p[8 * sp + 3]),
+                                                       pk_rne(p[8 * sp + 4], p[8 * sp + 5]),
+                                                       pk_rne(p[8 * sp + 6], p[8 * sp + 7])});
+            const h8 pb0 = pbv[0], pb1 = pbv[1];
 #pragma unroll
             for (int sp = 0; sp < 2; sp++) {
                 h8 vop[8];
@@ -921,10 +705,10 @@ void prefill_attn_rs_kernel(PrefillArgs a) {
         }
         if (n_tiles > 0) pv_tile(n_tiles - 1);
         __syncthreads();  // last tile applied
-        __syncthreads();  // (max, sum) in place
+        const float l_row = l_part + __shfl_xor(l_part, 32, 64);
         // ---- partial triple of row ln (dims 32 t + 8 j + 4 hh + c)
         if (r_ok) {
-            const float2 ml = pml[rg][lane];
+            const float2 ml = float2{m_last, l_row};
             float* out = a.part + ((size_t)(jq * H_q + hq) * a.n_split + split) * 258;
             const bool empty = (ml.x == -INFINITY);
 #pragma unroll
@@ -1060,13 +844,13 @@ hipError_t launch_ring_gather(const GatherArgs& a, hipStream_t st) {
 namespace {
 // Few query rows (a handful of queries, e.g. the one after a compression
 // event): the 16-row kernel, two blocks per CU (more, shorter splits); many:
-// the 32-row kernel (half the LDS operand traffic per flop).
+// the role-specialised 32-row kernel (half the LDS operand traffic per flop).
 bool few_rows(int n_rows) { return n_rows <= 128; }
 }  // namespace
 
 int prefill_splits(int n_q, int n_rep, int h_kv, int n_k, int* keys_per_split) {
     // Blocks that run at once: 2 per CU for the 16-row kernel (72 KB of LDS
-    // each), 1 for the 32-row kernel (registers).  The split count fills that
+    // each), 1 for the 32-row kernel (142 KB).  The split count fills that
     // many slots in one round: a few blocks past a round cost a whole round.
     static int n_cu = 0;
     if (n_cu == 0) {
@@ -1096,12 +880,9 @@ hipError_t launch_prefill_attn(const PrefillArgs& a, hipStream_t st) {
         const int mtiles = (n_rows + 15) / 16;
         hipLaunchKernelGGL(pf::prefill_attn_kernel, dim3((mtiles + 3) / 4, a.h_kv, a.n_split),
                            dim3(256), 0, st, a);
-    } else if (KHQ_PF_RS) {
+    } else {
         hipLaunchKernelGGL(pf::prefill_attn_rs_kernel, dim3((n_rows + 127) / 128, a.h_kv, a.n_split),
                            dim3(512), 0, st, a);
-    } else {
-        hipLaunchKernelGGL(pf::prefill_attn32_kernel, dim3((n_rows + 127) / 128, a.h_kv, a.n_split),
-                           dim3(256), 0, st, a);
     }
     return hipGetLastError();
 }
