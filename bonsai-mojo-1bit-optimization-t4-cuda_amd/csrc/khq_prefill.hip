@@ -650,6 +650,17 @@ void prefill_attn_rs_kernel(PrefillArgs a) {
         float l_part = 0.0f, m_last = -INFINITY;
         auto pv_tile = [&](int u) {
             const int cur = u % NKB;
+            // the tile's V^T operands first: their LDS latency runs under the
+            // exponentials below
+            h8 vop[2][8];
+#pragma unroll
+            for (int sp = 0; sp < 2; sp++)
+#pragma unroll
+                for (int t2 = 0; t2 < 8; t2++) {
+                    const uint2 va = *reinterpret_cast<const uint2*>(&vs[cur][32 * t2 + ln][16 * sp + 4 * hh]);
+                    const uint2 vb = *reinterpret_cast<const uint2*>(&vs[cur][32 * t2 + ln][16 * sp + 8 + 4 * hh]);
+                    vop[sp][t2] = __builtin_bit_cast(h8, uint4{va.x, va.y, vb.x, vb.y});
+                }
             const float2 mf = pmf[u & 1][rg][lane];
             const f4 s0 = pss[u & 1][rg][0][lane], s1 = pss[u & 1][rg][1][lane];
             const f4 s2v = pss[u & 1][rg][2][lane], s3 = pss[u & 1][rg][3][lane];
@@ -674,19 +685,10 @@ void prefill_attn_rs_kernel(PrefillArgs a) {
                                                        pk_rne(p[8 * sp + 2], p[8 * sp + 3]),
                                                        pk_rne(p[8 * sp + 4], p[8 * sp + 5]),
                                                        pk_rne(p[8 * sp + 6], p[8 * sp + 7])});
-            const h8 pb0 = pbv[0], pb1 = pbv[1];
 #pragma unroll
-            for (int sp = 0; sp < 2; sp++) {
-                h8 vop[8];
+            for (int sp = 0; sp < 2; sp++)
 #pragma unroll
-                for (int t2 = 0; t2 < 8; t2++) {
-                    const uint2 va = *reinterpret_cast<const uint2*>(&vs[cur][32 * t2 + ln][16 * sp + 4 * hh]);
-                    const uint2 vb = *reinterpret_cast<const uint2*>(&vs[cur][32 * t2 + ln][16 * sp + 8 + 4 * hh]);
-                    vop[t2] = __builtin_bit_cast(h8, uint4{va.x, va.y, vb.x, vb.y});
-                }
-#pragma unroll
-                for (int t2 = 0; t2 < 8; t2++) acc[t2] = mfma3232(vop[t2], sp ? pb1 : pb0, acc[t2]);
-            }
+                for (int t2 = 0; t2 < 8; t2++) acc[t2] = mfma3232(vop[sp][t2], pbv[sp], acc[t2]);
         };
         if (n_tiles > 0) {
             gload(k_lo);
