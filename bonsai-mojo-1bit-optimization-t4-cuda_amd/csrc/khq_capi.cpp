@@ -637,7 +637,16 @@ int khq_prefill_attn_fp16(const void* q_gate, const void* k, const void* vt, int
     if (!q_gate || !k || !vt || !out) return -100;
     return khq::prefill_attn_run(static_cast<const __half*>(q_gate), static_cast<const __half*>(k),
                                  static_cast<const __half*>(vt), ld_vt, n_k, n_q, vis0, H_q, H_kv,
-                                 scale, static_cast<__half*>(out), stream, 0, 0, 0, 0, 0);
+                                 scale, static_cast<__half*>(out), stream, 0, 0, 0, 0, 0, true);
+}
+
+int khq_prefill_attn_partials_fp16(const void* q_gate, const void* k, const void* vt, int ld_vt,
+                                   int n_k, int n_q, int vis0, int H_q, int H_kv, float scale,
+                                   hipStream_t stream) {
+    if (!q_gate || !k || !vt) return -100;
+    return khq::prefill_attn_run(static_cast<const __half*>(q_gate), static_cast<const __half*>(k),
+                                 static_cast<const __half*>(vt), ld_vt, n_k, n_q, vis0, H_q, H_kv,
+                                 scale, nullptr, stream, 0, 0, 0, 0, 0, false);
 }
 
 int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centroids_k,
@@ -809,7 +818,8 @@ namespace khq {
 
 int prefill_attn_run(const __half* q_gate, const __half* k, const __half* vt, int ld_vt, int n_k,
                      int n_q, int vis0, int H_q, int H_kv, float scale, __half* out,
-                     hipStream_t stream, int q_b, int hole_lo, int hole_hi, int ex_lo, int ex_hi) {
+                     hipStream_t stream, int q_b, int hole_lo, int hole_hi, int ex_lo, int ex_hi,
+                     bool merge) {
     if (n_k <= 0 || n_q <= 0 || vis0 < 1) return -100;
     if (q_b < 0 || q_b > n_q || hole_lo < 0 || hole_hi < hole_lo || hole_hi > n_k ||
         ex_hi < ex_lo || (ex_hi > ex_lo && ex_lo < n_k) ||
@@ -846,7 +856,7 @@ int prefill_attn_run(const __half* q_gate, const __half* k, const __half* vt, in
     a.ex_lo = ex_lo;
     a.ex_hi = ex_hi;
     e = launch_prefill_attn(a, stream);
-    if (e != hipSuccess) return rc_of(e);
+    if (e != hipSuccess || !merge) return rc_of(e);
     return rc_of(launch_prefill_merge(ws, q_gate, out, n_q * H_q, ns, 1e-8f, stream));
 }
 

@@ -227,10 +227,12 @@ hipError_t launch_compress_decode(const CompressJob& k, const CompressJob& v, co
 int prefill_splits(int n_q, int n_rep, int h_kv, int n_k, int* keys_per_split);
 hipError_t launch_prefill_attn(const PrefillArgs& a, hipStream_t st);
 // Prefill attention plus merge and gate through the shared workspace; the
-// hole / extra ranges as in PrefillArgs (all zero: plain causal prefill).
+// hole / extra ranges as in PrefillArgs (all zero: plain causal prefill);
+// merge = false: the attention launch alone (partials left in the workspace).
 int prefill_attn_run(const __half* q_gate, const __half* k, const __half* vt, int ld_vt, int n_k,
                      int n_q, int vis0, int H_q, int H_kv, float scale, __half* out,
-                     hipStream_t stream, int q_b, int hole_lo, int hole_hi, int ex_lo, int ex_hi);
+                     hipStream_t stream, int q_b, int hole_lo, int hole_hi, int ex_lo, int ex_hi,
+                     bool merge = true);
 // Merge of n_split partial triples per row, / (den + eps), sigmoid gate from
 // q_gate row r (f16 [r][512], gate at 256..511): out f16 [r][256].
 hipError_t launch_prefill_merge(const float* part, const __half* q_gate, __half* out, int n_rows,

@@ -35,6 +35,7 @@ SIGNATURES = {
     "khq_attn_step_batched_fp16": [P, I] + [P] * 7 + [I, I, F, F, F, F, P],
     "khq_decompress_fp16": [P] * 15 + [I, I, I, I, F, F, F, P, I, P, I, P],
     "khq_prefill_attn_fp16": [P, P, P, I, I, I, I, I, I, F, P, P],
+    "khq_prefill_attn_partials_fp16": [P, P, P, I, I, I, I, I, I, F, P],
     "khq_attn_partials_fp16": [P] * 16 + [I, I, I, F, F, F, F, P],
     "khq_attn_parts": [I],
     "khq_select_kernel": [I],

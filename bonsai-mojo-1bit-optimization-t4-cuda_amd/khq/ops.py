@@ -249,6 +249,17 @@ def prefill_attn(q_gate, k, vt, out, *, ld_vt: int, n_k: int, n_q: int, vis0: in
                 H_q, H_kv, scale, ptr(out), stream_handle(stream), check=check)
 
 
+def prefill_attn_partials(q_gate, k, vt, *, ld_vt: int, n_k: int, n_q: int, vis0: int, H_q: int,
+                          H_kv: int, scale: float, check: bool = True, stream=None) -> int:
+    """khq_prefill_attn_partials_fp16: the prefill attention kernel alone
+    (split partials into the library workspace; profiling)."""
+    _need(q_gate, torch.float16, n_q * H_q * 2 * D, "q_gate")
+    _need(k, torch.float16, n_k * H_kv * D, "k")
+    _need(vt, torch.float16, H_kv * D * ld_vt, "vt")
+    return call("khq_prefill_attn_partials_fp16", ptr(q_gate), ptr(k), ptr(vt), ld_vt, n_k, n_q,
+                vis0, H_q, H_kv, scale, stream_handle(stream), check=check)
+
+
 def attn_partials(q_gate, pay: Payload, cents: Centroids, *, H_q: int, H_kv: int, c_len: int,
                   scale: float, rope_base: float = 1e7, stream=None) -> int:
     """khq_attn_partials_fp16: the compressed-region kernel alone (profiling)."""

@@ -203,6 +203,12 @@ int khq_decompress_fp16(const void* k_payload, const void* v_payload, const void
 int khq_prefill_attn_fp16(const void* q_gate, const void* k, const void* vt, int ld_vt, int n_k,
                           int n_q, int vis0, int H_q, int H_kv, float scale, void* out,
                           hipStream_t stream);
+/* Profiling entry (no reference counterpart): launches only the attention
+ * kernel of khq_prefill_attn_fp16 (split partials into the library
+ * workspace, nothing merged), so its duration can be timed on its own. */
+int khq_prefill_attn_partials_fp16(const void* q_gate, const void* k, const void* vt, int ld_vt,
+                                   int n_k, int n_q, int vis0, int H_q, int H_kv, float scale,
+                                   hipStream_t stream);
 
 /* khq_attn_step_batched_fp16 copies its per-sequence arguments from host
  * staging memory on every call, so it returns -105 on a stream under HIP

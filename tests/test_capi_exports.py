@@ -20,7 +20,7 @@ def declared():
 
 def test_header_symbols_exported():
     names = declared()
-    assert "launch_khq_attn_fp16" in names and len(names) == 41
+    assert "launch_khq_attn_fp16" in names and len(names) == 42
     lib = ctypes.CDLL(LIB_PATH)
     for n in names:
         assert hasattr(lib, n), n
