@@ -161,6 +161,33 @@ def test_layer_prefill_matches_steps(device):
         close(got[j], want[j])
 
 
+def test_prefill_attn_rescales_vs_float64(device):
+    """Keys whose magnitude ramps up along the sequence: the row maxima rise by
+    more than the lazy-rescale gap several times within a split, so the
+    output side applies the rescale factors the score side hands over (the
+    32-row role-specialised kernel: 40 queries x 6 heads = 240 rows)."""
+    n_k, n_q, vis0 = 640, 40, 601
+    rng = np.random.default_rng(61)
+    ramp = (1.0 + np.arange(n_k) / 24.0).astype(np.float32)[:, None, None]
+    K = (rng.standard_normal((n_k, H_KV, D)) * 0.5 * ramp).astype(np.float16)
+    V = rng.standard_normal((n_k, H_KV, D)).astype(np.float16)
+    q = rng.standard_normal((n_q, H_Q, 2 * D)).astype(np.float16)
+    ld = ops.vt_ld(n_k)
+    vt = np.zeros((H_KV, D, ld), np.float16)
+    vt[:, :, :n_k] = V.transpose(1, 2, 0)
+    out = torch.zeros((n_q, H_Q, D), device=device, dtype=torch.float16)
+    ops.prefill_attn(t(q), t(K), t(vt), out, ld_vt=ld, n_k=n_k, n_q=n_q, vis0=vis0, H_q=H_Q,
+                     H_kv=H_KV, scale=SCALE)
+    torch.cuda.synchronize()
+    Kd = K.astype(np.float64)
+    want = _dense_reference(q, Kd, V.astype(np.float64), vis0, n_k)
+    # the test is meaningful only if the maxima rise by more than the gap
+    s_first = Kd[:32, 0, :] @ q[0, 0, :D].astype(np.float64) * SCALE
+    s_all = Kd[:vis0, 0, :] @ q[0, 0, :D].astype(np.float64) * SCALE
+    assert s_all.max() - s_first.max() > 10.0
+    close(out.cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("chunks", [(128,) * 6, (1, 5, 250, 128, 100, 216)])
 def test_layer_prefill_decoded_rows_match_decode(device, chunks):
     """The dense key space a layer's prefills build (compression events that
