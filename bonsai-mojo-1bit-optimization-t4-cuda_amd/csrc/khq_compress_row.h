@@ -146,8 +146,13 @@ __device__ __forceinline__ void compress_block(
     for (int c = 0; c < 4; c++)
         cbk[c] = is_v ? h2f(cents[(c & 1) * 256 + lane * 4 + 3]) : h2f(cents[2 * 256 + lane * 4 + c]);
 
+    // A V row's four wavefronts share one row: wavefront 0 computes its
+    // projection and hands it to the others through LDS (the search below
+    // is what needs all four).
+    __shared__ float s_pj[256];
+    const bool own_row = !is_v || wave == 0;  // uniform per wavefront
     float xv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (valid) {
+    if (valid && own_row) {
         const __half* xr = x + (size_t)row * 256 + lane * 4;
 #pragma unroll
         for (int c = 0; c < 4; c++) xv[c] = h2f(xr[c]);
@@ -156,17 +161,17 @@ __device__ __forceinline__ void compress_block(
     for (int c = 0; c < 4; c++) s_a[wave][lane * 4 + c] = xv[c];
     if (lane < 32) s_w[wave][lane] = 0u;
     __syncthreads();
-    const float sum_sq = fold_sq256(s_a[wave]);
-    const float norm = sqrtf(sum_sq + 1e-8f);
-    if (live && lane == 0) out_norms[row] = __float2half(norm);
+    float norm = 0.0f;
+    float proj[4] = {0.f, 0.f, 0.f, 0.f};
+    if (own_row) {
+        const float sum_sq = fold_sq256(s_a[wave]);
+        norm = sqrtf(sum_sq + 1e-8f);
+        if (live && lane == 0) out_norms[row] = __float2half(norm);
 
-    float r[4];
+        float r[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) r[c] = (xv[c] * dv4[c]) / (norm + 1e-8f);
-    fwht256(r);
-
-    float proj[4];
-    {
+        for (int c = 0; c < 4; c++) r[c] = (xv[c] * dv4[c]) / (norm + 1e-8f);
+        fwht256(r);
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             float acc = r[0] * rot[0 * 4 + c];
@@ -175,8 +180,16 @@ __device__ __forceinline__ void compress_block(
             acc = fmaf(r[3], rot[3 * 4 + c], acc);
             proj[c] = acc * f_s;
         }
+        if (is_v) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) s_pj[lane * 4 + c] = proj[c];
+        }
     }
-    __syncthreads();  // s_a reused below
+    __syncthreads();  // s_a reused below; a V row's projection in place
+    if (is_v && wave != 0) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) proj[c] = s_pj[lane * 4 + c];
+    }
 
     if (!is_v) {
         // ---- K branch, ref .cu:1314-1351 and :1429-1466
