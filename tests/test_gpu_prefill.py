@@ -161,6 +161,36 @@ def test_layer_prefill_matches_steps(device):
         close(got[j], want[j])
 
 
+@pytest.mark.parametrize("H_q,H_kv,n_q,n_k", [(8, 2, 50, 520), (12, 1, 9, 200), (4, 4, 3, 97)])
+def test_prefill_attn_other_gqa_shapes_vs_float64(device, H_q, H_kv, n_q, n_k):
+    """Other GQA shapes through khq_prefill_attn_fp16 (rows = n_q x n_rep of
+    each KV head: 200 and 108 rows take the role-specialised 32-row kernel
+    and the 16-row kernel respectively) against float64 causal attention."""
+    rep = H_q // H_kv
+    rng = np.random.default_rng(H_q * 100 + n_q)
+    K = rng.standard_normal((n_k, H_kv, D)).astype(np.float16)
+    V = rng.standard_normal((n_k, H_kv, D)).astype(np.float16)
+    q = rng.standard_normal((n_q, H_q, 2 * D)).astype(np.float16)
+    vis0 = n_k - n_q + 1
+    ld = ops.vt_ld(n_k)
+    vt = np.zeros((H_kv, D, ld), np.float16)
+    vt[:, :, :n_k] = V.transpose(1, 2, 0)
+    out = torch.zeros((n_q, H_q, D), device=device, dtype=torch.float16)
+    ops.prefill_attn(t(q), t(K), t(vt), out, ld_vt=ld, n_k=n_k, n_q=n_q, vis0=vis0, H_q=H_q,
+                     H_kv=H_kv, scale=SCALE)
+    torch.cuda.synchronize()
+    qf, Kd, Vd = q.astype(np.float64), K.astype(np.float64), V.astype(np.float64)
+    want = np.zeros((n_q, H_q, D))
+    for j in range(n_q):
+        vis = min(n_k, vis0 + j)
+        for hq in range(H_q):
+            kv = hq // rep
+            sc = Kd[:vis, kv, :] @ qf[j, hq, :D] * SCALE
+            p = np.exp(sc - sc.max())
+            want[j, hq] = (p @ Vd[:vis, kv, :]) / (p.sum() + 1e-8) / (1.0 + np.exp(-qf[j, hq, D:]))
+    close(out.cpu().numpy(), want)
+
+
 def test_prefill_attn_rescales_vs_float64(device):
     """Keys whose magnitude ramps up along the sequence: the row maxima rise by
     more than the lazy-rescale gap several times within a split, so the
