@@ -304,6 +304,38 @@ def test_gather_q_bitexact(device):
     assert np.array_equal(out.cpu().numpy(), q[:, :D])
 
 
+@pytest.mark.parametrize("win", [1, 17, 200, 256])
+def test_c3_window_block_lengths(device, win):
+    """At C3's size the fused step computes the raw window in one block of the
+    decode launch (window_block_all: scores, softmax, P x V on the matrix
+    cores with hi + lo weights).  Window lengths 1 (one half empty), 17, 200
+    and 256 (the full ring) against the separate launches: compressed
+    partials, window partials (window_part_kernel, oracle-checked) and the
+    merge with gate."""
+    lc, h = layer_consts(layer_id=2)
+    c_len = 32640
+    rows = random_rows_np(c_len * H_KV, seed=5)
+    rng = np.random.default_rng(6 + win)
+    q = rng.standard_normal((H_Q, 2 * D)).astype(np.float16)
+    ring_k = t(rng.standard_normal((256, H_KV, D)).astype(np.float16))
+    ring_v = t(rng.standard_normal((256, H_KV, D)).astype(np.float16))
+    pay = payload_from_rows(rows, c_len * H_KV, device)
+    cents = cents_dev(lc, device)
+    ws = c_len % 256
+    out = torch.zeros((H_Q, D), device=device, dtype=torch.float16)
+    ops.attn_step(t(q), pay, cents, ring_k, ring_v, out, H_q=H_Q, H_kv=H_KV, c_len=c_len,
+                  win_start=ws, win_len=win, ring_cap=256, scale=SCALE)
+    ac = torch.zeros((H_Q, D + 2), device=device)
+    aw = torch.zeros((H_Q, D + 2), device=device)
+    want = torch.zeros_like(out)
+    ops.attn(t(q), pay, cents, ac, c_len=c_len, H_q=H_Q, H_kv=H_KV, scale=SCALE)
+    ops.window_attn(t(q), ring_k, ring_v, aw, win_start=ws, win_len=win, ring_cap=256, H_q=H_Q,
+                    H_kv=H_KV, scale=SCALE)
+    ops.merge_gate(ac, aw, t(q), want, H_q=H_Q, has_w=True)
+    torch.cuda.synchronize()
+    close(out.cpu().numpy(), want.cpu().numpy())
+
+
 def test_c3_full_size(device, kernel):
     """Config 3 at its real shape: 32,640 compressed + 128 raw, vs the oracle."""
     lc, h = layer_consts(layer_id=0)
