@@ -1386,7 +1386,7 @@ int launch_cal_svq_train(const void* v, const void* attn, const void* init_cb, c
         if (rc) return rc;
         sd[i].best = (float)(l[0] + l[1]);
     }
-    // round 1: up to 30 steps per seed; states restored to their best
+    // tournament stage 1: up to 30 steps per seed; states restored to their best
     const int r1 = std::min(iterations, 30), r2 = iterations - r1;
     float prox[3];
     for (int i = 0; i < n_seeds; i++) {
@@ -1398,7 +1398,7 @@ int launch_cal_svq_train(const void* v, const void* attn, const void* init_cb, c
     for (int i = 0; i < n_seeds; i++)
         for (int j = i + 1; j < n_seeds; j++)
             if (prox[order[j]] < prox[order[i]]) std::swap(order[i], order[j]);
-    // round 2: the remaining steps for every seed, best proxy first
+    // tournament stage 2: the remaining steps for every seed, best proxy first
     if (r2 > 0)
         for (int k = 0; k < n_seeds; k++) {
             Seed& s = sd[order[k]];
