@@ -1369,19 +1369,40 @@ size_t attn_ws_smem_bytes() { return sizeof(ws::Smem); }
 
 int g_spin_limit = 1 << 20;
 
-// Chunking of the compressed region: at most 255 chunks (one CU of a 256-CU
-// part left for the window block), each of the same whole number of tiles.
+static int device_cu_count() {
+    static int n_cu = 0;
+    if (n_cu == 0) {
+        int dev = 0, v = 0;
+        n_cu = (hipGetDevice(&dev) == hipSuccess &&
+                hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+                   ? v : 256;
+    }
+    return n_cu;
+}
+
+// Chunking of the compressed region: at most n_cu - 1 chunks (one CU left for
+// the window), each of the same whole number of tiles.  When that leaves no
+// room for the NWIN per-KV-head window blocks and the chunks are short (a
+// chunk of p tiles takes about 10 + 2.3 p us, the single all-heads window
+// block about 23 us), the cap drops to n_cu - NWIN so the four window blocks
+// run beside the chunks instead.
 int attn_ws_tiles_per_chunk(int c_len, int* n_chunks) {
-    static const int max_chunks = [] {
+    static const int env_max = [] {
         const char* e = getenv("KHQ_MAX_CHUNKS");
-        const int v = e ? atoi(e) : 0;
-        return v > 0 ? v : 255;
+        return e ? atoi(e) : 0;
     }();
+    const int n_cu = device_cu_count();
     const int tiles = (c_len + ws::TT - 1) / ws::TT;
-    int chunks = tiles < max_chunks ? tiles : max_chunks;
-    if (chunks < 1) chunks = 1;
-    const int per = (tiles + chunks - 1) / chunks;
-    *n_chunks = (tiles + per - 1) / per;
+    auto split = [tiles](int max_chunks, int* n) {
+        int chunks = tiles < max_chunks ? tiles : max_chunks;
+        if (chunks < 1) chunks = 1;
+        const int per = (tiles + chunks - 1) / chunks;
+        *n = (tiles + per - 1) / per;
+        return per;
+    };
+    if (env_max > 0) return split(env_max, n_chunks);
+    int per = split(n_cu > 1 ? n_cu - 1 : 1, n_chunks);
+    if (*n_chunks + ws::NWIN > n_cu && per <= 4 && n_cu > ws::NWIN) per = split(n_cu - ws::NWIN, n_chunks);
     return per;
 }
 
@@ -1415,13 +1436,7 @@ hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks, 
     }
     // four window blocks when they fit beside the chunks, else one (it is
     // hidden behind chunks of several tiles then)
-    static int n_cu = 0;
-    if (n_cu == 0) {
-        int dev = 0, v = 0;
-        n_cu = (hipGetDevice(&dev) == hipSuccess &&
-                hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-                   ? v : 256;
-    }
+    const int n_cu = device_cu_count();
     AttnArgs b = a;
     b.win_blocks = n_chunks + ws::NWIN <= n_cu ? ws::NWIN : 1;
     const int blocks = n_chunks + (a.win_len > 0 ? b.win_blocks : 0);

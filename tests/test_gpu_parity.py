@@ -336,6 +336,49 @@ def test_c3_window_block_lengths(device, win):
     close(out.cpu().numpy(), want.cpu().numpy())
 
 
+@pytest.mark.parametrize("c_len", [4064, 8128, 12160, 20320])
+def test_mid_context_chunking(device, c_len):
+    """Contexts whose one-CU-spare split would use 253..255 chunks: with chunks
+    of up to four tiles the split drops to at most n_cu - 4 chunks so the four
+    per-KV-head window blocks run beside them (4064, 8128, 12160 tokens); with
+    longer chunks (20320) it keeps n_cu - 1 chunks and the all-heads window
+    block.  The fused step against the separate launches."""
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    tiles = (c_len + 15) // 16
+    parts = ops.attn_parts(c_len)
+    per = -(-tiles // parts)
+    assert -(-tiles // per) == parts
+    if per <= 4:
+        assert parts + 4 <= n_cu, (c_len, parts)
+    else:
+        assert parts <= n_cu - 1
+    lc, h = layer_consts(layer_id=3)
+    rows = random_rows_np(c_len * H_KV, seed=c_len)
+    rng = np.random.default_rng(c_len + 1)
+    q = rng.standard_normal((H_Q, 2 * D)).astype(np.float16)
+    ring_k = t(rng.standard_normal((256, H_KV, D)).astype(np.float16))
+    ring_v = t(rng.standard_normal((256, H_KV, D)).astype(np.float16))
+    pay = payload_from_rows(rows, c_len * H_KV, device)
+    cents = cents_dev(lc, device)
+    ws = c_len % 256
+    out = torch.zeros((H_Q, D), device=device, dtype=torch.float16)
+    ops.attn_step(t(q), pay, cents, ring_k, ring_v, out, H_q=H_Q, H_kv=H_KV, c_len=c_len,
+                  win_start=ws, win_len=128, ring_cap=256, scale=SCALE)
+    ac = torch.zeros((H_Q, D + 2), device=device)
+    aw = torch.zeros((H_Q, D + 2), device=device)
+    want = torch.zeros_like(out)
+    ops.attn(t(q), pay, cents, ac, c_len=c_len, H_q=H_Q, H_kv=H_KV, scale=SCALE)
+    ops.window_attn(t(q), ring_k, ring_v, aw, win_start=ws, win_len=128, ring_cap=256, H_q=H_Q,
+                    H_kv=H_KV, scale=SCALE)
+    ops.merge_gate(ac, aw, t(q), want, H_q=H_Q, has_w=True)
+    torch.cuda.synchronize()
+    close(out.cpu().numpy(), want.cpu().numpy())
+    # the compressed partials alone against the oracle at the smallest size
+    if c_len == 4064:
+        st = dict(rows=rows, h=h, lc=lc, q_gate=q, c_len=c_len)
+        check_triple(ac.cpu().numpy(), oracle_attn(st)[1])
+
+
 def test_c3_full_size(device, kernel):
     """Config 3 at its real shape: 32,640 compressed + 128 raw, vs the oracle."""
     lc, h = layer_consts(layer_id=0)
