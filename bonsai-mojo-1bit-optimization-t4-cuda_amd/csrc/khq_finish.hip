@@ -24,11 +24,7 @@ __device__ __forceinline__ f2 ldg_f2(const float* p) {
     return *(const __attribute__((address_space(1))) f2*)p;
 }
 // Partial rows are 258 floats long, so a row's dims are only 8-byte aligned:
-// four floats are read as two 8-byte loads.
-__device__ __forceinline__ f4 ldg_f4(const float* p) {
-    const f2 a = ldg_f2(p), b = ldg_f2(p + 2);
-    return f4{a.x, a.y, b.x, b.y};
-}
+// they are read as 8-byte loads.
 
 constexpr int DS = 32;         // dims per block
 constexpr int MAX_WIN = 256;   // ring capacity bound
@@ -259,95 +255,97 @@ __global__ __launch_bounds__(256) void step_finish_batched_kernel(const FinishAr
         __half_as_ushort(__float2half(val));
 }
 
-// Merge-only form (the window is already a part): every wavefront of a
-// 256-thread block works alone on 8 dims of one query head.  Lane l takes
-// parts l, l + 64, ...: their (max, sum) pairs give the wavefront the
-// head's maximum and denominator, their 8-dim rows its numerators; a
-// reduce-scatter over the 64 lanes then leaves dim j of the 8 in the lanes
-// whose bits 3..5 spell j.  No block barrier; for n_parts <= 256 every
-// load is issued before the first value is used.
+// Merge-only form (the window is already a part): one 256-thread block per
+// (query head, 32-dim slice).  Lane l of wavefront w reads dims
+// d0 + 4 (l % 8) .. + 3 of part 64 w + 8 i + l / 8 (i = 0..7), so one load
+// instruction covers eight part rows, 128 contiguous bytes each, instead of
+// 64 rows at 8 bytes a lane.  The head's maximum crosses the wavefronts
+// through LDS; numerators and denominators sum over the eight part lanes
+// (xor 8 / 16 / 32), then over the four wavefronts.  For n_parts <= 256
+// every load is issued before the first value is used.
 __device__ __forceinline__ f2 ld_ml(const float* pp) { return ldg_f2(pp + 256); }
 
 __global__ __launch_bounds__(256) void step_merge_kernel(FinishArgs a) {
-    const int lane = threadIdx.x & 63;
+    __shared__ float s_m[4], s_den[4];
+    __shared__ f4 s_num[4][8];
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int sub = lane >> 3, c = lane & 7;
     const int hq = blockIdx.x;
-    const int d0 = blockIdx.y * 32 + (threadIdx.x >> 6) * 8;
+    const int d = blockIdx.y * 32 + 4 * c;
     const float* base = a.part + (size_t)hq * a.part_stride * 258;
     const int np = a.n_parts, last = max(np - 1, 0);
-    float num[8], den = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; j++) num[j] = 0.0f;
+    f4 num = f4{0.f, 0.f, 0.f, 0.f};
+    float den = 0.0f;
+    auto block_max = [&](float m) {
+        m = wave_max(m);
+        if (lane == 0) s_m[w] = m;
+        __syncthreads();
+        return fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+    };
     if (np <= 256) {
-        f2 ml[4];
-        f4 o[4][2];
+        f2 ml[8], o[8][2];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const float* pp = base + (size_t)min(lane + 64 * k, last) * 258;
-            ml[k] = ld_ml(pp);
-            o[k][0] = ldg_f4(pp + d0);
-            o[k][1] = ldg_f4(pp + d0 + 4);
+        for (int i = 0; i < 8; i++) {
+            const float* pp = base + (size_t)min(64 * w + 8 * i + sub, last) * 258;
+            ml[i] = ld_ml(pp);
+            o[i][0] = ldg_f2(pp + d);
+            o[i][1] = ldg_f2(pp + d + 2);
         }
-        float M = -3.0e38f;
+        float m = -3.0e38f;
 #pragma unroll
-        for (int k = 0; k < 4; k++) M = fmaxf(M, ml[k].x);
-        M = wave_max(M);
+        for (int i = 0; i < 8; i++)
+            if (64 * w + 8 * i + sub < np) m = fmaxf(m, ml[i].x);
+        const float M = block_max(m);
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const float w = lane + 64 * k < np ? __expf(ml[k].x - M) : 0.0f;
-            den = fmaf(ml[k].y, w, den);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                num[j] = fmaf(o[k][0][j], w, num[j]);
-                num[4 + j] = fmaf(o[k][1][j], w, num[4 + j]);
-            }
+        for (int i = 0; i < 8; i++) {
+            const float wt = 64 * w + 8 * i + sub < np ? __expf(ml[i].x - M) : 0.0f;
+            den = fmaf(ml[i].y, wt, den);
+            num[0] = fmaf(o[i][0].x, wt, num[0]);
+            num[1] = fmaf(o[i][0].y, wt, num[1]);
+            num[2] = fmaf(o[i][1].x, wt, num[2]);
+            num[3] = fmaf(o[i][1].y, wt, num[3]);
         }
     } else {
-        float M = -3.0e38f;
-        for (int p = lane; p < np; p += 64) M = fmaxf(M, base[(size_t)p * 258 + 256]);
-        M = wave_max(M);
-        for (int p = lane; p < np; p += 64) {
-            const float* pp = base + (size_t)p * 258;
-            const f2 ml = ld_ml(pp);
-            const f4 o0 = ldg_f4(pp + d0), o1 = ldg_f4(pp + d0 + 4);
-            const float w = __expf(ml.x - M);
-            den = fmaf(ml.y, w, den);
+        float m = -3.0e38f;
+        for (int p = t; p < np; p += 256) m = fmaxf(m, base[(size_t)p * 258 + 256]);
+        const float M = block_max(m);
+        for (int p = 64 * w + sub; p < np; p += 256)
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                num[j] = fmaf(o0[j], w, num[j]);
-                num[4 + j] = fmaf(o1[j], w, num[4 + j]);
+            for (int i = 0; i < 8; i++) {
+                const int q = p + 8 * i;
+                if (q < np) {
+                    const float* pp = base + (size_t)q * 258;
+                    const f2 mq = ld_ml(pp), o0 = ldg_f2(pp + d), o1 = ldg_f2(pp + d + 2);
+                    const float wt = __expf(mq.x - M);
+                    den = fmaf(mq.y, wt, den);
+                    num[0] = fmaf(o0.x, wt, num[0]);
+                    num[1] = fmaf(o0.y, wt, num[1]);
+                    num[2] = fmaf(o1.x, wt, num[2]);
+                    num[3] = fmaf(o1.y, wt, num[3]);
+                }
             }
-        }
     }
-    den = wave_sum(den);
-    // reduce-scatter: xor 32 keeps half (4 + 2 + 1 values), then sum the rest
-    const bool b5 = (lane & 32) != 0, b4 = (lane & 16) != 0, b3 = (lane & 8) != 0;
-    float k4[4], k2[2];
+    // sum over the eight part lanes of each dim group
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float keep = b5 ? num[4 + i] : num[i];
-        const float send = b5 ? num[i] : num[4 + i];
-        k4[i] = keep + xor_lane<32>(send);
+    for (int j = 0; j < 4; j++) {
+        num[j] += xor_lane<8>(num[j]);
+        num[j] += xor_lane<16>(num[j]);
+        num[j] += xor_lane<32>(num[j]);
     }
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const float keep = b4 ? k4[2 + i] : k4[i];
-        const float send = b4 ? k4[i] : k4[2 + i];
-        k2[i] = keep + xor_lane<16>(send);
-    }
-    float v;
-    {
-        const float keep = b3 ? k2[1] : k2[0];
-        const float send = b3 ? k2[0] : k2[1];
-        v = keep + xor_lane<8>(send);
-    }
-    v += xor_lane<1>(v);
-    v += xor_lane<2>(v);
-    v += xor_lane<4>(v);
-    if ((lane & 7) == 0) {
-        const int d = d0 + (lane >> 3);
-        const float g = __half2float(a.q[(size_t)hq * 512 + 256 + d]);
-        const float val = v / (den + a.eps) * (1.0f / (1.0f + expf(-g)));
-        a.out[(size_t)hq * 256 + d] = __float2half(val);
+    den += xor_lane<8>(den);
+    den += xor_lane<16>(den);
+    den += xor_lane<32>(den);
+    if (lane < 8) s_num[w][c] = num;
+    if (lane == 0) s_den[w] = den;
+    __syncthreads();
+    if (t < 32) {
+        const int g = t >> 2, j = t & 3;
+        const float v = (s_num[0][g][j] + s_num[1][g][j]) + (s_num[2][g][j] + s_num[3][g][j]);
+        const float D = (s_den[0] + s_den[1]) + (s_den[2] + s_den[3]);
+        const int dd = blockIdx.y * 32 + t;
+        const float gt = __half2float(a.q[(size_t)hq * 512 + 256 + dd]);
+        const float val = v / (D + a.eps) * (1.0f / (1.0f + expf(-gt)));
+        a.out[(size_t)hq * 256 + dd] = __float2half(val);
     }
 }
 
