@@ -1353,11 +1353,10 @@ __global__ __launch_bounds__(NTHR, 1) void attn_ws_kernel(AttnArgs a, int tiles_
 // Batched form: block b works on sequence map[b].x, chunk map[b].y (the
 // sequence's n_parts compressed chunks, then its window block).
 __global__ __launch_bounds__(NTHR, 1) void attn_ws_batched_kernel(const AttnArgs* __restrict__ args,
-                                                                  const int2* __restrict__ map,
-                                                                  int tiles_per_chunk) {
+                                                                  const int2* __restrict__ map) {
     const int2 m = map[blockIdx.x];
     const AttnArgs& a = args[m.x];  // read in place (a private copy would go to scratch)
-    ws_block(a, m.y, tiles_per_chunk, a.n_parts);
+    ws_block(a, m.y, a.chunk_tiles, a.n_parts);
 }
 
 }  // namespace ws
@@ -1448,7 +1447,7 @@ hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks, 
 }
 
 hipError_t launch_attn_ws_batched(const AttnArgs* args, const int2* map, int n_blocks,
-                                  int tiles_per_chunk, hipStream_t st) {
+                                  hipStream_t st) {
     static bool configured = false;
     const size_t smem = sizeof(ws::Smem);
     if (!configured) {
@@ -1458,7 +1457,7 @@ hipError_t launch_attn_ws_batched(const AttnArgs* args, const int2* map, int n_b
         configured = true;
     }
     hipLaunchKernelGGL(ws::attn_ws_batched_kernel, dim3(n_blocks), dim3(ws::NTHR), smem, st,
-                       args, map, tiles_per_chunk);
+                       args, map);
     return hipGetLastError();
 }
 

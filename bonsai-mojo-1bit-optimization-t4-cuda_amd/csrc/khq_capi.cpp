@@ -717,8 +717,13 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
     size_t part_floats = 0;
     std::vector<size_t> off(n_seq);
     std::vector<int> chunks(n_seq), np(n_seq);
+    // each sequence's chunks share its tiles evenly (at most per each): the
+    // longest chunk sets the launch's length, so no sequence keeps one full
+    // chunk and a short remainder
+    std::vector<int> ctiles(n_seq);
     for (int i = 0; i < n_seq; i++) {
         chunks[i] = (tiles[i] + per - 1) / per;
+        ctiles[i] = chunks[i] > 0 ? (tiles[i] + chunks[i] - 1) / chunks[i] : 1;
         np[i] = chunks[i] + (seqs[i].win_len > 0 ? 1 : 0);
         if (np[i] > 1024) return -100;  // finishing kernel's part limit
         off[i] = part_floats;
@@ -763,6 +768,7 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
         a.win_len = q.win_len;
         a.ring_cap = ring;
         a.win_blocks = 4;
+        a.chunk_tiles = ctiles[i];
         khq::fill_rope_table(a);
         a.spin_limit = khq::g_spin_limit;
         h_args[i] = a;
@@ -790,7 +796,7 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
         std::vector<std::pair<int, int2>> cb;
         for (int i = 0; i < n_seq; i++)
             for (int c = 0; c < chunks[i]; c++)
-                cb.push_back({std::min(per, tiles[i] - c * per), int2{i, c}});
+                cb.push_back({std::min(ctiles[i], tiles[i] - c * ctiles[i]), int2{i, c}});
         std::stable_sort(cb.begin(), cb.end(),
                          [](const std::pair<int, int2>& x, const std::pair<int, int2>& y) {
                              return x.first > y.first;
@@ -807,7 +813,7 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
     std::memcpy(h_meta.data() + o_map, h_map.data(), h_map.size() * sizeof(int2));
     e = hipMemcpyAsync(meta, h_meta.data(), n_meta, hipMemcpyHostToDevice, stream);
     if (e != hipSuccess) return rc_of(e);
-    e = khq::launch_attn_ws_batched(d_args, d_map, (int)h_map.size(), per, stream);
+    e = khq::launch_attn_ws_batched(d_args, d_map, (int)h_map.size(), stream);
     if (e != hipSuccess) return rc_of(e);
     return rc_of(khq::launch_step_finish_batched(d_fin, n_seq, H_q, stream));
 }

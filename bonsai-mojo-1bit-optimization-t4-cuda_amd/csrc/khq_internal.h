@@ -37,6 +37,7 @@ struct AttnArgs {
     const __half* ring_v;
     int win_start, win_len, ring_cap;
     int win_blocks;  // window blocks after the chunks: 4 (one per KV head) or 1 (all heads)
+    int chunk_tiles;  // batched launch: tiles per compressed chunk of this sequence
     // Bound of the key / value hand-off waits of the wavefront-specialised
     // kernel, in sleeps (set by the launchers; a test knob may lower it).
     int spin_limit;
@@ -133,7 +134,7 @@ hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks,
 // its window fields; map[b] = (seq, chunk) for each of n_blocks blocks (chunk
 // == n_parts: the sequence's window block).
 hipError_t launch_attn_ws_batched(const AttnArgs* args, const int2* map, int n_blocks,
-                                  int tiles_per_chunk, hipStream_t st);
+                                  hipStream_t st);
 
 // Head RMSNorm + unroped capture + partial RoPE + ring writes of one token
 // (D = 256, rot <= 64): q_gate [H_q][512] and k [H_kv][256] in place.
