@@ -396,7 +396,8 @@ int launch_khq_gqa_attn_fp16(const void* q_gate, const void* k_cache, const void
     if (head_dim != 256 || seq_len <= 0 || H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 ||
         H_q / H_kv > 8)
         return -100;
-    const int np = std::max(1, std::min(256, (seq_len + 15) / 16));
+    // 8 positions per part (two per wavefront): 512 positions fill 256 blocks
+    const int np = std::max(1, std::min(256, (seq_len + 7) / 8));
     float* ws = nullptr;
     hipError_t e = workspace((size_t)H_q * np * 258 * sizeof(float), stream, &ws);
     if (e != hipSuccess) return rc_of(e);

@@ -320,37 +320,49 @@ __global__ __launch_bounds__(256) void window_part_kernel(WinArgs a) {
 #pragma unroll
         for (int c = 0; c < 4; c++) acc[i][c] = 0.0f;
     }
-    for (int s = lo + wave; s < hi; s += 4) {
-        const int slot = (a.win_start + s) % a.ring_cap;
-        const size_t off = ((size_t)slot * a.h_kv + hkv) * 256 + p * 4;
-        const uint2 kraw = *reinterpret_cast<const uint2*>(a.ring_k + off);
-        const uint2 vraw = *reinterpret_cast<const uint2*>(a.ring_v + off);
-        const __half* kh = reinterpret_cast<const __half*>(&kraw);
-        const __half* vh = reinterpret_cast<const __half*>(&vraw);
-        float k[4], v[4];
+    // the wavefront's slots lo + wave + 4 j in groups of WG, every load of a
+    // group issued before the first is used (same slot order as one at a time)
+    constexpr int WG = 4;
+    for (int s0 = lo + wave; s0 < hi; s0 += 4 * WG) {
+        uint2 kraw[WG], vraw[WG];
 #pragma unroll
-        for (int c = 0; c < 4; c++) { k[c] = h2f(kh[c]); v[c] = h2f(vh[c]); }
+        for (int j = 0; j < WG; j++) {
+            const int s = min(s0 + 4 * j, hi - 1);
+            const int slot = (a.win_start + s) % a.ring_cap;
+            const size_t off = ((size_t)slot * a.h_kv + hkv) * 256 + p * 4;
+            kraw[j] = *reinterpret_cast<const uint2*>(a.ring_k + off);
+            vraw[j] = *reinterpret_cast<const uint2*>(a.ring_v + off);
+        }
 #pragma unroll
-        for (int i = 0; i < NREP; i++) {
-            float t = q[i][0] * k[0];
-            t = fmaf(q[i][1], k[1], t);
-            t = fmaf(q[i][2], k[2], t);
-            t = fmaf(q[i][3], k[3], t);
-            const float sv = wave_sum(t) * a.sc;
-            float e;
-            if (sv > mx[i]) {
-                const float fac = expf(mx[i] - sv);
-                sm[i] = fmaf(sm[i], fac, 1.0f);
+        for (int j = 0; j < WG; j++) {
+            if (s0 + 4 * j >= hi) break;  // uniform per wavefront
+            const __half* kh = reinterpret_cast<const __half*>(&kraw[j]);
+            const __half* vh = reinterpret_cast<const __half*>(&vraw[j]);
+            float k[4], v[4];
 #pragma unroll
-                for (int c = 0; c < 4; c++) acc[i][c] *= fac;
-                mx[i] = sv;
-                e = 1.0f;
-            } else {
-                e = expf(sv - mx[i]);
-                sm[i] += e;
+            for (int c = 0; c < 4; c++) { k[c] = h2f(kh[c]); v[c] = h2f(vh[c]); }
+#pragma unroll
+            for (int i = 0; i < NREP; i++) {
+                float t = q[i][0] * k[0];
+                t = fmaf(q[i][1], k[1], t);
+                t = fmaf(q[i][2], k[2], t);
+                t = fmaf(q[i][3], k[3], t);
+                const float sv = wave_sum(t) * a.sc;
+                float e;
+                if (sv > mx[i]) {
+                    const float fac = expf(mx[i] - sv);
+                    sm[i] = fmaf(sm[i], fac, 1.0f);
+#pragma unroll
+                    for (int c = 0; c < 4; c++) acc[i][c] *= fac;
+                    mx[i] = sv;
+                    e = 1.0f;
+                } else {
+                    e = expf(sv - mx[i]);
+                    sm[i] += e;
+                }
+#pragma unroll
+                for (int c = 0; c < 4; c++) acc[i][c] = fmaf(e, v[c], acc[i][c]);
             }
-#pragma unroll
-            for (int c = 0; c < 4; c++) acc[i][c] = fmaf(e, v[c], acc[i][c]);
         }
     }
 #pragma unroll
