@@ -416,8 +416,18 @@ int launch_khq_gqa_attn_fp16(const void* q_gate, const void* k_cache, const void
     w.sc = scale;
     e = khq::launch_window_parts(w, H_q / H_kv, dim3(np, H_kv), stream);
     if (e != hipSuccess) return rc_of(e);
-    return rc_of(khq::launch_combine_gate(ws, static_cast<const __half*>(q_gate),
-                                          static_cast<__half*>(out), H_q, np, 1e-9f, stream));
+    // merge of the parts with every load issued up front (the window is all parts)
+    khq::FinishArgs f{};
+    f.part = ws;
+    f.n_parts = np;
+    f.part_stride = np;
+    f.q = static_cast<const __half*>(q_gate);
+    f.h_kv = H_kv;
+    f.n_rep = H_q / H_kv;
+    f.sc = scale;
+    f.eps = 1e-9f;
+    f.out = static_cast<__half*>(out);
+    return rc_of(khq::launch_step_finish(f, H_q, stream));
 }
 
 int khq_attn_partials_fp16(const void* q_gate, const void* k_payload, const void* v_payload,
