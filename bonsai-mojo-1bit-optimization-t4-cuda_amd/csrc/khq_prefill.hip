@@ -731,7 +731,8 @@ void prefill_attn_rs_kernel(PrefillArgs a) {
 // Merge of the key splits, normalisation and gate: one wavefront per (query,
 // head) row, lane l owning dims 4 l .. 4 l + 3; lane s < n_split holds split
 // s's (m, l) pair.  Each group of up to 16 splits has every load in flight
-// before the first is used; the sums run in split order.
+// before the first is used (the first group's with the (m, l) loads, ahead of
+// the maximum); the sums run in split order.
 constexpr int MG = 16;  // splits per load group
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part,
                                                             const __half* __restrict__ q_gate,
@@ -740,6 +741,17 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= n_rows) return;  // uniform per wavefront
     const float* base = part + (size_t)row * n_split * 258;
+    float2 a[MG][2];
+    auto load_group = [&](int s0) {
+#pragma unroll
+        for (int j = 0; j < MG; j++)
+            if (s0 + j < n_split) {
+                const float* pp = base + (size_t)(s0 + j) * 258 + 4 * lane;
+                a[j][0] = *reinterpret_cast<const float2*>(pp);
+                a[j][1] = *reinterpret_cast<const float2*>(pp + 2);
+            }
+    };
+    load_group(0);  // in flight with the (m, l) pairs below
     float m = -1e30f, l = 0.0f;
     if (lane < n_split) {
         const float2 ml = *reinterpret_cast<const float2*>(base + (size_t)lane * 258 + 256);
@@ -753,14 +765,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
     const float lw = l * w;
     float num[4] = {0.f, 0.f, 0.f, 0.f}, den = 0.0f;
     for (int s0 = 0; s0 < n_split; s0 += MG) {
-        float2 a[MG][2];
-#pragma unroll
-        for (int j = 0; j < MG; j++)
-            if (s0 + j < n_split) {
-                const float* pp = base + (size_t)(s0 + j) * 258 + 4 * lane;
-                a[j][0] = *reinterpret_cast<const float2*>(pp);
-                a[j][1] = *reinterpret_cast<const float2*>(pp + 2);
-            }
+        if (s0 > 0) load_group(s0);
 #pragma unroll
         for (int j = 0; j < MG; j++)
             if (s0 + j < n_split) {
