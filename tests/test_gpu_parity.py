@@ -413,7 +413,11 @@ def test_c3_full_size(device, kernel):
 def test_gqa_baseline_reference_cases(device):
     from test_oracle_pins import _modular_inputs, gqa_fp64
 
-    for H_q, H_kv, seq, max_seq in [(24, 4, 8, 16), (4, 2, 16, 16), (4, 2, 1, 16), (24, 4, 512, 512)]:
+    # 512 positions: 64 parts of 8 (two slots per wavefront); 3000 and 5000:
+    # 256 parts of 12 and 20 (a wavefront's slots in one part-filled group,
+    # and in a full group of four plus one)
+    for H_q, H_kv, seq, max_seq in [(24, 4, 8, 16), (4, 2, 16, 16), (4, 2, 1, 16), (24, 4, 512, 512),
+                                    (24, 4, 3000, 3000), (24, 4, 5000, 5000)]:
         qg, k, v = _modular_inputs(H_q, H_kv, 256, max_seq)
         qg16, k16, v16 = (a.astype(np.float16) for a in (qg, k, v))
         out = torch.zeros((H_q, D), device=device, dtype=torch.float16)
