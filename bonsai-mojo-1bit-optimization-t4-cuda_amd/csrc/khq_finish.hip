@@ -351,6 +351,24 @@ __global__ __launch_bounds__(256) void step_merge_kernel(FinishArgs a) {
 
 }  // namespace fin
 
+// Upload of a metadata block from pinned host memory by the GPU itself
+// (16-byte loads over the host link, one per thread, so the whole block is a
+// single round trip): it runs in stream order like a copy, but the host call
+// that queues it returns at once.
+__global__ __launch_bounds__(256) void meta_upload_kernel(const uint4* __restrict__ src,
+                                                          uint4* __restrict__ dst, int n16) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n16) dst[i] = src[i];
+}
+
+hipError_t launch_meta_upload(const void* host_src, void* dst, size_t bytes, hipStream_t st) {
+    if (bytes % 16 != 0) return hipErrorInvalidValue;
+    const int n16 = (int)(bytes / 16);
+    hipLaunchKernelGGL(meta_upload_kernel, dim3((n16 + 255) / 256), dim3(256), 0, st,
+                       static_cast<const uint4*>(host_src), static_cast<uint4*>(dst), n16);
+    return hipGetLastError();
+}
+
 hipError_t launch_step_finish_batched(const FinishArgs* args, int n_seq, int H_q,
                                       hipStream_t st) {
     hipLaunchKernelGGL(fin::step_finish_batched_kernel, dim3(n_seq * H_q), dim3(256), 0, st, args,

@@ -77,6 +77,9 @@ struct FinishArgs {
 hipError_t launch_step_finish(const FinishArgs& a, int H_q, hipStream_t st);
 // n_seq sequences, args a device array; the window must already be a part
 // (win_len = 0 in every FinishArgs).
+// Copies bytes (a multiple of 16) from pinned host memory to device memory
+// with a one-block kernel on st.
+hipError_t launch_meta_upload(const void* host_src, void* dst, size_t bytes, hipStream_t st);
 hipError_t launch_step_finish_batched(const FinishArgs* args, int n_seq, int H_q,
                                       hipStream_t st);
 

@@ -68,6 +68,46 @@ def test_batched_matches_oracle(device, order):
         close(s["out"].cpu().numpy(), _oracle_out(st))
 
 
+def test_batched_back_to_back_calls(device):
+    """Six batched calls queued back to back with no synchronisation between
+    them (each stages its arguments in a pinned slot of a four-slot ring that
+    the GPU uploads in stream order; the fifth and sixth calls reuse slots)
+    give bit for bit the outputs of the same calls made one at a time."""
+    lc, h = layer_consts()
+    rng = np.random.default_rng(12)
+    cents = ops.Centroids(lc, device)
+    calls = []
+    for k in range(6):
+        cases = CASES[k % len(CASES):] + CASES[:k % len(CASES)]
+        cases = cases[: 3 + k]
+        seqs = []
+        for i, (c, ws, wl) in enumerate(cases):
+            st = _seq_state(rng, lc, h, c, ws, wl, seed=500 + 10 * k + i)
+            n_rows = st["rows"]["kmask"].shape[0]
+            seqs.append(dict(q_gate=t(st["q_gate"]), pay=payload_from_rows(st["rows"], n_rows),
+                             ring_k=t(st["ring_k"]), ring_v=t(st["ring_v"]),
+                             out=torch.zeros((H_Q, D), device=device, dtype=torch.float16),
+                             c_len=st["c_len"], win_start=st["win_start"], win_len=st["win_len"],
+                             ring_cap=256))
+        calls.append(seqs)
+    want = []
+    for seqs in calls:
+        assert ops.attn_step_batched(seqs, cents, H_q=H_Q, H_kv=H_KV, scale=SCALE) == 0
+        torch.cuda.synchronize()
+        want.append([s["out"].clone() for s in seqs])
+        for s in seqs:
+            s["out"].zero_()
+    torch.cuda.synchronize()
+    for seqs in calls:
+        assert ops.attn_step_batched(seqs, cents, H_q=H_Q, H_kv=H_KV, scale=SCALE) == 0
+    torch.cuda.synchronize()
+    for k, seqs in enumerate(calls):
+        for i, s in enumerate(seqs):
+            a = s["out"].cpu().numpy().view(np.uint16)
+            b = want[k][i].cpu().numpy().view(np.uint16)
+            assert np.array_equal(a, b), (k, i)
+
+
 def test_batched_error_codes(device):
     lc, _ = layer_consts()
     cents = ops.Centroids(lc, device)
