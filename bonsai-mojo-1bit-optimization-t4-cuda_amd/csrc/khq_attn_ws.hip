@@ -1368,17 +1368,6 @@ size_t attn_ws_smem_bytes() { return sizeof(ws::Smem); }
 
 int g_spin_limit = 1 << 20;
 
-static int device_cu_count() {
-    static int n_cu = 0;
-    if (n_cu == 0) {
-        int dev = 0, v = 0;
-        n_cu = (hipGetDevice(&dev) == hipSuccess &&
-                hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-                   ? v : 256;
-    }
-    return n_cu;
-}
-
 // Chunking of the compressed region: at most n_cu - 1 chunks (one CU left for
 // the window), each of the same whole number of tiles.  When that leaves no
 // room for the NWIN per-KV-head window blocks and the chunks are short (a
@@ -1425,14 +1414,9 @@ void fill_rope_table(AttnArgs& a) {
 }
 
 hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks, hipStream_t st) {
-    static bool configured = false;
     const size_t smem = sizeof(ws::Smem);
-    if (!configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ws::attn_ws_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-        if (e != hipSuccess) return e;
-        configured = true;
-    }
+    hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(&ws::attn_ws_kernel), (int)smem);
+    if (e != hipSuccess) return e;
     // four window blocks when they fit beside the chunks, else one (it is
     // hidden behind chunks of several tiles then)
     const int n_cu = device_cu_count();
@@ -1448,14 +1432,10 @@ hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks, 
 
 hipError_t launch_attn_ws_batched(const AttnArgs* args, const int2* map, int n_blocks,
                                   hipStream_t st) {
-    static bool configured = false;
     const size_t smem = sizeof(ws::Smem);
-    if (!configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ws::attn_ws_batched_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-        if (e != hipSuccess) return e;
-        configured = true;
-    }
+    hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(&ws::attn_ws_batched_kernel),
+                                      (int)smem);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(ws::attn_ws_batched_kernel, dim3(n_blocks), dim3(ws::NTHR), smem, st,
                        args, map);
     return hipGetLastError();

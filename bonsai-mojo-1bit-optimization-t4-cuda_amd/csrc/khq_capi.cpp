@@ -27,13 +27,20 @@ int rc_of(hipError_t e) { return e == hipSuccess ? 0 : static_cast<int>(e); }
 // new stream wait for it, so two streams never use the workspace at once.
 // A stream under graph capture is not ordered this way (a graph runs when it
 // is replayed, not when it is captured): replays of a captured graph and
-// eager launches on other streams must not overlap.
+// eager launches on other streams must not overlap.  A buffer that a captured
+// launch has used is never freed: when a later eager call needs more space,
+// that buffer is retired (kept until the process ends) and a larger one
+// allocated, so an earlier graph keeps replaying into memory it owns.  A
+// captured call that would need to grow the workspace fails instead
+// (hipErrorStreamCaptureUnsupported): reserve before capture.
 struct Workspace {
     void* p = nullptr;
     size_t bytes = 0;
     bool used = false;
+    bool in_graph = false;       // a captured graph holds this buffer's address
     hipStream_t last = nullptr;  // stream of the previous use
     hipEvent_t ev = nullptr;     // handed from the previous stream to the next
+    std::vector<void*> retired;  // buffers captured graphs may still replay into
 };
 std::mutex g_ws_mu;
 Workspace g_ws[kMaxDevices];
@@ -51,13 +58,24 @@ hipError_t workspace(size_t bytes, hipStream_t stream, float** out, bool use = t
     if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> lk(g_ws_mu);
     Workspace& w = g_ws[dev];
+    const bool cap = use && capturing(stream);
     if (w.bytes < bytes) {
+        // growing under capture would bake a pointer that is freed later, and
+        // the synchronisation it needs is illegal there: reserve beforehand
+        if (cap) return hipErrorStreamCaptureUnsupported;
         size_t want = std::max(bytes, (size_t)4 << 20);
         if (w.p) {
-            e = hipDeviceSynchronize();
-            if (e != hipSuccess) return e;
-            e = hipFree(w.p);
-            if (e != hipSuccess) return e;
+            if (w.in_graph) {
+                // a graph captured earlier replays into the old buffer: keep
+                // it alive for the life of the process
+                w.retired.push_back(w.p);
+                w.in_graph = false;
+            } else {
+                e = hipDeviceSynchronize();
+                if (e != hipSuccess) return e;
+                e = hipFree(w.p);
+                if (e != hipSuccess) return e;
+            }
             w.p = nullptr;
             w.bytes = 0;
         }
@@ -78,10 +96,19 @@ hipError_t workspace(size_t bytes, hipStream_t stream, float** out, bool use = t
         }
         w.used = true;
         w.last = stream;
+        if (cap) w.in_graph = true;
     }
     *out = static_cast<float*>(w.p);
     return hipSuccess;
 }
+
+std::mutex g_dev_mu;
+int g_cu_count[kMaxDevices] = {0};
+struct LdsSet {
+    const void* fn;
+    int dev, bytes;
+};
+std::vector<LdsSet> g_lds_set;
 
 // Partials of khq_attn_step_noalloc_fp16: a fixed device array per GPU
 // (8 MiB, enough for H_q 24 at any context: at most 255 chunk parts + 64
@@ -859,14 +886,24 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
     std::memcpy(ms.host + o_map, h_map.data(), h_map.size() * sizeof(int2));
     e = khq::launch_meta_upload(ms.dev, meta, n_meta, stream);
     if (e != hipSuccess) return rc_of(e);
+    // from here on the upload may be reading the slot: every exit marks it
+    // pending behind an event, so its reuse waits for the upload
+    auto fail = [&](hipError_t err) {
+        if (hipEventRecord(ms.done, stream) == hipSuccess) ms.pending = true;
+        else (void)hipStreamSynchronize(stream);
+        return rc_of(err);
+    };
     e = khq::launch_attn_ws_batched(d_args, d_map, (int)h_map.size(), stream);
-    if (e != hipSuccess) return rc_of(e);
+    if (e != hipSuccess) return fail(e);
     e = khq::launch_step_finish_batched(d_fin, n_seq, H_q, stream);
-    if (e != hipSuccess) return rc_of(e);
+    if (e != hipSuccess) return fail(e);
     // behind the call's kernels (a marker between the upload and the
     // attention launch would delay the latter)
     e = hipEventRecord(ms.done, stream);
-    if (e != hipSuccess) return rc_of(e);
+    if (e != hipSuccess) {
+        (void)hipStreamSynchronize(stream);
+        return rc_of(e);
+    }
     ms.pending = true;
     return 0;
 }
@@ -885,8 +922,10 @@ int prefill_attn_run(const __half* q_gate, const __half* k, const __half* vt, in
         (q_b > 0 && ex_hi - ex_lo != hole_hi - hole_lo))
         return -100;
     const int n_tot = std::max(n_k, ex_hi);
+    // both attention kernels read V^T in 32-key tiles without a clamp, so the
+    // leading dimension must cover the last tile
     if (H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || ld_vt % 8 != 0 ||
-        ld_vt < (n_tot + 15) / 16 * 16)
+        ld_vt < (n_tot + 31) / 32 * 32)
         return -100;
     const int n_rep = H_q / H_kv;
     int per = 0;
@@ -919,5 +958,28 @@ int prefill_attn_run(const __half* q_gate, const __half* k, const __half* vt, in
     return rc_of(launch_prefill_merge(ws, q_gate, out, n_q * H_q, ns, 1e-8f, stream));
 }
 
-}  // namespace khq
+int device_cu_count() {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    std::lock_guard<std::mutex> lk(g_dev_mu);
+    if (g_cu_count[dev] == 0)
+        g_cu_count[dev] =
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0
+                ? v : 256;
+    return g_cu_count[dev];
+}
 
+hipError_t ensure_dynamic_lds(const void* kernel, int bytes) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lk(g_dev_mu);
+    for (const LdsSet& x : g_lds_set)
+        if (x.fn == kernel && x.dev == dev && x.bytes >= bytes) return hipSuccess;
+    e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) return e;
+    g_lds_set.push_back(LdsSet{kernel, dev, bytes});
+    return hipSuccess;
+}
+
+}  // namespace khq

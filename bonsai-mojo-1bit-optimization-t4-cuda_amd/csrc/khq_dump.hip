@@ -27,6 +27,7 @@
 #include <vector>
 
 #include "khq.h"
+#include "khq_internal.h"
 
 namespace {
 
@@ -239,13 +240,8 @@ int khq_dump_attn(khq_dump* d, int layer, const void* q_gate, const void* k_rope
     const int n_valid = pos + 1;
     const size_t smem = (size_t)(D + n_valid + 64) * sizeof(float);
     if (smem > 160 * 1024) return -100;  // histories up to ~40K tokens
-    static bool configured = false;
-    if (!configured) {
-        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&dump_scores_kernel),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        if (e != hipSuccess) return (int)e;
-        configured = true;
-    }
+    e = khq::ensure_dynamic_lds(reinterpret_cast<const void*>(&dump_scores_kernel), 160 * 1024);
+    if (e != hipSuccess) return (int)e;
     hipLaunchKernelGGL(dump_scores_kernel, dim3(H_q), dim3(kThreads), smem, stream,
                        static_cast<const __half*>(q_gate), d->hist[layer], d->d_scores, n_valid,
                        H_kv, D, H_q / H_kv, scale);

@@ -242,4 +242,11 @@ int prefill_attn_run(const __half* q_gate, const __half* k, const __half* vt, in
 hipError_t launch_prefill_merge(const float* part, const __half* q_gate, __half* out, int n_rows,
                                 int n_split, float eps, hipStream_t st);
 
+// Per-device launch set-up, cached per device index under a lock (a process
+// may drive several GPUs from several threads): the CU count of the current
+// device, and the dynamic-LDS limit of a kernel raised to `bytes` on the
+// current device (once per (kernel, device)).
+int device_cu_count();
+hipError_t ensure_dynamic_lds(const void* kernel, int bytes);
+
 }  // namespace khq

@@ -859,15 +859,7 @@ int prefill_splits(int n_q, int n_rep, int h_kv, int n_k, int* keys_per_split) {
     // Blocks that run at once: 2 per CU for the 16-row kernel (72 KB of LDS
     // each), 1 for the 32-row kernel (142 KB).  The split count fills that
     // many slots in one round: a few blocks past a round cost a whole round.
-    static int n_cu = 0;
-    if (n_cu == 0) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-            n_cu = v;
-        else
-            n_cu = 256;
-    }
+    const int n_cu = device_cu_count();
     const int n_rows = n_q * n_rep;
     const bool few = few_rows(n_rows);
     const int slots = few ? 2 * n_cu : n_cu;

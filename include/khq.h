@@ -199,7 +199,8 @@ int khq_decompress_fp16(const void* k_payload, const void* v_payload, const void
  * k f16 [n_k][H_kv][256], vt f16 [H_kv][256][ld_vt]; query j (q_gate row j,
  * f16 [n_q][H_q][512]) sees keys [0, min(n_k, vis0 + j)).  out f16
  * [n_q][H_q][256] = softmax-weighted V / (den + 1e-8) * sigmoid(gate), the
- * merge_gate convention. */
+ * merge_gate convention.  ld_vt: a multiple of 8 and at least n_k rounded up
+ * to 32 (V^T is read in 32-key tiles); smaller returns -100. */
 int khq_prefill_attn_fp16(const void* q_gate, const void* k, const void* vt, int ld_vt, int n_k,
                           int n_q, int vis0, int H_q, int H_kv, float scale, void* out,
                           hipStream_t stream);

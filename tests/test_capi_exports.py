@@ -34,3 +34,21 @@ def test_header_symbols_exported():
 def test_binding_table_matches_header():
     assert set(_lib.SIGNATURES) | {"khq_version"} == declared()
     assert _lib.version().startswith("khq-mi355x")
+
+
+def test_prefill_ld_vt_guard_rejects_short_last_tile():
+    """The prefill kernels read V^T in 32-key tiles without a clamp, so a
+    leading dimension that covers n_k only to a multiple of 16 is refused
+    (-100) before anything touches the device; the fake pointers are never
+    dereferenced."""
+    lib = ctypes.CDLL(LIB_PATH)
+    fn = lib.khq_prefill_attn_fp16
+    fn.argtypes = _lib.SIGNATURES["khq_prefill_attn_fp16"]
+    fn.restype = ctypes.c_int
+    fake = ctypes.c_void_p(0x1000)
+    for n_k in (333, 17, 48 + 16):
+        short = (n_k + 15) // 16 * 16
+        if short % 32 == 0:
+            continue
+        rc = fn(fake, fake, fake, short, n_k, 1, 1, 24, 4, 0.0625, fake, None)
+        assert rc == -100, (n_k, short, rc)

@@ -66,3 +66,39 @@ def test_captured_step_replays_match_eager(device, noalloc):
             b = out_e.cpu().numpy().view(np.uint16)
             assert np.array_equal(a, b), (name, rep)
             assert np.isfinite(out_g.float().cpu().numpy()).all()
+
+
+def test_graph_survives_workspace_growth(device):
+    """A graph captured over the shared workspace keeps replaying correctly
+    after a later eager call grows the workspace: the captured buffer is
+    retired, not freed, so memory torch hands out afterwards (filled with NaN
+    here) never aliases it."""
+    rng = np.random.default_rng(57)
+    c = _cases(device)["8192+128"]
+    q = torch.from_numpy(rng.standard_normal((H_Q, 2 * D)).astype(np.float16)).to(device)
+    out_g = torch.zeros((H_Q, D), device=device, dtype=torch.float16)
+    out_e = torch.zeros_like(out_g)
+
+    def step(out, check=True):
+        return ops.attn_step(q, c["pay"], c["cents"], c["ring_k"], c["ring_v"], out,
+                             H_q=H_Q, H_kv=H_KV, c_len=c["c_len"], win_start=c["win_start"],
+                             win_len=c["win_len"], ring_cap=256, scale=SCALE, check=check)
+
+    step(out_g)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        assert step(out_g, check=False) == 0
+    print("graph captured; growing the workspace past every earlier size", flush=True)
+    ops.workspace_reserve(768 << 20)
+    junk = [torch.full((64 << 20,), float("nan"), device=device) for _ in range(4)]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        out_g.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert step(out_e) == 0
+        torch.cuda.synchronize()
+        assert np.array_equal(out_g.cpu().numpy().view(np.uint16),
+                              out_e.cpu().numpy().view(np.uint16)), rep
+    del junk

@@ -98,6 +98,27 @@ def test_prefill_attn_vs_float64(device, n_k, n_q, vis0):
     close(out.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("n_k,n_q,vis0", [(333, 37, 297), (44, 3, 40), (1000 - 24, 130, 847)])
+def test_prefill_attn_minimum_vt_leading_dim(device, n_k, n_q, vis0):
+    """n_k % 32 in 1..16 with ld_vt at its minimum (n_k rounded up to 32) and a
+    V^T buffer of exactly H_kv * 256 * ld_vt halves: the last 32-key tile of
+    the last head ends at the buffer's end."""
+    rng = np.random.default_rng(n_k * 7 + n_q)
+    K = rng.standard_normal((n_k, H_KV, D)).astype(np.float16)
+    V = rng.standard_normal((n_k, H_KV, D)).astype(np.float16)
+    q = rng.standard_normal((n_q, H_Q, 2 * D)).astype(np.float16)
+    ld = (n_k + 31) // 32 * 32
+    assert 1 <= n_k % 32 <= 16
+    vt = np.zeros((H_KV, D, ld), np.float16)
+    vt[:, :, :n_k] = V.transpose(1, 2, 0)
+    out = torch.zeros((n_q, H_Q, D), device=device, dtype=torch.float16)
+    ops.prefill_attn(t(q), t(K), t(vt), out, ld_vt=ld, n_k=n_k, n_q=n_q, vis0=vis0, H_q=H_Q,
+                     H_kv=H_KV, scale=SCALE)
+    torch.cuda.synchronize()
+    want = _dense_reference(q, K.astype(np.float64), V.astype(np.float64), vis0, n_k)
+    close(out.cpu().numpy(), want)
+
+
 def _tokens(n, seed, pos0=0):
     rng = np.random.default_rng(seed)
     k = rng.standard_normal((n, H_KV, D)).astype(np.float16)
