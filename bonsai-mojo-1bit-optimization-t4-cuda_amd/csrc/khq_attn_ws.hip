@@ -23,14 +23,18 @@
 //               and the dot with q (key split hi + lo), all on MFMA.
 // K contraction order: K-step st, lane group lg, element e <-> dim
 // 64 lg + 8 st + e, so lane (token li, lg) owns dims 64 lg .. 64 lg + 63 of
-// its token in every K-step.  Outliers are expanded per K-step without a
-// walk: the 8-dim outlier pattern p indexes byte-permute tables that place
-// the nibbles and signs of outlier ordinals q .. q + 7 (q = outliers before
-// these dims) at their dims.  The B operand splits into
-//   b1 = sgn * cb (outliers take their stored sign), exact fp16;
-//   b2 = sgn * nib * 2^-14 at outliers, 0 elsewhere, exact fp16;
+// its token in every K-step.  Outliers are expanded without a walk: per
+// tile, each token's outlier payload becomes a rank-window array E[r] =
+// (h_r, h_r+1) of fp16 halves h_r = -+nib_r * 2^-24 (sign from the stored
+// sign bit; an exact subnormal), so the four halves from any rank r are the
+// read pair E[r], E[r + 2].  Per 4-dim group (one mask byte) a table gives
+// the sign halves of its codes and the byte selectors that put the window
+// halves of its outliers (ranks r .. r + 3, r = outliers before the group)
+// at their dims.  The B operand splits into
+//   b1 = sgn * cb (an outlier's sign OR-ed in from its window half), exact;
+//   b2 = -+nib * 2^-24 at outliers, 0 elsewhere, exact;
 // both go through the same A operands and b2's products are scaled by
-// 2^14 rs / mult afterwards, per token.
+// 2^24 rs / mult afterwards, per token.
 // V is accumulated in the rotated domain; lane (patch 16 g + li, tokens
 // 4 lg .. 4 lg + 3) decodes straight into the B operand of 16x16x16 MFMAs:
 //   dims (p, k<3): codebook value * (w * a_v * norm * energy)
@@ -81,7 +85,9 @@ __device__ unsigned long long block_times[1024][2];
 constexpr int TT = 16;          // tokens per tile
 constexpr int NTHR = 512;       // 4 key + 4 value wavefronts
 constexpr int CB_PS = 768;      // halves per codebook patch (256 codes x 3)
-constexpr int KP_TS = 14;       // words per staged kpay row (see key_role staging)
+constexpr int KP_TS = 12;       // words per staged kpay row: the 40-byte row, 2 zero words
+constexpr int KE_S = 68;        // words per token of the rank-window array (ranks 0..67)
+constexpr int KE_MAXQ = 50;     // ordinals >= 50 carry no payload (nibble 0, sign -1)
 constexpr int VP_TS = 26;       // words per staged vpay row
 constexpr float RESCALE_GAP = 8.0f;
 
@@ -90,11 +96,10 @@ struct __align__(16) Smem {
     float o[4][6 * 256];         // setup: query transforms; end: V sums 24576 B
     uint32_t vp[4][TT * VP_TS];  // staged vpay rows per KV head         6656 B
                                  // (setup: rotor_k)
-    uint32_t kp[4][TT * KP_TS];  // staged kpay rows per KV head         3584 B
-    uint2 sgn[256];              // mask byte -> 4 fp16 signs {0,-1,+1,0}
-    uint4 seln[256];             // outlier pattern -> nibble byte selectors
-    uint4 sels[256];             // outlier pattern -> sign byte selectors
-    uint2 sgnb[256];             // 8 sign bits -> sign bytes (even, odd ordinals)
+    uint32_t kp[4][TT * KP_TS];  // staged kpay rows per KV head         3072 B
+    uint32_t ke[4][TT * KE_S];   // rank windows E[r] = (h_r, h_r+1)    17408 B
+    uint4 ktab[256];             // mask byte -> sign halves, window selectors
+    uint2 sgb[256];              // 8 flags -> bytes 0x80 / 0 (flags 0..3, 4..7)
     _Float16 cbk[256];           // cents_k[2]
     float pw[2][4][6][TT];       // scaled scores, by tile parity
     float rope[4][3][8];         // per lane group: freq, cos(16 f), sin(16 f)
@@ -382,27 +387,50 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
     }
     const _Float16* cbq = &S.cbk[64 * lg];
     uint32_t* kpw = S.kp[h];
-    // Staged kpay row of a token, in words: 0 c_base_mult, 1..7 nibbles 0..55
-    // with 50..55 (sign bits in the packed row) cleared, 8..9 zero (nibble
-    // reads at ordinals up to 56 + 15), 10 sign bits 0..23, 11 sign bits
-    // 24..55 (bits past 49 cleared when read).  Ordinals >= 50 so read
-    // nibble 0 and sign 0 (negative), the stored format's default.
+    uint32_t* kew = S.ke[h];
+    // Staged kpay row of a token: the 40 bytes as stored (word 0 c_base_mult,
+    // bytes 4..28 nibbles of ordinals 0..49, bytes 29..35 their sign bits),
+    // then two zero words.
+    // Past the row: word 10 holds nibble word 7 with only ordinals 48, 49
+    // (the sign bytes that follow cleared) and word 9 (shared meta) and the
+    // sign bits past 49 read as 0, so every rank-window item reads clean
+    // words at fixed offsets.
     auto stage_kp = [&](int tok, int part, u2v v) {
-        uint32_t w0 = v[0], w1 = v[1], extra = v[0];
-        int eslot = 11;
-        if (part == 3) {
-            extra = w1 >> 8;
-            eslot = 10;
-            w1 &= 0xFFu;
-        }
-        if (part == 4) {
-            w0 = 0u;
-            w1 = 0u;
-        }
         uint32_t* row = &kpw[tok * KP_TS];
-        *reinterpret_cast<u2v*>(&row[2 * part]) = u2v{w0, w1};
-        if (part >= 3) row[eslot] = extra;
+        if (part == 4) v = u2v{v[0] & 0x03FFFFFFu, 0u};
+        *reinterpret_cast<u2v*>(&row[2 * part]) = v;
+        if (part == 3) row[10] = v[1] & 0xFFu;
     };
+    // Rank windows: h_r = fp16 bits (sign_r negative ? 0x8000 : 0) | nib_r,
+    // i.e. -+nib_r * 2^-24 as an fp16 subnormal (exact; 0x8000 = -0 past
+    // ordinal 49, the format's default of residual 0, sign -1), and
+    // E[r] = h_r | h_(r+1) << 16 for every rank r, so the four halves from
+    // any rank are one read pair E[r], E[r + 2].  Item (token, j) of this
+    // lane builds E[8 j .. 8 j + 7] from nibble word 1 + j and sign bits
+    // 8 j .. 8 j + 8 (byte 29 + j); E[56 ..] is constant (set up once).
+    const int e_it0 = lane, e_it1 = min(lane + 64, 111);
+    const bool e_two = lane + 64 < 112;
+    auto build_e = [&](int item) {
+        const int row = item / 7, j = item - 7 * (item / 7);
+        const uint32_t* W = &kpw[row * KP_TS];
+        const int sb_w = (29 + j) >> 2, sb_sh = 8 * ((29 + j) & 3);
+        const uint32_t nw = W[j < 6 ? 1 + j : 10];        // ordinals 8 j .. 8 j + 7
+        const uint32_t nn = W[j < 6 ? 2 + j : 11] & 0xFu;  // ordinal 8 j + 8
+        const uint32_t sb = __builtin_amdgcn_alignbit(W[sb_w + 1], W[sb_w], sb_sh);
+        const uint2 sg = S.sgb[~sb & 0xFFu];  // negative flags -> byte top bits
+        const uint32_t lo = nw & 0x0F0F0F0Fu, hi = (nw >> 4) & 0x0F0F0F0Fu;
+        const uint32_t nb01 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // ordinals 0..3
+        const uint32_t nb23 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // ordinals 4..7
+        const uint32_t H0 = __builtin_amdgcn_perm(sg.x, nb01, 0x05010400u);
+        const uint32_t H1 = __builtin_amdgcn_perm(sg.x, nb01, 0x07030602u);
+        const uint32_t H2 = __builtin_amdgcn_perm(sg.y, nb23, 0x05010400u);
+        const uint32_t H3 = __builtin_amdgcn_perm(sg.y, nb23, 0x07030602u);
+        const uint32_t H4 = nn | ((~sb & 0x100u) << 7);
+        uint4* dst = reinterpret_cast<uint4*>(&kew[row * KE_S + 8 * j]);
+        dst[0] = uint4{H0, __builtin_amdgcn_alignbit(H1, H0, 16), H1, __builtin_amdgcn_alignbit(H2, H1, 16)};
+        dst[1] = uint4{H2, __builtin_amdgcn_alignbit(H3, H2, 16), H3, __builtin_amdgcn_alignbit(H4, H3, 16)};
+    };
+    const uint32_t* kerow = &kew[li * KE_S];
     PHASE(1);
 
     for (int it = 0; it <= n_tiles; it++) {
@@ -424,28 +452,31 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
                     sincos_rev((float)(a.start_pos + s0 + li) * S.rope[lg][0][u], bc[u], bs[u]);
             }
             wave_sync();
+            build_e(e_it0);
+            if (e_two) build_e(e_it1);
+            wave_sync();
             PHASE(2);
 
             // ---- per-token scalars of this lane's token
-            const uint32_t* krow = &kpw[li * KP_TS];
-            float mult = (float)krow[0] / 1000.0f;
-            if (mult < 0.1f || mult > 10.0f || isnan(mult)) mult = 1.0f;
-            const float rr = rs / mult;
+            // c_base_mult = word / 1000 when that lies in [0.1, 10] (word in
+            // [100, 10000]), else 1; the product with the rounded 1 / 1000
+            // and the hardware reciprocal are within 2 ulp of the quotients
+            const uint32_t mraw = kpw[li * KP_TS];
+            const bool m_ok = mraw - 100u <= 9900u;
+            const float mult = m_ok ? (float)mraw * 0.001f : 1.0f;
+            const float rr = rs * __builtin_amdgcn_rcpf(mult);
+            const float fsc = a.a_k * nk * mult * a.sc;
 
-            // ---- outliers of dims 64 lg .. 64 lg + 63: pattern bits and the
-            // ordinal of the first one (outliers of the quarters before)
+            // ---- outliers (code 3) of dims 64 lg .. 64 lg + 63: flags at the
+            // even bit of each code, and the rank of the first one (outliers
+            // of the quarters before this lane's)
             const uint32_t mw[4] = {mc.x, mc.y, mc.z, mc.w};
-            uint64_t msk = 0;
+            uint32_t ow[4];
             int cnt = 0;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                uint32_t x = (mw[i] & (mw[i] >> 1)) & 0x55555555u;
-                cnt += __popc(x);
-                x = (x | (x >> 1)) & 0x33333333u;
-                x = (x | (x >> 2)) & 0x0F0F0F0Fu;
-                x = (x | (x >> 4)) & 0x00FF00FFu;
-                x = (x | (x >> 8)) & 0x0000FFFFu;
-                msk |= (uint64_t)x << (16 * i);
+                ow[i] = (mw[i] & (mw[i] >> 1)) & 0x55555555u;
+                cnt += __popc(ow[i]);
             }
             int qrun;
             {
@@ -457,12 +488,13 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
                 const auto p32 = __builtin_amdgcn_permlane32_swap(pair, pair, false, false);
                 qrun = (int)(((lg & 1) ? c_even : 0u) + ((lg >= 2) ? p32[0] : 0u));
             }
-            const uint32_t sw10 = krow[10], sw11 = krow[11];
-            const uint64_t sig = (uint64_t)(sw10 | (sw11 << 24)) |
-                                 ((uint64_t)((sw11 >> 8) & 0x3FFFFu) << 32);
 
             PHASE(3);
-            // ---- b1 / b2 operands + pass / fold MFMAs
+            // ---- b1 / b2 operands + pass / fold MFMAs.  Per 4-dim group (a
+            // mask byte): the table gives the sign halves (codes 1 / 2 / 3 ->
+            // -1 / +1 / +1) and the selectors that place the window halves of
+            // the group's outliers at their dims; the outlier's own sign then
+            // comes from its window half (b1 = sign * cb, b2 = -+nib * 2^-24).
             f4 cs = f4{0.f, 0.f, 0.f, 0.f}, cs2 = cs;
             f4 zt[4], zt2[4];
 #pragma unroll
@@ -471,53 +503,50 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
                 zt2[T] = zt[T];
             }
             {
+                int q = 0;
 #pragma unroll
                 for (int st = 0; st < 8; st++) {
-                    const uint32_t word = mw[st >> 1];
+                    const uint32_t word = mw[st >> 1], owd = ow[st >> 1];
                     const int sh = 16 * (st & 1);
-                    const uint2 sg0 = S.sgn[(word >> sh) & 0xFFu];
-                    const uint2 sg1 = S.sgn[(word >> (sh + 8)) & 0xFFu];
-                    const uint32_t pat = (uint32_t)(msk >> (8 * st)) & 0xFFu;
-                    const int q = min(qrun, 56);
-                    qrun += __popc(pat);
-                    const uint4 sn = S.seln[pat], ss = S.sels[pat];
-                    const uint32_t* nrow = krow + 1 + (q >> 3);
-                    const uint32_t nw = __builtin_amdgcn_alignbit(nrow[1], nrow[0], (q & 7) * 4);
-                    const uint32_t nl = nw & 0x0F0F0F0Fu, nh = (nw >> 4) & 0x0F0F0F0Fu;
-                    const uint2 sb = S.sgnb[(uint32_t)(sig >> q) & 0xFFu];
+                    // ranks past 49 all read the constant window: the rank is
+                    // clamped once per mask word (at most 16 more before the
+                    // next clamp, so every read stays inside the token's row)
+                    if ((st & 1) == 0) q = min(qrun, KE_MAXQ);
+                    const int rA = q;
+                    const int rB = rA + __popc(__builtin_amdgcn_ubfe(owd, sh, 8));
+                    q = rA + __popc(__builtin_amdgcn_ubfe(owd, sh, 16));
+                    if (st & 1) qrun = q;
+                    const uint4 tA = S.ktab[__builtin_amdgcn_ubfe(word, sh, 8)];
+                    const uint4 tB = S.ktab[__builtin_amdgcn_ubfe(word, sh + 8, 8)];
+                    const uint32_t eA0 = kerow[rA], eA1 = kerow[rA + 2];
+                    const uint32_t eB0 = kerow[rB], eB1 = kerow[rB + 2];
+                    const uint32_t nv[4] = {__builtin_amdgcn_perm(eA1, eA0, tA.z),
+                                            __builtin_amdgcn_perm(eA1, eA0, tA.w),
+                                            __builtin_amdgcn_perm(eB1, eB0, tB.z),
+                                            __builtin_amdgcn_perm(eB1, eB0, tB.w)};
+                    const uint32_t sgv[4] = {tA.x, tA.y, tB.x, tB.y};
                     const uint4 cbw = *reinterpret_cast<const uint4*>(&cbq[8 * st]);
-                    const uint32_t sgw[4] = {sg0.x, sg0.y, sg1.x, sg1.y};
                     const uint32_t cbv[4] = {cbw.x, cbw.y, cbw.z, cbw.w};
-                    const uint32_t snv[4] = {sn.x, sn.y, sn.z, sn.w};
-                    const uint32_t ssv[4] = {ss.x, ss.y, ss.z, ss.w};
-                    uint32_t b1w[4], b2w[4];
+                    uint32_t b1w[4];
 #pragma unroll
                     for (int k = 0; k < 4; k++) {
-                        // at outlier dims: xs = +-1024, xn = nib * 2^-24 (an fp16
-                        // subnormal, exact), so b2 = xn * xs = +-nib * 2^-14 and
-                        // b1 = (sgn + xs / 1024) * cb; both products are exact
-                        const h2 xs = __builtin_bit_cast(h2, __builtin_amdgcn_perm(sb.y, sb.x, ssv[k]));
-                        const h2 xn = __builtin_bit_cast(h2, __builtin_amdgcn_perm(nh, nl, snv[k]));
-                        b2w[k] = __builtin_bit_cast(uint32_t, xn * xs);
-                        const h2 sgy = __builtin_elementwise_fma(
-                            xs, h2{(_Float16)0.0009765625f, (_Float16)0.0009765625f},
-                            __builtin_bit_cast(h2, sgw[k]));
-                        b1w[k] = __builtin_bit_cast(uint32_t, sgy * __builtin_bit_cast(h2, cbv[k]));
+                        const uint32_t sg = (nv[k] & 0x80008000u) | sgv[k];
+                        b1w[k] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, sg) * __builtin_bit_cast(h2, cbv[k]));
                     }
                     const h8 b1 = __builtin_bit_cast(h8, uint4{b1w[0], b1w[1], b1w[2], b1w[3]});
-                    const h8 b2 = __builtin_bit_cast(h8, uint4{b2w[0], b2w[1], b2w[2], b2w[3]});
+                    const h8 b2 = __builtin_bit_cast(h8, uint4{nv[0], nv[1], nv[2], nv[3]});
                     cs = mfma32(At[st], b1, cs);
                     cs2 = mfma32(At[st], b2, cs2);
                     const h8 aw = (st & 1) == s_fold ? Aw[st >> 1] : hzero;
                     zt[st >> 1] = mfma32(aw, b1, zt[st >> 1]);
                     zt2[st >> 1] = mfma32(aw, b2, zt2[st >> 1]);
                 }
-                const float rr1024 = rr * 16384.0f;  // b2 carries nib * 2^-14
+                const float rr24 = rr * 16777216.0f;  // b2 carries nib * 2^-24
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
-                    cs[c] = fmaf(rr1024, cs2[c], cs[c]);
+                    cs[c] = fmaf(rr24, cs2[c], cs[c]);
 #pragma unroll
-                    for (int T = 0; T < 4; T++) zt[T][c] = fmaf(rr1024, zt2[T][c], zt[T][c]);
+                    for (int T = 0; T < 4; T++) zt[T][c] = fmaf(rr24, zt2[T][c], zt[T][c]);
                 }
             }
 
@@ -565,7 +594,6 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
 
             // ---- scores of heads 2 lg, 2 lg + 1 for token li
             const bool tok_ok = (s0 + li) < s_hi;
-            const float fsc = a.a_k * nk * mult * a.sc;
             float sc2[2];
             sc2[0] = tok_ok ? (cs[0] + cs[1]) * fsc : -INFINITY;
             sc2[1] = tok_ok ? (cs[2] + cs[3]) * fsc : -INFINITY;
@@ -577,7 +605,9 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
             // ---- raw scores to the value side (it keeps the softmax state);
             // buffer t & 1 last held tile t - 2
             const int buf = t & 1;
+            PHASE(5);
             wait_count(&S.vread[h], t - 1, a.spin_limit, &S.fault);
+            PHASE(23);
             if (lg < 3) {
                 S.pw[buf][h][2 * lg][li] = sc2[0];
                 S.pw[buf][h][2 * lg + 1][li] = sc2[1];
@@ -696,7 +726,9 @@ __device__ __forceinline__ void value_role(const AttnArgs& a, Smem& S, const Set
             const int buf = t & 1;
             // ---- the key side's scores of this tile: row head r_head, tokens
             // 4 lg .. 4 lg + 3 (read first: their latency overlaps the staging)
+            PHASE(14);
             wait_count(&S.kdone[h], t + 1, a.spin_limit, &S.fault);
+            PHASE(22);
             f4 sc4 = f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
             if (r_ok) sc4 = *reinterpret_cast<const f4*>(&S.pw[buf][h][r_head][4 * lg]);
             // ---- take the staged tile, start loading the next one
@@ -1242,46 +1274,48 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
         }
         if (tid == 0) S.fault = 0;
         if (wv < 4) {
-            h4 s;
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const int code = (t >> (2 * c)) & 3;
-                s[c] = code == 2 ? (_Float16)1.0f : (code == 1 ? (_Float16)-1.0f : (_Float16)0.0f);
-            }
-            S.sgn[t] = __builtin_bit_cast(uint2, s);
-            // sign bits t (bit r: ordinal r positive) -> high bytes of +-1024
-            uint32_t ev = 0, od = 0;
-#pragma unroll
-            for (int m = 0; m < 4; m++) {
-                ev |= (((t >> (2 * m)) & 1) ? 0x64u : 0xE4u) << (8 * m);
-                od |= (((t >> (2 * m + 1)) & 1) ? 0x64u : 0xE4u) << (8 * m);
-            }
-            S.sgnb[t] = uint2{ev, od};
-        } else {
-            // outlier pattern t (bit i: dim i of 8 is an outlier): output
-            // word k holds dims 2k, 2k + 1 as fp16 halves; the nibble selector
-            // puts the byte of ordinal rank(i) in the low byte of the half, the
-            // sign selector in the high byte.  Bytes of even ordinals come
-            // from the second perm source, odd ones from the first (4 + r / 2).
-            uint32_t sn[4], ss[4];
+            // mask byte t (codes of 4 dims): sign halves (code 1 -> -1, codes
+            // 2 and 3 -> +1; an outlier's own sign is OR-ed in from its window
+            // half) and, per output word (dims 0, 1 | dims 2, 3), the byte
+            // selectors of the window halves: the d-th outlier of the byte
+            // takes window half d (bytes 2 d, 2 d + 1), other dims 0x0C (zero).
+            uint32_t sg[2], sl[2];
             int r = 0;
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                uint32_t n = 0x0C0C0C0Cu, g = 0x0C0C0C0Cu;
+            for (int k = 0; k < 2; k++) {
+                uint32_t g = 0u, n = 0x0C0C0C0Cu;
 #pragma unroll
                 for (int e = 0; e < 2; e++) {
-                    if ((t >> (2 * k + e)) & 1) {
-                        const uint32_t src = (r & 1) ? 4u + (uint32_t)(r >> 1) : (uint32_t)(r >> 1);
-                        n = (n & ~(0xFFu << (16 * e))) | (src << (16 * e));
-                        g = (g & ~(0xFFu << (16 * e + 8))) | (src << (16 * e + 8));
+                    const int code = (t >> (2 * (2 * k + e))) & 3;
+                    const uint32_t hv = code == 1 ? 0xBC00u : (code >= 2 ? 0x3C00u : 0u);
+                    g |= hv << (16 * e);
+                    if (code == 3) {
+                        n = (n & ~(0xFFFFu << (16 * e))) |
+                            (((uint32_t)(2 * r) | ((uint32_t)(2 * r + 1) << 8)) << (16 * e));
                         r++;
                     }
                 }
-                sn[k] = n;
-                ss[k] = g;
+                sg[k] = g;
+                sl[k] = n;
             }
-            S.seln[t] = uint4{sn[0], sn[1], sn[2], sn[3]};
-            S.sels[t] = uint4{ss[0], ss[1], ss[2], ss[3]};
+            S.ktab[t] = uint4{sg[0], sg[1], sl[0], sl[1]};
+            uint32_t f0 = 0u, f1 = 0u;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                f0 |= ((t >> k) & 1) ? 0x80u << (8 * k) : 0u;
+                f1 |= ((t >> (4 + k)) & 1) ? 0x80u << (8 * k) : 0u;
+            }
+            S.sgb[t] = uint2{f0, f1};
+        } else {
+            // the constant tail of every rank-window row (ranks 56 ..) and the
+            // two zero words of every staged kpay row
+#pragma unroll
+            for (int i = 0; i < 3; i++) {
+                const int x = t + 256 * i;  // 768 = 4 heads x 16 tokens x 12 ranks
+                const int row = x / 12, r = 56 + x % 12;
+                (&S.ke[0][0])[row * KE_S + r] = 0x80008000u;
+            }
+            if (t < 128) (&S.kp[0][0])[(t >> 1) * KP_TS + 10 + (t & 1)] = 0u;
         }
     }
 
