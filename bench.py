@@ -63,6 +63,9 @@ def parse():
                     help="profiling aid for rocprofv3 --pmc: a 256 MiB device copy (the "
                          "calibration kernel of known size), then the compressed-region kernel "
                          "on 4 C3 layers, 3 times; prints no JSON")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="default run only: skip the short runs of configs 1, 2, 4 and 5 "
+                         "reported under 'configs'")
     ap.add_argument("--no-sweep", action="store_true",
                     help="skip the C3 sweep of the reference entry sequence at splits "
                          "1/8/32/64 (launch_khq_attn_fp16 + window + merge, and the split-K "
@@ -81,11 +84,11 @@ def main():
 
     _lib.call("khq_select_kernel", ["auto", "portable"].index(args.kernel))
     if args.config in ("c1", "c2"):
-        return bench_small(args)
+        return print(json.dumps(bench_small(args)), flush=True)
     if args.config == "c4":
-        return bench_c4(args)
+        return print(json.dumps(bench_c4(args)), flush=True)
     if args.config == "c5":
-        return bench_c5(args)
+        return print(json.dumps(bench_c5(args)), flush=True)
     if args.counters_run:
         return counters_run(args)
     from khq.centroids import synthetic_layer
@@ -270,7 +273,32 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(layers[0], c_len, win_len, win_start, scale,
                                               args.cpu_seconds)
+    if not args.no_configs and args.layers == 16 and args.ctx == 32768:
+        del layers
+        torch.cuda.synchronize()
+        result["configs"] = other_configs(args)
     print(json.dumps(result), flush=True)
+
+
+def other_configs(args):
+    """Short runs of the other configurations (2, 4
+    and 5), each with its own roofline and CPU baseline, for the default
+    benchmark line: 16 layers each, fewer steps, smaller CPU samples."""
+    import copy
+
+    out = {}
+    drop = ("n_gpus", "higher_is_better", "scaling", "vs_baseline")
+    for name, fn, steps, warm in (("c1", bench_small, 10, 2), ("c2", bench_small, 10, 2),
+                                  ("c4", bench_c4, 5, 2), ("c5", bench_c5, 2, 1)):
+        a = copy.copy(args)
+        a.config, a.steps, a.warmup = name, min(args.steps, steps), min(args.warmup, warm)
+        a.cpu_seconds = min(args.cpu_seconds, 3.0)
+        t0 = time.perf_counter()
+        r = fn(a)
+        r = {k: v for k, v in r.items() if k not in drop}
+        r["wall_s"] = round(time.perf_counter() - t0, 1)
+        out[name] = r
+    return out
 
 
 def graph_us(step, reps, layers=None):
@@ -470,8 +498,11 @@ def bench_c5(args):
             "with_merge_us": round(attn_us, 3),
             "with_merge_tflops": round(attn_flops / (attn_us * 1e-6) / 1e12, 2),
         },
+        "cpu_baseline": None,
     }
-    print(json.dumps(result), flush=True)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline_c5(args.cpu_seconds)
+    return result
 
 
 def bench_small(args):
@@ -591,7 +622,7 @@ def bench_small(args):
             L0 = dict(pay=pay, lc=synthetic_layer(0, seed=1234), q=q, ring_k=rk, ring_v=rv)
             result["cpu_baseline"] = cpu_baseline(L0, 384, 128, 384 % RING, scale,
                                                   args.cpu_seconds)
-    print(json.dumps(result))
+    return result
 
 
 def bench_c4(args):
@@ -687,8 +718,17 @@ def bench_c4(args):
         "hbm_pct_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
         "bytes_per_layer_step": step_bytes,
         "sequential_calls_us_per_layer_step": round(ms_s * 1000.0 / args.layers, 3),
+        "roofline": {"bound": "hbm", "kernel": "whole batched layer-step (argument upload, "
+                     "attn_ws_batched_kernel, step_finish_batched_kernel)",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": None,
     }
-    print(json.dumps(result), flush=True)
+    if not args.no_cpu:
+        cents0, seqs0 = layers[0]
+        result["cpu_baseline"] = cpu_baseline_c4(seqs0, synthetic_layer(0, seed=1234), scale,
+                                                 args.cpu_seconds)
+    return result
 
 
 def cpu_baseline_c1(q, k, v, scale, budget_s):
@@ -717,6 +757,106 @@ def cpu_baseline_c1(q, k, v, scale, budget_s):
             "kind": "port",
             "sample": "layer 0 of the same workload (512 positions, 24/4 heads), repeated; "
                       "value with OpenMP over query heads, single_thread_us on one core"}
+
+
+def _oracle_decode_step(oracle, rows, h, lc, q, rk, rv, c_len, win_start, win_len, scale):
+    """One decode layer-step through the CPU oracle: compressed attention at
+    the BONSAI_KHQ_SPLITS default, raw window, merge and gate."""
+    from khq.layer import split_count
+
+    _, ac, _ = oracle.attn(q, rows["kpay"], rows["vpay"], rows["vsm"], rows["kmask"],
+                           rows["knorm"], rows["krn"], rows["vnorm"], rows["vrn"],
+                           h["cents_k"], h["cents_v"], h["vq"], h["rotor_k"], h["rotor_v"],
+                           h["d_k"], h["d_v"], num_queries=H_Q, num_heads=H_Q, L_q=1,
+                           c_len=c_len, n_rep=H_Q // H_KV, scale=scale, alpha_k=lc.alpha_k,
+                           alpha_v=lc.alpha_v, rope_base=1e7, start_pos=0,
+                           num_splits=split_count(c_len, 16))
+    _, aw = oracle.window_attn(q, rk, rv, win_start=win_start, win_len=win_len, ring_cap=RING,
+                               H_q=H_Q, H_kv=H_KV, scale=scale)
+    oracle.merge_gate(ac, aw, q, H_q=H_Q, has_w=True)
+
+
+def _payload_np(pay, n_rows):
+    import numpy as np
+
+    rows = {k: getattr(pay, k)[:n_rows].cpu().numpy()
+            for k in ("kmask", "kpay", "knorm", "krn", "vpay", "vnorm", "vrn", "vsm")}
+    rows["kmask"] = rows["kmask"].view(np.uint32)
+    return rows
+
+
+def cpu_baseline_c4(seqs, lc, scale, budget_s):
+    """Config 4's CPU path: the oracle's decode step per sequence (layer 0),
+    sequences taken in order until the time budget is spent; the value is
+    that time scaled to all 32 sequences by their compressed and raw bytes."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    oracle.set_num_threads(threads)
+    h = lc.fp16()
+
+    def nbytes(s):
+        return s["c_len"] * H_KV * ROW_BYTES + s["win_len"] * H_KV * D * 2 * 2
+
+    done, el, t0 = 0, 0.0, time.perf_counter()
+    for s in seqs:
+        rows = _payload_np(s["pay"], s["c_len"] * H_KV)
+        q = s["q_gate"].cpu().numpy()
+        rk, rv = s["ring_k"].cpu().numpy(), s["ring_v"].cpu().numpy()
+        t1 = time.perf_counter()
+        _oracle_decode_step(oracle, rows, h, lc, q, rk, rv, s["c_len"], s["win_start"],
+                            s["win_len"], scale)
+        el += time.perf_counter() - t1
+        done += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    frac = sum(nbytes(s) for s in seqs[:done]) / sum(nbytes(s) for s in seqs)
+    return {"value": round(el / frac * 1e6, 1), "unit": "us/layer-step", "cores": threads,
+            "host_nproc": os.cpu_count(), "kind": "port",
+            "sample": f"{done} of the {len(seqs)} sequences of layer 0 through the oracle's "
+                      f"decode step (OpenMP over query head x split), scaled to all "
+                      f"{len(seqs)} by bytes ({100 * frac:.1f}% sampled)"}
+
+
+def cpu_baseline_c5(budget_s):
+    """Config 5's CPU path: the reference answers a chunk of queries one decode
+    step at a time, so the oracle's decode step (8,064 compressed rows of
+    seeded uniform-random codes plus the raw window, layer 0 constants) is
+    timed for successive queries of the chunk until the budget is spent and
+    scaled to the chunk's 128 queries (the compression event's own cost, 128
+    rows once per chunk, is not counted)."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    from khq import ops, synth
+    from khq.centroids import synthetic_layer
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    oracle.set_num_threads(threads)
+    lc = synthetic_layer(0, seed=1234)
+    h = lc.fp16()
+    c_len = 8064
+    rows = {k: v.numpy() for k, v in synth.random_rows(c_len * H_KV, seed=77, device="cpu").items()}
+    rows["kmask"] = rows["kmask"].view(np.uint32)
+    rng = np.random.default_rng(78)
+    rk = rng.standard_normal((RING, H_KV, D)).astype(np.float16)
+    rv = rng.standard_normal((RING, H_KV, D)).astype(np.float16)
+    q = rng.standard_normal((H_Q, 2 * D)).astype(np.float16)
+    done, t0 = 0, time.perf_counter()
+    while True:
+        j = done % 127
+        _oracle_decode_step(oracle, rows, h, lc, q, rk, rv, c_len, c_len % RING, 129 + j, scale=1 / 16)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or done >= 128:
+            break
+    return {"value": round(el / done * 128 * 1e6, 1), "unit": "us/layer-step", "cores": threads,
+            "host_nproc": os.cpu_count(), "kind": "port",
+            "sample": f"{done} decode step(s) of the chunk's queries (8,064 compressed rows + "
+                      f"129.. raw) through the oracle, scaled to 128 queries"}
 
 
 def cpu_baseline(L, c_len, win_len, win_start, scale, budget_s):
