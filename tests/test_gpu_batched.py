@@ -15,7 +15,7 @@ import oracle
 from khq import ops, synth
 from khqdata import (D, H_KV, H_Q, SCALE, layer_consts, oracle_attn, oracle_window,
                      random_rows_np)
-from test_gpu_parity import close, payload_from_rows, t
+from test_gpu_parity import close, margins, payload_from_rows, t
 
 pytestmark = pytest.mark.gpu
 
@@ -172,7 +172,20 @@ def test_batched_c4_ragged_32(device):
         st = dict(rows=rows, h=h, lc=lc, q_gate=s["q_gate"].cpu().numpy(), c_len=s["c_len"],
                   ring_k=s["ring_k"].cpu().numpy(), ring_v=s["ring_v"].cpu().numpy(),
                   win_start=s["win_start"], win_len=s["win_len"])
-        close(s["out"].cpu().numpy(), _oracle_out(st))
+        want = _oracle_out(st)
+        close(s["out"].cpu().numpy(), want)
+        # the outputs are fp16: beyond the tolerance, the error of every output
+        # of magnitude >= 1e-3 is at most one fp16 unit in the last place of
+        # the float64 result (the two sides round near-ties differently); the
+        # share of the tolerance is reported
+        got16 = s["out"].cpu().numpy()
+        big = np.abs(want) >= 1e-3
+        ulp = np.spacing(np.abs(want[big]).astype(np.float16)).astype(np.float64)
+        ulps = (np.abs(got16.astype(np.float64)[big] - want[big]) / ulp).max()
+        m_abs, m_rel = margins(got16, want)
+        print(f"C4 sequence of {s['c_len']} + {s['win_len']} tokens: max-abs err / 2e-3 = "
+              f"{m_abs:.3f}, rel err / 1e-3 = {m_rel:.3f}, {ulps:.2f} fp16 ulp", flush=True)
+        assert ulps <= 1.0, ulps
 
 
 def test_batched_refuses_graph_capture(device):
