@@ -7,7 +7,9 @@ from the reference's algorithm in float64 so they can check the GPU steps
 (tests/test_gpu_calib.py); each is itself pinned in tests/test_calib_ref.py
 against closed forms (explicit Hadamard matrix, numpy eigh, SVD polar
 factor, Lloyd fixed points, the independent format decoders of
-tests/npref.py, central differences of the SmartVQ loss and of its
+tests/npref.py (the SmartV round trip also against a scalar restatement
+of the reference's encoder loops), synthetic error landscapes with known
+minima for the ops 8 / 9 search, central differences of the SmartVQ loss and of its
 straight-through surrogate, Adam's closed-form first steps).  Nothing in the
 product imports this file.
 """

@@ -331,3 +331,170 @@ def test_svq_train_keeps_the_best_state():
                             iterations=it, n_seeds=2, lr=lr)
         np.testing.assert_array_equal(cb, c["cb"])
         np.testing.assert_array_equal(W, np.eye(256))
+
+
+# ------------------------------------------------- SmartV round trip, pinned
+def _encode_v_loops(proj, cents, vq, alpha):
+    """Row by row, patch by patch, the V encoder of ref .cu:2863-2958 (SmartV
+    codes): exhaustive nearest fp16(vq) * alpha codeword (first minimum),
+    dim-3 centroid by |p3 - fp16(c) alpha| (the first on a strict <), the
+    largest dim-3 residual g, dumps clamp(round(res / max(g, 1e-4) * 7 + 8)),
+    energy ratio sqrt(sum |p|^2 / sum |codeword|^2) over dims 0..2.  Returns
+    per row the 104-byte payload, fp16(ratio) and g."""
+    f16 = lambda v: float(np.float16(v))
+    n = proj.shape[0]
+    vpay = np.zeros((n, 104), np.uint8)
+    rn = np.zeros(n)
+    gmax = np.zeros(n)
+    for r in range(n):
+        codes, d3s, pres = [], [], []
+        te = ve = 0.0
+        for p in range(64):
+            v = proj[r, 4 * p: 4 * p + 4]
+            best, bd = 0, 1e30
+            for k in range(256):
+                c = [f16(vq[p, k, j]) * alpha for j in range(3)]
+                dd = sum((v[j] - c[j]) ** 2 for j in range(3))
+                if dd < bd:
+                    best, bd = k, dd
+            codes.append(best)
+            te += sum(v[j] ** 2 for j in range(3))
+            ve += sum((f16(vq[p, best, j]) * alpha) ** 2 for j in range(3))
+            cv0, cv1 = f16(cents[0, 4 * p + 3]) * alpha, f16(cents[1, 4 * p + 3]) * alpha
+            if abs(v[3] - cv0) < abs(v[3] - cv1):
+                d3s.append(0)
+                pres.append(v[3] - cv0)
+            else:
+                d3s.append(1)
+                pres.append(v[3] - cv1)
+        g = max(abs(x) for x in pres)
+        gmax[r] = g
+        rsc = max(g, 1e-4)
+        dumps = []
+        for x in pres:
+            y = x / rsc * 7.0 + 8.0
+            rv = int(np.floor(y + 0.5)) if y >= 0 else -int(np.floor(-y + 0.5))  # roundf
+            dumps.append(min(max(rv, 0), 15))
+        pv = [(codes[p] & 0x7F) | (d3s[p] << 7) | (dumps[p] << 8) for p in range(64)]
+        words = []
+        for grp in range(8):
+            q = pv[8 * grp: 8 * grp + 8]
+            words += [q[0] | (q[1] << 12) | ((q[2] & 0xFF) << 24),
+                      (q[2] >> 8) | (q[3] << 4) | (q[4] << 16) | ((q[5] & 0xF) << 28),
+                      (q[5] >> 4) | (q[6] << 8) | (q[7] << 20)]
+        words.append(sum(((codes[i] >> 7) & 1) << i for i in range(32)))
+        words.append(sum(((codes[32 + i] >> 7) & 1) << i for i in range(32)))
+        vpay[r] = np.array([w & 0xFFFFFFFF for w in words], np.uint32).view(np.uint8)
+        rn[r] = f16(np.sqrt(te / (ve + 1e-8)))
+    return vpay, rn, gmax
+
+
+def test_roundtrip_v_matches_encoder_loops_and_independent_decoder():
+    """The tournament's V round trip equals an independent encode (a scalar
+    restatement of the reference's loops, packed into the 104-byte format)
+    followed by tests/npref.decode_v, the decoder the hot-path pins use.  The
+    tables are fp16-exact so both sides read the same values; a slip in the
+    V scaling (1/16 vs 1/256, the energy ratio on dim 3, the dump offset)
+    breaks the match."""
+    rng = np.random.default_rng(9)
+    n, alpha = 3, 0.9
+    vq = np.float16(rng.standard_normal((64, 256, 3)) * 0.3).astype(np.float64)
+    cents = np.zeros((4, 256))
+    cents[:2] = np.float16(rng.standard_normal((2, 256)) * 0.3).astype(np.float64)
+    proj = rng.standard_normal((n, 256)) * 0.3
+    # a few dim-3 values exactly halfway between the two centroids (ties go to 1)
+    proj[0, 3] = (np.float16(cents[0, 3]) + np.float16(cents[1, 3])) * alpha / 2
+    norms = np.float16(rng.uniform(0.5, 2.0, n)).astype(np.float64)
+    rp = np.float16(np.stack([np.linalg.qr(rng.standard_normal((4, 4)))[0]
+                              for _ in range(64)]).reshape(64, 16)).astype(np.float64)
+    d = np.float16(np.where(rng.random(256) < 0.5, -1.0, 1.0) * rng.uniform(0.5, 2.0, 256)
+                   ).astype(np.float64)
+    got = R.roundtrip_v(proj, norms, cents, vq, rp, d, alpha)
+    vpay, rn, g = _encode_v_loops(proj, cents, vq, alpha)
+    want = npref.decode_v(vpay, norms.astype(np.float16), rn.astype(np.float16),
+                          g.astype(np.float32).view(np.uint8), cents.astype(np.float16),
+                          rp.astype(np.float16), d.astype(np.float16), vq.astype(np.float16),
+                          alpha)
+    assert np.abs(want).max() > 0.1
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-6 * np.abs(want).max())
+
+
+# ------------------------------------------------ SmartK / SmartV tournament
+def test_tournament_search_and_max_error_rule(monkeypatch):
+    """Ops 8 / 9's search (ref .cu:4688-4790) over a synthetic error landscape
+    whose per-criterion minima are known in closed form.  The K round trip is
+    replaced by x32 minus errors that depend on (alpha, ts): 250 dims carry
+    |(a, m) - F| (they dominate the flat MSE), dim 0 carries 10 min(|(a, m) -
+    M|, 0.05) (the only dim with magnitude weight), dim 1 carries 10 min(|(a,
+    m) - V|, 0.02) (the only dim with variance weight).  F, M and V lie where
+    the 8 x 8 grid and the +-0.03 / +0.04 refinements around each criterion's
+    best reach them exactly, so the best-per-criterion map is {f: F, m: M,
+    v: V}; their max errors are 0.5, |M - F|, 0.5, so the max-error rule picks
+    M (strictly smaller than F's, V's not smaller than M's)."""
+    F, M, V = np.array([0.93, 1.02]), np.array([1.12, 0.87]), np.array([0.84, 0.96])
+    x32 = np.zeros((2, 256))
+    x32[:, 0] = 5.0
+    x32[:, 1] = [1e-3, -1e-3]
+    ts0 = 1.0
+
+    def errors(a, m):
+        pt = np.array([a, m])
+        e = np.zeros(256)
+        e[3:253] = np.linalg.norm(pt - F)
+        e[0] = 10.0 * min(np.linalg.norm(pt - M), 0.05)
+        e[1] = 10.0 * min(np.linalg.norm(pt - V), 0.02)
+        return e
+
+    seen = []
+
+    def fake_roundtrip_k(proj, norms, cents, rp, d, a):
+        m = float(cents[0, 0]) / ts0  # the tournament passes fp16(base * ts), base = 1
+        seen.append((a, m))
+        return x32 - errors(a, m)[None, :]
+
+    monkeypatch.setattr(R, "roundtrip_k", fake_roundtrip_k)
+    x16 = np.ones((2, 256), np.float16)
+    d = np.ones(256)
+    rp = np.tile(np.eye(4).reshape(16), (64, 1))
+    ts, alpha = R.tournament(x32, x16, d, rp, np.full((4, 256), ts0), ts0)
+    assert len(seen) == 4 * 64
+    # closed form: M's (ts, alpha), with the fp16 rounding the tournament's
+    # centroid scaling applies to ts
+    assert abs(alpha - M[0]) < 1e-9
+    assert abs(ts - M[1]) < 1e-9
+    # max errors of the three criterion winners, as the rule compares them
+    me = {k: errors(*p).max() for k, p in (("f", F), ("m", M), ("v", V))}
+    assert me["m"] < me["f"] and not (me["v"] < me["m"])
+
+
+def test_tournament_refinement_reach_and_strict_tie_rule(monkeypatch):
+    """Two more properties of the search: (1) the refinement reaches +0.04
+    from a phase-0 grid point (ts and alpha of the flat-MSE minimum F = (0.99,
+    1.04) sit 0.04 past the best grid point (0.95, 1.00), the points with
+    alpha > 0.995 carrying a penalty on 100 of the flat dims); (2) the
+    max-error rule replaces the winner only on a strictly smaller max error:
+    F's, M's and V's max errors are all 0.5 (capped dims 0 and 1), so F stays."""
+    F, M, V = np.array([0.99, 1.04]), np.array([1.12, 0.87]), np.array([0.84, 0.96])
+    x32 = np.zeros((2, 256))
+    x32[:, 0] = 5.0
+    x32[:, 1] = [1e-3, -1e-3]
+    ts0 = 1.0
+
+    def errors(a, m):
+        pt = np.array([a, m])
+        e = np.zeros(256)
+        e[3:253] = np.linalg.norm(pt - F)
+        if a > 0.995:
+            e[3:103] += 0.1
+        e[0] = 10.0 * min(np.linalg.norm(pt - M), 0.05)
+        e[1] = 10.0 * min(np.linalg.norm(pt - V), 0.05)
+        return e
+
+    monkeypatch.setattr(R, "roundtrip_k", lambda proj, norms, cents, rp, d, a:
+                        x32 - errors(a, float(cents[0, 0]) / ts0)[None, :])
+    x16 = np.ones((2, 256), np.float16)
+    rp = np.tile(np.eye(4).reshape(16), (64, 1))
+    ts, alpha = R.tournament(x32, x16, np.ones(256), rp, np.full((4, 256), ts0), ts0)
+    assert abs(alpha - F[0]) < 1e-9 and abs(ts - F[1]) < 1e-9
+    me = [errors(*p).max() for p in (F, M, V)]
+    assert me[0] == me[1] == me[2] == 0.5
