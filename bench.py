@@ -65,6 +65,10 @@ def parse():
                          "on 4 C3 layers, 3 times; prints no JSON")
     ap.add_argument("--prewarm", type=float, default=0.5,
                     help="seconds of untimed steps before the warmup steps (GPU clock ramp)")
+    ap.add_argument("--graph-batches", type=int, default=0,
+                    help="profiling aid: after the eager timing, replay the captured C3 step "
+                         "in this many batches of 10 (no warm replays) and print each batch's "
+                         "us per layer-step to stderr")
     ap.add_argument("--no-configs", action="store_true",
                     help="default run only: skip the short runs of configs 1, 2, 4 and 5 "
                          "reported under 'configs'")
@@ -244,6 +248,20 @@ def main():
             e0.elapsed_time(e1) * 1000.0 / args.steps, 3)
         del upay
 
+    if args.graph_batches:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        torch.cuda.synchronize()
+        for b in range(args.graph_batches):
+            e0.record(stream)
+            for _ in range(10):
+                g.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            print(f"graph replay batch {b}: {e0.elapsed_time(e1) * 100.0 / args.layers:.2f} "
+                  "us/layer-step", file=sys.stderr, flush=True)
+        del g
     # the same fused step replayed from a HIP graph (launch overhead off the
     # host), checked bit for bit against the eager outputs
     result["graph_layer_step_us"] = round(graph_us(step, args.steps, layers) / args.layers, 3)
