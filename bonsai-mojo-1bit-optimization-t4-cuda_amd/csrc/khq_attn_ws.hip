@@ -59,7 +59,7 @@ namespace ws {
 using namespace mu;
 
 #ifdef KHQ_PHASE_TIMING
-__device__ unsigned long long phase_cycles[24];
+__device__ unsigned long long phase_cycles[32];
 __device__ unsigned long long block_times[1024][2];
 #define PHASE(k)                                                              \
     do {                                                                      \
@@ -73,7 +73,7 @@ __device__ unsigned long long block_times[1024][2];
         __builtin_amdgcn_s_waitcnt(0x0F70);                                   \
         PHASE(k);                                                             \
     } while (0)
-#define PH_PARAMS , unsigned long long ph_t, unsigned (&ph_acc)[24]
+#define PH_PARAMS , unsigned long long ph_t, unsigned (&ph_acc)[32]
 #define PH_ARGS , ph_t, ph_acc
 #else
 #define PHASE(k) do { } while (0)
@@ -317,6 +317,7 @@ __device__ __forceinline__ void key_role(const AttnArgs& a, Smem& S, const Setup
     PHASE(16);
     if (n_tiles > 0) prefetch(s_lo);
     query_transform(in, S, h, 0, lane);
+    PHASE(27);
     store_tables(S, threadIdx.x, tb);
     PHASE(17);
 
@@ -1251,9 +1252,9 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
 #ifdef KHQ_PHASE_TIMING
     unsigned long long ph_t = __builtin_amdgcn_s_memtime();
     const unsigned long long rt0 = __builtin_amdgcn_s_memrealtime();
-    unsigned ph_acc[24];
+    unsigned ph_acc[32];
 #pragma unroll
-    for (int k = 0; k < 24; k++) ph_acc[k] = 0;
+    for (int k = 0; k < 32; k++) ph_acc[k] = 0;
 #endif
 
     // ---- shared tables: the sign and outlier selector tables are computed
@@ -1265,6 +1266,7 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
     {
         load_setup(a, h, wv, lane, in);
         load_tables(a, tid, tb);
+        PHASE(24);
         // key wavefronts: sign tables; value wavefronts: outlier selectors
         // (a wavefront-uniform split)
         const int t = tid & 255;
@@ -1342,6 +1344,7 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
 #pragma unroll
     for (int c = 0; c < 4; c++)  // hardware reciprocal: 1 ulp, far below the output bar
         rdv[c] = 0.0625f * __builtin_amdgcn_rcpf((float)S.dvh[lane * 4 + c] + 1e-8f);
+    PHASE(25);
 #pragma unroll
     for (int hh = 0; hh < 3; hh++) {
         const int hd = 3 * (wv >> 2) + hh;
@@ -1357,6 +1360,7 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
             u[c] = t;
         }
         fwht256(u, lane);
+        PHASE(26);
         const int hq = h * 6 + hd;
         float* out = a.part + ((size_t)hq * a.part_stride + a.part_offset + chunk) * 258;
         const float M = bad ? __builtin_nanf("") : S.ml[h][hd][0];
@@ -1371,7 +1375,7 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
     PHASE(15);
 #ifdef KHQ_PHASE_TIMING
     if ((threadIdx.x & 0xFF) == 0)
-        for (int k = 0; k < 24; k++) atomicAdd(&phase_cycles[k], (unsigned long long)ph_acc[k]);
+        for (int k = 0; k < 32; k++) atomicAdd(&phase_cycles[k], (unsigned long long)ph_acc[k]);
     if (threadIdx.x == 0 && blockIdx.x < 1024) {
         block_times[blockIdx.x][0] = rt0;
         block_times[blockIdx.x][1] = __builtin_amdgcn_s_memrealtime();
@@ -1489,9 +1493,9 @@ hipError_t fault_status(int* out, int clear) {
 #ifdef KHQ_PHASE_TIMING
 extern "C" int khq_ws_phase_cycles(unsigned long long* out, int reset) {
     hipError_t e = hipMemcpyFromSymbol(out, HIP_SYMBOL(khq::ws::phase_cycles),
-                                       sizeof(unsigned long long) * 24);
+                                       sizeof(unsigned long long) * 32);
     if (e == hipSuccess && reset) {
-        unsigned long long z[24] = {0};
+        unsigned long long z[32] = {0};
         e = hipMemcpyToSymbol(HIP_SYMBOL(khq::ws::phase_cycles), z, sizeof(z));
     }
     return e == hipSuccess ? 0 : (int)e;
