@@ -1404,7 +1404,7 @@ static_assert((4 * 6 * 256 + 4 * 6 * 2 + 4 * 6 * 256) * sizeof(float) + 8 * 256 
               "window block LDS: scores, sums, half-sums and V^T staging fit the block's LDS");
 size_t attn_ws_smem_bytes() { return sizeof(ws::Smem); }
 
-int g_spin_limit = 1 << 20;
+std::atomic<int> g_spin_limit{1 << 20};
 
 // Chunking of the compressed region: at most n_cu - 1 chunks (one CU left for
 // the window), each of the same whole number of tiles.  When that leaves no
@@ -1462,7 +1462,7 @@ hipError_t launch_attn_ws(const AttnArgs& a, int tiles_per_chunk, int n_chunks, 
     b.win_blocks = n_chunks + ws::NWIN <= n_cu ? ws::NWIN : 1;
     const int blocks = n_chunks + (a.win_len > 0 ? b.win_blocks : 0);
     fill_rope_table(b);
-    b.spin_limit = g_spin_limit;
+    b.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
     hipLaunchKernelGGL(ws::attn_ws_kernel, dim3(blocks), dim3(ws::NTHR), smem, st, b,
                        tiles_per_chunk, n_chunks);
     return hipGetLastError();

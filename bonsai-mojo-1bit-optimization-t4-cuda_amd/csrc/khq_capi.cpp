@@ -7,6 +7,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -140,10 +141,10 @@ hipError_t scratch_ptr(float** out) {
 
 // 0 = automatic (wavefront-specialised matrix-core kernel for the 24/4/256
 // shape), 1 = portable lane-per-patch kernel for every shape.
-int g_kernel_choice = 0;
+std::atomic<int> g_kernel_choice{0};
 
 bool use_mfma(int n_rep, int h_kv, int L_q) {
-    return g_kernel_choice != 1 && n_rep == 6 && h_kv == 4 && L_q == 1;
+    return g_kernel_choice.load(std::memory_order_relaxed) != 1 && n_rep == 6 && h_kv == 4 && L_q == 1;
 }
 
 // Launches the compressed-region partials of query heads into part
@@ -208,7 +209,7 @@ int khq_attn_parts(int c_len) { return compressed_parts(c_len, 6, 4, 1); }
 
 int khq_select_kernel(int which) {
     if (which < 0 || which > 1) return -100;
-    g_kernel_choice = which;
+    g_kernel_choice.store(which, std::memory_order_relaxed);
     return 0;
 }
 
@@ -219,7 +220,7 @@ int khq_fault_status(int* flags, int clear) {
 
 int khq_set_spin_limit(int sleeps) {
     if (sleeps < 0) return -100;
-    khq::g_spin_limit = sleeps > 0 ? sleeps : (1 << 20);
+    khq::g_spin_limit.store(sleeps > 0 ? sleeps : (1 << 20), std::memory_order_relaxed);
     return 0;
 }
 
@@ -512,7 +513,8 @@ static int attn_step_impl(const void* q_gate, const void* k_payload, const void*
     // finishing launch only merges; otherwise the finishing launch computes
     // the window too.  Longer windows: window partials + combine.
     const bool fused_tail = win_len <= 256 && npc <= 1000;
-    const bool win_in_ws = fused_tail && npc > 0 && win_len > 0 && g_kernel_choice == 0 &&
+    const bool win_in_ws = fused_tail && npc > 0 && win_len > 0 &&
+                           g_kernel_choice.load(std::memory_order_relaxed) == 0 &&
                            use_mfma(n_rep, H_kv, 1);
     const int npw = (win_len > 0 && !fused_tail) ? window_parts(win_len) : (win_in_ws ? 1 : 0);
     const int np = npc + npw;
@@ -707,7 +709,7 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
             return -100;
     }
     const int n_rep = H_q / H_kv;
-    bool batched = g_kernel_choice == 0 && use_mfma(n_rep, H_kv, 1);
+    bool batched = g_kernel_choice.load(std::memory_order_relaxed) == 0 && use_mfma(n_rep, H_kv, 1);
     for (int i = 0; i < n_seq && batched; i++) batched = seqs[i].win_len <= 256;
     if (!batched) {  // one fused step per sequence
         for (int i = 0; i < n_seq; i++) {
@@ -808,7 +810,7 @@ int khq_attn_step_batched_fp16(const khq_seq* seqs, int n_seq, const void* centr
         a.win_blocks = 4;
         a.chunk_tiles = ctiles[i];
         khq::fill_rope_table(a);
-        a.spin_limit = khq::g_spin_limit;
+        a.spin_limit = khq::g_spin_limit.load(std::memory_order_relaxed);
         h_args[i] = a;
         if (np[i] > chunks[i])  // window blocks, one per KV head
             for (int w = 0; w < 4; w++) h_map.push_back(int2{i, chunks[i] + w});

@@ -5,6 +5,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace khq {
 
 // Compressed-region work: token range [0, c_len) of KV head blockIdx.y cut
@@ -127,7 +129,7 @@ int attn_ws_tiles_per_chunk(int c_len, int* n_chunks);
 // hand-off wait gave up), read with a synchronous copy; clear resets it.
 hipError_t fault_status(int* out, int clear);
 // Hand-off wait bound used by the launchers (default 2^20 sleeps).
-extern int g_spin_limit;
+extern std::atomic<int> g_spin_limit;
 size_t attn_ws_smem_bytes();
 // Fills a.rope_tab from a.rope_base (host).
 void fill_rope_table(AttnArgs& a);
