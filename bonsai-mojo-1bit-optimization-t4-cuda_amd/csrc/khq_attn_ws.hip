@@ -1231,10 +1231,19 @@ __device__ __forceinline__ void ws_block(const AttnArgs& a, int chunk, int tiles
     const int h = wv & 3;
     const int lane = tid & 63;
     if (chunk >= n_chunks) {  // the window block(s) after the compressed chunks
+#ifdef KHQ_PHASE_TIMING
+        const unsigned long long wt0 = __builtin_amdgcn_s_memrealtime();
+#endif
         if (a.win_blocks == NWIN)
             window_block(a, S, a.part_offset + n_chunks, chunk - n_chunks);
         else
             window_block_all(a, S, a.part_offset + n_chunks);
+#ifdef KHQ_PHASE_TIMING
+        if (threadIdx.x == 0 && blockIdx.x < 1024) {
+            block_times[blockIdx.x][0] = wt0;
+            block_times[blockIdx.x][1] = __builtin_amdgcn_s_memrealtime();
+        }
+#endif
         return;
     }
     const int c_len = a.c_len;

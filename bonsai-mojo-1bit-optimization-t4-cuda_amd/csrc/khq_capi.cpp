@@ -104,7 +104,7 @@ hipError_t workspace(size_t bytes, hipStream_t stream, float** out, bool use = t
 }
 
 std::mutex g_dev_mu;
-int g_cu_count[kMaxDevices] = {0};
+std::atomic<int> g_cu_count[kMaxDevices] = {};  // 0 until first queried
 struct LdsSet {
     const void* fn;
     int dev, bytes;
@@ -961,14 +961,16 @@ int prefill_attn_run(const __half* q_gate, const __half* k, const __half* vt, in
 }
 
 int device_cu_count() {
-    int dev = 0, v = 0;
+    int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
-    std::lock_guard<std::mutex> lk(g_dev_mu);
-    if (g_cu_count[dev] == 0)
-        g_cu_count[dev] =
-            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0
+    int n = g_cu_count[dev].load(std::memory_order_relaxed);
+    if (n == 0) {  // first query on this device: every caller computes the same value
+        int v = 0;
+        n = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0
                 ? v : 256;
-    return g_cu_count[dev];
+        g_cu_count[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
 }
 
 hipError_t ensure_dynamic_lds(const void* kernel, int bytes) {

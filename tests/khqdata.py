@@ -110,3 +110,23 @@ def random_rows_np(rows, seed):
                 vpay=vpay, vnorm=rng.uniform(0.5, 2.0, rows).astype(np.float16),
                 vrn=rng.uniform(0.8, 1.2, rows).astype(np.float16),
                 vsm=rng.uniform(0.01, 0.05, rows).astype(np.float32).view(np.uint8).reshape(rows, 4))
+
+
+def stressed_rows_np(rows, seed):
+    """random_rows_np with rows the compressor never writes but the format
+    defines: more than 50 code-3 dims (ordinals >= 50 decode with sign -1 and
+    residual 0; up to every dim an outlier) and stored multipliers outside
+    [0.1, 10] (read as 1)."""
+    r = random_rows_np(rows, seed)
+    rng = np.random.default_rng(seed + 1)
+    n_out = rng.choice([0, 49, 50, 51, 64, 128, 200, 256], size=rows)
+    rank = rng.random((rows, D)).argsort(1).argsort(1)
+    codes = rng.integers(0, 3, (rows, D))
+    codes = np.where(rank < n_out[:, None], 3, codes).astype(np.uint64)
+    words = (codes.reshape(rows, 16, 16) << (2 * np.arange(16, dtype=np.uint64))).sum(2)
+    r["kmask"] = words.astype(np.uint32)
+    mraw = rng.choice(np.array([0, 99, 100, 5000, 10000, 10001, 0xFFFFFFFF], dtype=np.uint32),
+                      size=rows)
+    r["kpay"][:, 0:4] = mraw.view(np.uint8).reshape(rows, 4)
+    return r
+

@@ -13,7 +13,8 @@ import oracle
 from khq import ops, synth
 from khq.centroids import synthetic_layer
 from khqdata import (D, H_KV, H_Q, N_REP, SCALE, THETA, layer_consts, oracle_attn,
-                     oracle_window, random_rows_np, two_region_state)
+                     oracle_window, random_rows_np, stressed_rows_np,
+                     two_region_state)
 
 pytestmark = pytest.mark.gpu
 
@@ -205,6 +206,22 @@ def test_attn_random_rows(device, kernel, c_len):
     print(f"c_len {c_len}: max-abs err / 2e-3 = {m_abs:.3f}, rel err / 1e-3 = {m_rel:.3f}",
           flush=True)
     assert m_abs <= 0.5 and m_rel <= 0.5, (m_abs, m_rel)
+
+
+def test_attn_outliers_past_cap_and_mult_range(device, kernel):
+    """Rows with more than 50 outliers and multipliers outside [0.1, 10]
+    (khqdata.stressed_rows_np), over several tiles, both kernels."""
+    c_len = 300
+    lc, h = layer_consts()
+    rows = stressed_rows_np(c_len * H_KV, seed=4242)
+    q = np.random.default_rng(4243).standard_normal((H_Q, 2 * D)).astype(np.float16)
+    st = dict(rows=rows, h=h, lc=lc, q_gate=q, c_len=c_len)
+    pay = payload_from_rows(rows, c_len * H_KV, device)
+    out = torch.zeros((H_Q, D + 2), device=device)
+    ops.attn(t(q), pay, cents_dev(lc, device), out, c_len=c_len, H_q=H_Q, H_kv=H_KV,
+             scale=SCALE)
+    torch.cuda.synchronize()
+    check_triple(out.cpu().numpy(), oracle_attn(st)[1])
 
 
 def test_attn_lq_start_pos(device):

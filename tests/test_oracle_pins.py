@@ -14,7 +14,7 @@ import npref
 import oracle
 from khqdata import (D, H_KV, H_Q, N_REP, SCALE, THETA, compress_rows, layer_consts,
                      oracle_attn, oracle_window, random_rows_np, rope_fp16_rows,
-                     two_region_state)
+                     stressed_rows_np, two_region_state)
 
 
 def cos_sim(a, b):
@@ -181,6 +181,25 @@ def test_attn_oracle_random_rows_long_and_reanchor():
         got, glse = npref.triple_to_out(out)
         np.testing.assert_allclose(got, want, rtol=2e-4, atol=2e-5)
         np.testing.assert_allclose(glse, lse, atol=2e-5)
+
+
+def test_attn_oracle_outliers_past_cap_and_mult_range():
+    # ordinals >= 50 (sign -1, residual 0) and out-of-range multipliers (1):
+    # the oracle's decode against the independent float64 decoder
+    lc, h = layer_consts()
+    rows = stressed_rows_np(120 * H_KV, seed=77)
+    n_out = (((rows["kmask"][:, :, None] >> (2 * np.arange(16, dtype=np.uint32))) & 3) == 3).sum((1, 2))
+    assert (n_out > 50).any() and (n_out == 256).any()
+    rng = np.random.default_rng(78)
+    st = dict(rows=rows, h=h, lc=lc, q_gate=rng.standard_normal((H_Q, 2 * D)).astype(np.float16),
+              c_len=120)
+    K, V, q = _brute_compressed(st, 120)
+    want, lse = npref.attention(q, K, V, SCALE, N_REP)
+    rc, out, _ = oracle_attn(st)
+    assert rc == 0
+    got, glse = npref.triple_to_out(out)
+    np.testing.assert_allclose(got, want, rtol=2e-4, atol=2e-5)
+    np.testing.assert_allclose(glse, lse, atol=2e-5)
 
 
 def test_attn_oracle_start_pos_and_lq():
